@@ -1,0 +1,163 @@
+/*
+ * tgx.h -- C ABI of libtgx.so, the MI355X (gfx950) fused temporal data pipeline.
+ *
+ * Plain C: device pointers, sizes, dtype enums and a HIP stream passed as
+ * `void*` (a hipStream_t; NULL means the legacy default stream).  No torch
+ * types cross this boundary.  Every entry point:
+ *   - launches only on the given stream and never synchronises the device;
+ *   - never allocates or frees device memory: outputs, ring arrays and the
+ *     workspace belong to the caller;
+ *   - keeps no state between calls (safe from any host thread);
+ *   - returns TGX_OK (0) or an error code; the message of the last failure on
+ *     the calling thread is returned by tgx_last_error().
+ *
+ * Reference interfaces replaced (paths relative to the tgengine checkout):
+ *   tgx_ring_append   <- TemporalGraph.advance post-freeze branch
+ *                        tgengine/core/temporal_graph.py:123-129 and
+ *                        _append_overflow :351-387 (pure torch there; no native op)
+ *   tgx_recent        <- TemporalGraph.recent :183-349 (ring merge _merge_overflow
+ *                        :307-349, CSR window :241-305) and the pybind op
+ *                        temporal_recent_k (tgengine/core/csrc/temporal_sample.cu:291-329,
+ *                        bound at :546-555 via tgengine/core/kernels.py:135-154), fused
+ *                        with FixedCosineTimeEncoder (tgengine/nn/time_encoding.py:37-63)
+ *                        and DyGFormer co-occurrence counting
+ *                        (tgengine/models/dygformer.py:71-87)
+ *   tgx_co_occurrence <- pybind op co_occurrence_freq (temporal_sample.cu:514-543,
+ *                        kernels.py:203-221) and the (B,) pair count of
+ *                        DataPipeline._co_occur_from_neighbors
+ *                        (tgengine/pipeline/__init__.py:206-219)
+ */
+#ifndef TGX_H
+#define TGX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TGX_ABI_VERSION 1
+
+/* status codes */
+#define TGX_OK 0
+#define TGX_ERR_ARG 1      /* bad argument (null pointer, negative size, ...) */
+#define TGX_ERR_DTYPE 2    /* unsupported dtype */
+#define TGX_ERR_LIMIT 3    /* size beyond a documented limit */
+#define TGX_ERR_HIP 4      /* a HIP runtime call failed (message has the HIP error) */
+
+/* feature storage dtypes */
+#define TGX_F32 0
+#define TGX_BF16 1
+
+/* dt conventions of the time encoding */
+#define TGX_DT_DYGFORMER 0 /* dt = f32(q) - f32(t) in fp32; padding slots encode to 0 */
+#define TGX_DT_TGN 1       /* dt = f32(q - t) (float64 subtract); padding uses t = 0.0 */
+
+/* co-occurrence modes (pairs = queries 0 and 1 of every plan group) */
+#define TGX_CO_NONE 0
+#define TGX_CO_FREQ 1      /* int32 (P,K,2) counts per sequence + (P,) pair count */
+#define TGX_CO_DYGFORMER 2 /* int32 (P,1+K,2): DyGFormer counts with the node at pos 0 */
+
+/* device-side diagnostics: int32 status[TGX_STATUS_WORDS], accumulated */
+#define TGX_STATUS_WORDS 8
+#define TGX_ST_BAD_EVENT_NODE 0   /* append: src/dst outside [0, num_nodes) (entry skipped) */
+#define TGX_ST_KEY_COLLISION 1    /* append: int(max t)+2 <= 2b-1 (reference key not lexicographic) */
+#define TGX_ST_BAD_QUERY_NODE 2   /* recent: query node >= num_nodes (query returns padding) */
+
+/* Per-node ring of `slots` entries (reference: temporal_graph.py:89-102).
+ * ids int32 [N,B] (-1 empty), times float64 [N,B], feats [N,B,feat_dim] of
+ * feat_dtype, write_pos int64 [N], eids int64 [N,B] (optional, may be NULL). */
+typedef struct tgx_ring {
+  int64_t num_nodes;
+  int32_t slots;
+  int32_t feat_dim;
+  int32_t feat_dtype;
+  int32_t reserved;
+  int32_t* ids;
+  double* times;
+  void* feats;
+  int64_t* write_pos;
+  int64_t* eids;
+} tgx_ring;
+
+/* Frozen CSR (reference: temporal_graph.py:133-181): offsets int64 [N+1],
+ * ids int32 [E], times float64 [E] (ascending within a node), feats [E,feat_dim],
+ * eids int64 [E] (optional). */
+typedef struct tgx_csr {
+  int64_t num_nodes;
+  int64_t num_entries;
+  int32_t feat_dim;
+  int32_t feat_dtype;
+  const int64_t* offsets;
+  const int32_t* ids;
+  const double* times;
+  const void* feats;
+  const int64_t* eids;
+} tgx_csr;
+
+typedef struct tgx_recent_args {
+  /* queries */
+  const int64_t* nodes;    /* [Q] node ids; < 0 = padding query */
+  const double* times;     /* [Q] query times */
+  int64_t num_queries;
+  int32_t k;               /* neighbours per query, 1..TGX_MAX_K */
+  /* work plan: group g handles queries plan[g*group + j], j < group (-1 = none).
+   * NULL plan: group g handles queries g*group .. g*group+group-1. */
+  const int32_t* plan;
+  int32_t group;           /* 1..8 */
+  int64_t num_groups;
+  /* outputs (row = query index); out_feats / out_eids / out_te may be NULL */
+  int32_t* out_ids;        /* [Q,K] */
+  double* out_times;       /* [Q,K] */
+  void* out_feats;         /* [Q,K,feat_dim] in the storage dtype */
+  uint8_t* out_mask;       /* [Q,K] 0/1 */
+  int64_t* out_eids;       /* [Q,K] */
+  /* fused FixedCosineTimeEncoder: out_te[Q,K,d_t] = cos(fl32(dt*w) [+ b]) */
+  int32_t d_t;             /* 0 = off */
+  const float* te_w;       /* [d_t] */
+  const float* te_b;       /* [d_t] or NULL (bias 0) */
+  int32_t dt_mode;         /* TGX_DT_* */
+  float* out_te;
+  /* fused co-occurrence for the (query 0, query 1) pair of every group */
+  int32_t co_mode;         /* TGX_CO_* */
+  int32_t* co_a;           /* FREQ: [P,K,2]; DYGFORMER: [P,1+K,2] */
+  int32_t* co_c;
+  float* co_pair;          /* FREQ only: [P] float count, may be NULL */
+  int32_t* status;         /* [TGX_STATUS_WORDS] or NULL */
+} tgx_recent_args;
+
+#define TGX_MAX_SLOTS 64
+#define TGX_MAX_K 256
+#define TGX_MAX_GROUP 8
+#define TGX_MAX_DT 512
+
+/* Ring update for one batch of b undirected events (kernel a).
+ * Entries are the 2b directed edges in the order [src->dst ..., dst->src ...];
+ * per node the last min(c, B) entries in that order are written to slots
+ * (write_pos + m) % B, m = 0.., and write_pos grows by min(c, B).
+ * feat: [b, feat_dim] in ring->feat_dtype, or NULL for zero features.
+ * eids (if the ring has them) receive eid_base + event index.
+ * workspace: tgx_ring_append_workspace_size(b) bytes of device memory. */
+int tgx_ring_append(const tgx_ring* ring, const int64_t* src, const int64_t* dst,
+                    const double* time, const void* feat, int64_t b, int64_t eid_base,
+                    void* workspace, size_t workspace_bytes, int32_t* status, void* stream);
+size_t tgx_ring_append_workspace_size(int64_t b);
+
+/* Fused most-recent-K gather (+ time encoding, + co-occurrence) (kernels b, c).
+ * ring and/or csr may be NULL (no candidates from that store). */
+int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args* args,
+               void* stream);
+
+/* Stand-alone co-occurrence over neighbour-id rows a, c int32 [P,K] (-1 = pad):
+ * a_cnt/c_cnt int32 [P,K,2] (mode FREQ) and pair_count float [P] (may be NULL). */
+int tgx_co_occurrence(const int32_t* a_ids, const int32_t* c_ids, int64_t pairs, int32_t k,
+                      int32_t* a_cnt, int32_t* c_cnt, float* pair_count, void* stream);
+
+const char* tgx_last_error(void);
+int tgx_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TGX_H */

@@ -1,0 +1,395 @@
+"""TemporalGraph: the drop-in for tgengine/core/temporal_graph.py:31-564 on MI355X.
+
+Same lifecycle and semantics as the reference:
+
+1. Build: ``advance()`` before the first query accumulates events on the host.
+2. Freeze: the first query (or ``freeze_csr()``) sorts them into an immutable
+   CSR on the device (temporal_graph.py:133-181).
+3. Stream: every ``advance()`` after the freeze goes to the per-node ring of
+   ``buffer_size`` slots (allocated lazily, :89-102) through the HIP kernel
+   ``tgx_ring_append`` (reference ``_append_overflow`` :351-387).
+
+``recent`` merges the CSR window with the valid ring slots in one HIP launch
+(``tgx_recent``; reference :183-349).  Every device computation goes through
+libtgx.so on the caller's current stream; there is no CPU fallback and a
+missing library raises.
+
+Extensions (keyword-only, defaults match the reference):
+``feat_dtype`` (torch.float32 or torch.bfloat16 ring storage) and
+``track_edge_ids`` (keep the global event index of every ring/CSR entry).
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+import torch
+from torch import Tensor
+
+from . import _lib
+from .batch import NeighborData
+
+_DTYPES = {torch.float32: _lib.TGX_F32, torch.bfloat16: _lib.TGX_BF16}
+
+
+@dataclass
+class Snapshot:
+    """Ring state for eval restore (reference temporal_graph.py:17-28); the CSR is immutable."""
+
+    overflow_ids: Tensor
+    overflow_times: Tensor
+    overflow_feats: Tensor
+    overflow_write_pos: Tensor
+    num_edges: int
+    overflow_eids: Optional[Tensor] = None
+
+
+def _stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+class TemporalGraph:
+    PADDING_ID: int = -1
+
+    def __init__(self, num_nodes: int, edge_feat_dim: int = 172,
+                 device: str | torch.device = "cuda", overflow_size: int = 64,
+                 buffer_size: Optional[int] = None, use_triton: bool = True, *,
+                 feat_dtype: torch.dtype = torch.float32, track_edge_ids: bool = False):
+        if buffer_size is not None:
+            overflow_size = buffer_size
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise RuntimeError(
+                f"tgengine_amd.TemporalGraph runs on a ROCm GPU (device='cuda'), got {device!r}; "
+                "there is no CPU path")
+        if self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+        _lib.lib()  # raises when libtgx.so is missing
+        if feat_dtype not in _DTYPES:
+            raise TypeError(f"feat_dtype must be torch.float32 or torch.bfloat16, got {feat_dtype}")
+        if not 1 <= int(overflow_size) <= _lib.TGX_MAX_SLOTS:
+            raise ValueError(f"buffer_size must be in [1, {_lib.TGX_MAX_SLOTS}], got {overflow_size}")
+        if not 0 < int(num_nodes) < 2 ** 31:
+            raise ValueError(f"num_nodes must be in [1, 2^31), got {num_nodes}")
+        self._use_triton = use_triton  # accepted for signature compatibility
+        self.num_nodes = int(num_nodes)
+        self.edge_feat_dim = int(edge_feat_dim)
+        self.overflow_size = int(overflow_size)
+        self.feat_dtype = feat_dtype
+        self.track_edge_ids = bool(track_edge_ids)
+        self._num_edges = 0
+
+        self._build: list = []       # pre-freeze (src, dst, time, feat, eid_base) host chunks
+        self._frozen = False
+        self._offsets: Optional[Tensor] = None
+        self._nbr_ids: Optional[Tensor] = None
+        self._nbr_times: Optional[Tensor] = None
+        self._nbr_feats: Optional[Tensor] = None
+        self._nbr_eids: Optional[Tensor] = None
+
+        self._ov_ids: Optional[Tensor] = None
+        self._ov_times: Optional[Tensor] = None
+        self._ov_feats: Optional[Tensor] = None
+        self._ov_write_pos: Optional[Tensor] = None
+        self._ov_eids: Optional[Tensor] = None
+
+        self._status = torch.zeros(_lib.TGX_STATUS_WORDS, dtype=torch.int32, device=self.device)
+        self._ws: Optional[Tensor] = None
+        self._ring_struct: Optional[_lib.TgxRing] = None
+        self._csr_struct: Optional[_lib.TgxCsr] = None
+
+    # ------------------------------------------------------------------ ring
+    def _ensure_overflow(self) -> None:
+        if self._ov_ids is not None:
+            return
+        N, B, d = self.num_nodes, self.overflow_size, self.edge_feat_dim
+        dev = self.device
+        self._ov_ids = torch.full((N, B), self.PADDING_ID, dtype=torch.int32, device=dev)
+        self._ov_times = torch.zeros((N, B), dtype=torch.float64, device=dev)
+        self._ov_feats = torch.zeros((N, B, d), dtype=self.feat_dtype, device=dev)
+        self._ov_write_pos = torch.zeros(N, dtype=torch.int64, device=dev)
+        if self.track_edge_ids:
+            self._ov_eids = torch.full((N, B), -1, dtype=torch.int64, device=dev)
+        self._ring_struct = None
+
+    def _ring(self) -> Optional[_lib.TgxRing]:
+        if self._ov_ids is None:
+            return None
+        if self._ring_struct is None:
+            self._ring_struct = _lib.TgxRing(
+                num_nodes=self.num_nodes, slots=self.overflow_size, feat_dim=self.edge_feat_dim,
+                feat_dtype=_DTYPES[self.feat_dtype], reserved=0,
+                ids=self._ov_ids.data_ptr(), times=self._ov_times.data_ptr(),
+                feats=self._ov_feats.data_ptr(), write_pos=self._ov_write_pos.data_ptr(),
+                eids=_lib.ptr(self._ov_eids))
+        return self._ring_struct
+
+    def _csr(self) -> Optional[_lib.TgxCsr]:
+        if not self._frozen:
+            return None
+        if self._csr_struct is None:
+            self._csr_struct = _lib.TgxCsr(
+                num_nodes=self.num_nodes, num_entries=int(self._nbr_ids.shape[0]),
+                feat_dim=self.edge_feat_dim, feat_dtype=_DTYPES[self.feat_dtype],
+                offsets=self._offsets.data_ptr(), ids=_lib.ptr(self._nbr_ids),
+                times=_lib.ptr(self._nbr_times), feats=_lib.ptr(self._nbr_feats),
+                eids=_lib.ptr(self._nbr_eids))
+        return self._csr_struct
+
+    def _feat_in(self, edge_feat: Optional[Tensor], b: int) -> Optional[Tensor]:
+        if edge_feat is None:
+            return None
+        if edge_feat.dim() != 2 or edge_feat.shape[0] != b or edge_feat.shape[1] != self.edge_feat_dim:
+            raise ValueError(f"edge_feat must be ({b}, {self.edge_feat_dim}), got {tuple(edge_feat.shape)}")
+        if edge_feat.dtype != self.feat_dtype:
+            if self.feat_dtype == torch.bfloat16 and edge_feat.dtype == torch.float32:
+                edge_feat = edge_feat.to(torch.bfloat16)  # round to nearest even
+            else:
+                raise RuntimeError("Index put requires the source and destination dtypes match, "
+                                   f"got {self.feat_dtype} for the ring and {edge_feat.dtype} for edge_feat")
+        return edge_feat.to(self.device).contiguous()
+
+    def _workspace(self, nbytes: int) -> Tensor:
+        if self._ws is None or self._ws.numel() < nbytes:
+            self._ws = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=self.device)
+        return self._ws
+
+    def advance(self, src: Tensor, dst: Tensor, time: Tensor,
+                edge_feat: Optional[Tensor] = None) -> None:
+        """Append a batch of undirected events (reference temporal_graph.py:104-131)."""
+        b = int(src.shape[0])
+        if dst.shape[0] != b or time.shape[0] != b:
+            raise ValueError("src, dst and time must have the same length")
+        if not self._frozen:
+            feat = (torch.zeros((b, self.edge_feat_dim), dtype=self.feat_dtype)
+                    if edge_feat is None else self._feat_in(edge_feat, b).cpu())
+            self._build.append((src.detach().to("cpu", torch.int64), dst.detach().to("cpu", torch.int64),
+                                time.detach().to("cpu", torch.float64), feat, self._num_edges))
+        else:
+            self._ensure_overflow()
+            if b > 0:
+                self._append_ring(src, dst, time, edge_feat, b)
+        self._num_edges += b
+
+    def _append_ring(self, src, dst, time, edge_feat, b: int) -> None:
+        dev = self.device
+        src = src.to(dev, torch.int64).contiguous()
+        dst = dst.to(dev, torch.int64).contiguous()
+        time = time.to(dev, torch.float64).contiguous()
+        feat = self._feat_in(edge_feat, b)
+        L = _lib.lib()
+        need = int(L.tgx_ring_append_workspace_size(b))
+        ws = self._workspace(need)
+        rc = L.tgx_ring_append(ctypes.byref(self._ring()), src.data_ptr(), dst.data_ptr(),
+                               time.data_ptr(), _lib.ptr(feat), b, self._num_edges,
+                               ws.data_ptr(), ws.numel(), self._status.data_ptr(),
+                               _stream_handle(dev))
+        _lib.check(rc, "tgx_ring_append")
+
+    # ------------------------------------------------------------------ CSR
+    def freeze_csr(self) -> None:
+        """Sort the pre-freeze events into the device CSR (reference :133-181).
+
+        Build order per advance() call is [src->dst ..., dst->src ...]; entries
+        are sorted stably by time, then stably by node, so a node's entries are
+        time-ascending with ties in build order.
+        """
+        N, d, dev = self.num_nodes, self.edge_feat_dim, self.device
+        if not self._build:
+            self._offsets = torch.zeros(N + 1, dtype=torch.int64, device=dev)
+            self._nbr_ids = torch.empty(0, dtype=torch.int32, device=dev)
+            self._nbr_times = torch.empty(0, dtype=torch.float64, device=dev)
+            self._nbr_feats = torch.empty((0, d), dtype=self.feat_dtype, device=dev)
+            self._nbr_eids = torch.empty(0, dtype=torch.int64, device=dev) if self.track_edge_ids else None
+        else:
+            frm, to, tt, ff, ee = [], [], [], [], []
+            for (s, t_, tm, f, eb) in self._build:
+                bb = s.shape[0]
+                ev = torch.arange(bb, dtype=torch.int64) + eb
+                frm += [s, t_]
+                to += [t_, s]
+                tt += [tm, tm]
+                ff += [f, f]
+                ee += [ev, ev]
+            frm_t = torch.cat(frm)
+            if frm_t.numel() and (int(frm_t.min()) < 0 or int(frm_t.max()) >= N):
+                raise IndexError("advance() got node ids outside [0, num_nodes)")
+            to_t = torch.cat(to).to(torch.int32)
+            tt_t = torch.cat(tt)
+            ff_t = torch.cat(ff)
+            ee_t = torch.cat(ee)
+            perm = torch.argsort(tt_t, stable=True)
+            perm = perm[torch.argsort(frm_t[perm], stable=True)]
+            counts = torch.bincount(frm_t, minlength=N)
+            offsets = torch.zeros(N + 1, dtype=torch.int64)
+            offsets[1:] = counts.cumsum(0)
+            self._offsets = offsets.to(dev)
+            self._nbr_ids = to_t[perm].to(dev)
+            self._nbr_times = tt_t[perm].to(dev)
+            self._nbr_feats = ff_t[perm].to(dev).contiguous()
+            self._nbr_eids = ee_t[perm].to(dev) if self.track_edge_ids else None
+        self._frozen = True
+        self._build = []
+        self._csr_struct = None
+
+    # ------------------------------------------------------------------ queries
+    def _query(self, nodes: Tensor, times: Tensor, k: int, *, plan: Optional[Tensor] = None,
+               group: int = 1, num_groups: Optional[int] = None, d_t: int = 0,
+               te_w: Optional[Tensor] = None, te_b: Optional[Tensor] = None,
+               dt_mode: int = _lib.TGX_DT_DYGFORMER, co_mode: int = _lib.TGX_CO_NONE,
+               want_eids: bool = False) -> dict:
+        """One tgx_recent launch; returns the output tensors by name."""
+        if not self._frozen:
+            self.freeze_csr()
+        dev = self.device
+        k = int(k)
+        if not 1 <= k <= _lib.TGX_MAX_K:
+            raise ValueError(f"k must be in [1, {_lib.TGX_MAX_K}], got {k}")
+        Q = int(nodes.shape[0])
+        if times.shape[0] != Q:
+            raise ValueError("nodes and times must have the same length")
+        nodes = nodes.to(dev, torch.int64).contiguous()
+        times = times.to(dev, torch.float64).contiguous()
+        out = {
+            "ids": torch.empty((Q, k), dtype=torch.int32, device=dev),
+            "times": torch.empty((Q, k), dtype=torch.float64, device=dev),
+            "feats": torch.empty((Q, k, self.edge_feat_dim), dtype=self.feat_dtype, device=dev),
+            "mask": torch.empty((Q, k), dtype=torch.uint8, device=dev),
+        }
+        if want_eids:
+            out["eids"] = torch.empty((Q, k), dtype=torch.int64, device=dev)
+        if d_t > 0:
+            out["te"] = torch.empty((Q, k, d_t), dtype=torch.float32, device=dev)
+        if num_groups is None:
+            num_groups = (Q + group - 1) // group
+        if co_mode != _lib.TGX_CO_NONE:
+            L = k if co_mode == _lib.TGX_CO_FREQ else k + 1
+            out["co_a"] = torch.empty((num_groups, L, 2), dtype=torch.int32, device=dev)
+            out["co_c"] = torch.empty((num_groups, L, 2), dtype=torch.int32, device=dev)
+            out["co_pair"] = torch.empty((num_groups,), dtype=torch.float32, device=dev)
+        args = _lib.TgxRecentArgs(
+            nodes=nodes.data_ptr() if Q else 0, times=times.data_ptr() if Q else 0, num_queries=Q,
+            k=k, plan=_lib.ptr(plan), group=group, num_groups=num_groups,
+            out_ids=out["ids"].data_ptr(), out_times=out["times"].data_ptr(),
+            out_feats=out["feats"].data_ptr(), out_mask=out["mask"].data_ptr(),
+            out_eids=_lib.ptr(out.get("eids")),
+            d_t=d_t, te_w=_lib.ptr(te_w), te_b=_lib.ptr(te_b), dt_mode=dt_mode,
+            out_te=_lib.ptr(out.get("te")), co_mode=co_mode, co_a=_lib.ptr(out.get("co_a")),
+            co_c=_lib.ptr(out.get("co_c")), co_pair=_lib.ptr(out.get("co_pair")),
+            status=self._status.data_ptr())
+        if Q > 0:
+            ring = self._ring()
+            csr = self._csr()
+            L_ = _lib.lib()
+            rc = L_.tgx_recent(ctypes.byref(ring) if ring is not None else None,
+                               ctypes.byref(csr) if csr is not None else None,
+                               ctypes.byref(args), _stream_handle(dev))
+            _lib.check(rc, "tgx_recent")
+        out["mask"] = out["mask"].view(torch.bool)
+        out["_keep"] = (nodes, times, plan, te_w, te_b)
+        return out
+
+    def recent(self, nodes: Tensor, times: Tensor, k: int) -> NeighborData:
+        """Most recent k neighbours before each query time (reference :183-280)."""
+        o = self._query(nodes, times, k, want_eids=self.track_edge_ids)
+        return NeighborData(neighbor_ids=o["ids"], timestamps=o["times"], edge_feats=o["feats"],
+                            mask=o["mask"], edge_ids=o.get("eids"))
+
+    def recent_2hop(self, nodes: Tensor, times: Tensor, k1: int, k2: int) -> NeighborData:
+        """1-hop and 2-hop neighbours (reference :397-473): the 2-hop query of slot
+        (b, i) is (hop1 id, hop1 time); positions under an invalid hop-1 slot are padding."""
+        hop1 = self.recent(nodes, times, k1)
+        N, K1 = hop1.neighbor_ids.shape
+        hop2 = self.recent(hop1.neighbor_ids.reshape(-1).to(torch.int64),
+                           hop1.timestamps.reshape(-1), k2)
+        h2_mask = hop2.mask.reshape(N, K1, k2) & hop1.mask.unsqueeze(-1)
+        hop1.hop2_mask = h2_mask
+        hop1.hop2_ids = hop2.neighbor_ids.reshape(N, K1, k2).masked_fill(~h2_mask, self.PADDING_ID)
+        hop1.hop2_times = hop2.timestamps.reshape(N, K1, k2).masked_fill(~h2_mask, 0.0)
+        hop1.hop2_feats = hop2.edge_feats.reshape(N, K1, k2, self.edge_feat_dim).masked_fill(
+            ~h2_mask.unsqueeze(-1), 0.0)
+        return hop1
+
+    def co_neighbors(self, src: Tensor, dst: Tensor, times: Tensor, k: int = 32) -> Tensor:
+        """(B,) float32 count of src neighbours that also occur among dst's
+        neighbours (reference :475-498)."""
+        B = int(src.shape[0])
+        if B == 0:
+            return torch.zeros(0, dtype=torch.float32, device=self.device)
+        nodes = torch.cat([src.to(self.device, torch.int64), dst.to(self.device, torch.int64)])
+        qt = torch.cat([times, times]).to(self.device, torch.float64)
+        plan = pair_plan(B, self.device)
+        o = self._query(nodes, qt, k, plan=plan, group=2, num_groups=B,
+                        co_mode=_lib.TGX_CO_FREQ)
+        return o["co_pair"]
+
+    # ------------------------------------------------------------------ state
+    def reset(self) -> None:
+        self._frozen = False
+        self._build = []
+        self._offsets = self._nbr_ids = self._nbr_times = self._nbr_feats = self._nbr_eids = None
+        self._ov_ids = self._ov_times = self._ov_feats = self._ov_write_pos = self._ov_eids = None
+        self._ring_struct = None
+        self._csr_struct = None
+        self._num_edges = 0
+
+    def snapshot(self) -> Snapshot:
+        """Device clone of the ring state (reference :517-526); allocates the ring if absent."""
+        self._ensure_overflow()
+        return Snapshot(self._ov_ids.clone(), self._ov_times.clone(), self._ov_feats.clone(),
+                        self._ov_write_pos.clone(), self._num_edges,
+                        None if self._ov_eids is None else self._ov_eids.clone())
+
+    def restore(self, snap: Snapshot) -> None:
+        self._ov_ids.copy_(snap.overflow_ids)
+        self._ov_times.copy_(snap.overflow_times)
+        self._ov_feats.copy_(snap.overflow_feats)
+        self._ov_write_pos.copy_(snap.overflow_write_pos)
+        if self._ov_eids is not None and snap.overflow_eids is not None:
+            self._ov_eids.copy_(snap.overflow_eids)
+        self._num_edges = snap.num_edges
+
+    @property
+    def num_edges(self) -> int:
+        return self._num_edges
+
+    def status(self) -> dict:
+        """Device diagnostics accumulated by the kernels (synchronises the stream)."""
+        s = self._status.cpu().tolist()
+        return {"bad_event_nodes": s[_lib.TGX_ST_BAD_EVENT_NODE],
+                "key_collisions": s[_lib.TGX_ST_KEY_COLLISION],
+                "bad_query_nodes": s[_lib.TGX_ST_BAD_QUERY_NODE]}
+
+    def clear_status(self) -> None:
+        self._status.zero_()
+
+    @classmethod
+    def from_dataset(cls, src: Tensor, dst: Tensor, time: Tensor, edge_feat: Optional[Tensor],
+                     num_nodes: int, device: str = "cuda", **kwargs) -> "TemporalGraph":
+        """Replay all events, then freeze (reference :540-564)."""
+        d_edge = edge_feat.shape[1] if edge_feat is not None else 172
+        graph = cls(num_nodes, edge_feat_dim=d_edge, device=device, **kwargs)
+        chunk = 10000
+        n = src.shape[0]
+        for s in range(0, n, chunk):
+            e = min(s + chunk, n)
+            graph.advance(src[s:e], dst[s:e], time[s:e],
+                          edge_feat[s:e] if edge_feat is not None else None)
+        graph.freeze_csr()
+        return graph
+
+
+_PLAN_CACHE: dict = {}
+
+
+def pair_plan(B: int, device: torch.device) -> Tensor:
+    """Plan pairing query p with query B+p in group p (int32, device)."""
+    key = ("pair", B, str(device))
+    t = _PLAN_CACHE.get(key)
+    if t is None:
+        a = np.arange(B, dtype=np.int32)
+        t = torch.from_numpy(np.stack([a, a + B], 1).reshape(-1).copy()).to(device)
+        _PLAN_CACHE[key] = t
+    return t

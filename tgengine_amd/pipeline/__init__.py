@@ -1,0 +1,212 @@
+"""DataPipeline: the drop-in for tgengine/pipeline/__init__.py:14-219.
+
+``prepare`` keeps the reference's query grouping (``[src, dst, neg (row-major
+flatten), neg_src]`` with the matching times, :40-70) and output split, but
+runs the whole batch -- gather, feature rows, optional FixedCosineTimeEncoder
+and co-occurrence -- in ONE ``tgx_recent`` launch.  With co-occurrence the
+launch uses an event-major plan: workgroup p holds event p's queries, src
+first and dst second, so the pair meets in one LDS.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import numpy as np
+import torch
+from torch import Tensor
+
+from tgengine_amd.core import _lib
+from tgengine_amd.core.batch import NeighborData, PreparedBatch, RawBatch
+from tgengine_amd.core.gather_spec import GatherSpec
+from tgengine_amd.core.temporal_graph import TemporalGraph
+
+_DT_MODES = {"dygformer": _lib.TGX_DT_DYGFORMER, "tgn": _lib.TGX_DT_TGN}
+_CO_MODES = {"freq": _lib.TGX_CO_FREQ, "dygformer": _lib.TGX_CO_DYGFORMER}
+
+
+def cosine_time_weights(d_t: int) -> np.ndarray:
+    """w = 1/10**linspace(0, 9, d_t) in fp32 (tgengine/nn/time_encoding.py:49)."""
+    return (1.0 / (10 ** np.linspace(0, 9, d_t, dtype=np.float32))).astype(np.float32)
+
+
+def event_plan(b: int, groups: list) -> np.ndarray:
+    """Event-major plan: row p lists event p's query indices in ``groups`` order.
+
+    ``groups`` is [(offset, per_event)] for each query group in the flattened
+    query list; group g of event p owns indices offset + p*per_event + j.
+    """
+    cols = []
+    p = np.arange(b, dtype=np.int64)
+    for off, per in groups:
+        for j in range(per):
+            cols.append(off + p * per + j)
+    return np.stack(cols, 1).astype(np.int32).reshape(-1)
+
+
+class DataPipeline:
+    def __init__(self, spec: GatherSpec, graph: TemporalGraph, time_encoder=None):
+        self.spec = spec
+        self.graph = graph
+        self.time_encoder = time_encoder
+        self._plans: dict = {}
+        self._te: dict = {}
+
+    # -- cached device constants ------------------------------------------
+    def _te_params(self, d_t: int):
+        """(w, b) device tensors; b is None for a zero bias."""
+        enc = self.time_encoder
+        if enc is not None:
+            w = enc.linear.weight.detach().reshape(-1).to(self.graph.device, torch.float32).contiguous()
+            bias = enc.linear.bias
+            b = None
+            if bias is not None and bool(torch.any(bias.detach() != 0)):
+                b = bias.detach().to(self.graph.device, torch.float32).contiguous()
+            if w.numel() != d_t:
+                raise ValueError(f"time encoder has {w.numel()} frequencies, spec asks for {d_t}")
+            return w, b
+        t = self._te.get(d_t)
+        if t is None:
+            t = torch.from_numpy(cosine_time_weights(d_t)).to(self.graph.device)
+            self._te[d_t] = t
+        return t, None
+
+    def _plan(self, key, b: int, groups: list) -> Tensor:
+        t = self._plans.get(key)
+        if t is None:
+            t = torch.from_numpy(event_plan(b, groups)).to(self.graph.device)
+            self._plans[key] = t
+        return t
+
+    # -- prepare -------------------------------------------------------------
+    def prepare(self, raw_batch: RawBatch) -> PreparedBatch:
+        spec = self.spec
+        k, k2 = spec.neighbors.k, spec.neighbors.k2
+        fn = spec.neighbors.for_nodes
+        device = raw_batch.device
+        b = raw_batch.src.shape[0]
+
+        names, node_groups, time_groups, sizes, per_event = [], [], [], [], []
+        if "src" in fn:
+            names.append("src"); node_groups.append(raw_batch.src); time_groups.append(raw_batch.time)
+            sizes.append(b); per_event.append(1)
+        if "dst" in fn:
+            names.append("dst"); node_groups.append(raw_batch.dst); time_groups.append(raw_batch.time)
+            sizes.append(b); per_event.append(1)
+        if "neg" in fn and raw_batch.neg is not None:
+            neg = raw_batch.neg
+            if neg.ndim > 1:
+                node_groups.append(neg.reshape(-1))
+                time_groups.append(raw_batch.time.unsqueeze(1).expand_as(neg).reshape(-1))
+                per_event.append(neg.shape[1])
+            else:
+                node_groups.append(neg)
+                time_groups.append(raw_batch.time)
+                per_event.append(1)
+            names.append("neg"); sizes.append(node_groups[-1].shape[0])
+        if "neg" in fn and raw_batch.neg_src is not None:
+            names.append("neg_src"); node_groups.append(raw_batch.neg_src)
+            time_groups.append(raw_batch.time); sizes.append(b); per_event.append(1)
+
+        all_nodes = torch.cat(node_groups)
+        all_times = torch.cat(time_groups)
+
+        want_co = spec.co_occurrence and "src" in names and "dst" in names
+        co_mode = _CO_MODES[spec.co_occurrence_mode] if want_co else _lib.TGX_CO_NONE
+        d_t = int(spec.time_encoding)
+        te_w = te_b = None
+        if d_t > 0:
+            te_w, te_b = self._te_params(d_t)
+        dt_mode = _DT_MODES[spec.dt_mode]
+
+        if k2 > 0:
+            hop = self.graph.recent_2hop(all_nodes, all_times, k, k2)
+            out = {"ids": hop.neighbor_ids, "times": hop.timestamps, "feats": hop.edge_feats,
+                   "mask": hop.mask, "eids": hop.edge_ids}
+            extra = {"hop2_ids": hop.hop2_ids, "hop2_times": hop.hop2_times,
+                     "hop2_feats": hop.hop2_feats, "hop2_mask": hop.hop2_mask}
+            if d_t > 0 or want_co:
+                o2 = self._fused(all_nodes, all_times, k, b, per_event, names, d_t, te_w, te_b,
+                                 dt_mode, co_mode)
+                out.update({kk: o2[kk] for kk in ("te", "co_a", "co_c", "co_pair") if kk in o2})
+        else:
+            out = self._fused(all_nodes, all_times, k, b, per_event, names, d_t, te_w, te_b,
+                              dt_mode, co_mode)
+            extra = {}
+
+        def split(t):
+            return None if t is None else torch.split_with_sizes(t, sizes, dim=0)
+
+        parts = {kk: split(out.get(kk)) for kk in ("ids", "times", "feats", "mask", "te", "eids")}
+        hparts = {kk: split(v) for kk, v in extra.items()}
+        nbrs = {}
+        for i, name in enumerate(names):
+            nd = NeighborData(parts["ids"][i], parts["times"][i], parts["feats"][i], parts["mask"][i])
+            if parts["te"] is not None:
+                nd.time_enc = parts["te"][i]
+            if parts["eids"] is not None:
+                nd.edge_ids = parts["eids"][i]
+            for kk, v in hparts.items():
+                setattr(nd, kk, v[i])
+            nbrs[name] = nd
+
+        co_occur = co_freq = None
+        if spec.co_occurrence:
+            if want_co:
+                co_occur = out["co_pair"]
+                co_freq = (out["co_a"], out["co_c"])
+            else:
+                co_occur = self.graph.co_neighbors(raw_batch.src, raw_batch.dst, raw_batch.time, k=k)
+
+        return PreparedBatch(
+            src=raw_batch.src, dst=raw_batch.dst,
+            neg=raw_batch.neg if raw_batch.neg is not None else torch.empty(0, device=device),
+            time=raw_batch.time,
+            src_neighbors=nbrs.get("src"), dst_neighbors=nbrs.get("dst"),
+            neg_neighbors=nbrs.get("neg"), neg_src_neighbors=nbrs.get("neg_src"),
+            neg_src=raw_batch.neg_src, co_occurrence=co_occur,
+            node_labels=raw_batch.node_labels, edge_labels=raw_batch.edge_labels,
+            node_feat=raw_batch.node_feat, co_occurrence_freq=co_freq)
+
+    def _fused(self, all_nodes, all_times, k, b, per_event, names, d_t, te_w, te_b, dt_mode,
+               co_mode) -> dict:
+        g = self.graph
+        if co_mode != _lib.TGX_CO_NONE:
+            # event-major groups: event p -> [src p, dst p, its negatives, neg_src p]
+            offs, off = [], 0
+            for per in per_event:
+                offs.append((off, per))
+                off += b * per
+            G = sum(per_event)
+            if G > _lib.TGX_MAX_GROUP:
+                raise ValueError(f"{G} queries per event exceed the fused group limit {_lib.TGX_MAX_GROUP}")
+            plan = self._plan(("ev", b, tuple(per_event)), b, offs)
+            return g._query(all_nodes, all_times, k, plan=plan, group=G, num_groups=b, d_t=d_t,
+                            te_w=te_w, te_b=te_b, dt_mode=dt_mode, co_mode=co_mode,
+                            want_eids=self.spec.edge_ids)
+        return g._query(all_nodes, all_times, k, d_t=d_t, te_w=te_w, te_b=te_b, dt_mode=dt_mode,
+                        want_eids=self.spec.edge_ids)
+
+    @staticmethod
+    def _co_occur_from_neighbors(src_nbrs: NeighborData, dst_nbrs: NeighborData) -> Tensor:
+        """(B,) float shared-neighbour count from already-gathered neighbours
+        (reference pipeline/__init__.py:206-219), computed by tgx_co_occurrence."""
+        a = src_nbrs.neighbor_ids.contiguous()
+        c = dst_nbrs.neighbor_ids.contiguous()
+        P, K = a.shape
+        dev = a.device
+        a_cnt = torch.empty((P, K, 2), dtype=torch.int32, device=dev)
+        c_cnt = torch.empty((P, K, 2), dtype=torch.int32, device=dev)
+        pair = torch.empty((P,), dtype=torch.float32, device=dev)
+        if P and K:
+            rc = _lib.lib().tgx_co_occurrence(a.data_ptr(), c.data_ptr(), P, K, a_cnt.data_ptr(),
+                                              c_cnt.data_ptr(), pair.data_ptr(),
+                                              torch.cuda.current_stream(dev).cuda_stream)
+            _lib.check(rc, "tgx_co_occurrence")
+        else:
+            pair.zero_()
+        return pair
+
+
+from tgengine_amd.pipeline.async_pipeline import AsyncDataPipeline  # noqa: E402
+
+__all__ = ["DataPipeline", "AsyncDataPipeline", "cosine_time_weights", "event_plan"]
