@@ -1,0 +1,263 @@
+"""Benchmark of the fused temporal data pipeline on one MI355X.
+
+A step is one pass of the hot path over one batch of the synthetic stream:
+``DataPipeline.prepare(batch i)`` (fused gather + feature rows + 100-d cosine
+time encoding [+ co-occurrence]) followed by ``TemporalGraph.advance(batch i)``
+(ring update), on a graph created empty -- the BASELINE streaming regime.  The
+whole stream window (W warm-up + K timed batches) is staged in HBM before the
+timed region.
+
+Reported (one JSON line): whole-job prepared queries/s over the timed steps,
+plus the prepare kernel's roofline (algorithmic bytes per launch over the mean
+launch time, from HIP events on the launch stream) and the CPU baseline: the
+torch-CPU restatement of the reference path run on the same ring state for a
+bounded window of following batches (its outputs must equal the GPU's).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_HBM_GBS = 8000.0
+METRIC = "prepared queries/sec (K-nbr gather+time-enc); achieved HBM GB/s % of peak"
+
+
+def bytes_per_batch(cfg, Q: int, V: int, pairs: int, d_t: int = 100) -> int:
+    """Algorithmic bytes of one prepare launch: per query R = 16 + B*12 + V_q*d*s_f,
+    W = K*13 + K*d*s_f + K*d_t*4, plus 16*K per co-occurrence pair."""
+    s_f = cfg.feat_bytes
+    d, K, B = cfg.feat_dim, cfg.k, cfg.buffer_size
+    r = Q * (16 + B * 12) + V * d * s_f
+    w = Q * (K * 13 + K * d * s_f + K * d_t * 4)
+    return int(r + w + pairs * 16 * K)
+
+
+class EventTimer:
+    """HIP events around every tgx_recent launch, recorded on the launching stream."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.pairs = []
+        self.active = False
+
+    def before(self):
+        if self.active:
+            e = self.torch.cuda.Event(enable_timing=True)
+            e.record()
+            self.pairs.append([e, None])
+
+    def after(self):
+        if self.active:
+            e = self.torch.cuda.Event(enable_timing=True)
+            e.record()
+            self.pairs[-1][1] = e
+
+    def total_ms(self):
+        return sum(a.elapsed_time(b) for a, b in self.pairs)
+
+
+def stage_stream(cfg, first: int, count: int, torch, device):
+    from tgengine_amd.synthetic import gen_batch
+    bts = [gen_batch(cfg, i) for i in range(first, first + count)]
+    cat = lambda k: np.concatenate([bt[k] for bt in bts])  # noqa: E731
+    dev = {k: torch.from_numpy(cat(k)).to(device) for k in ("src", "dst", "time", "neg")}
+    feat = torch.from_numpy(cat("feat"))
+    if cfg.feat_dtype == "bf16":
+        feat = feat.view(torch.bfloat16)
+    dev["feat"] = feat.to(device)
+    lens = [len(bt["src"]) for bt in bts]
+    return dev, lens, bts
+
+
+def cpu_baseline(cfg, g, pipe, first, seconds, torch, log, last):
+    """Time the torch-CPU restatement of the reference path on batches first.. of the
+    stream, starting from the GPU ring state; its outputs must equal the GPU's."""
+    from oracle.refpath_torch import RefPathCPU
+    from tgengine_amd import RawBatch
+    from tgengine_amd.synthetic import gen_batch
+    import stream_check
+    cpu = RefPathCPU(cfg.num_nodes, cfg.feat_dim, cfg.buffer_size)
+    cpu.ids.copy_(g._ov_ids.cpu())
+    cpu.times.copy_(g._ov_times.cpu())
+    cpu.feats.copy_(g._ov_feats.float().cpu())
+    cpu.wp.copy_(g._ov_write_pos.cpu())
+    threads = torch.get_num_threads()
+    spent = 0.0
+    queries = 0
+    batches = 0
+    i = first
+    while (spent < seconds or batches < 2) and i < last:
+        bt = gen_batch(cfg, i)
+        rb = stream_check.to_raw(cfg, bt)
+        pb = pipe.prepare(rb)
+        src = torch.from_numpy(bt["src"])
+        dst = torch.from_numpy(bt["dst"])
+        tt = torch.from_numpy(bt["time"])
+        neg = torch.from_numpy(bt["neg"])
+        f32 = torch.from_numpy(bt["feat"])
+        if cfg.feat_dtype == "bf16":
+            f32 = f32.view(torch.bfloat16).float()
+        t0 = time.perf_counter()
+        out = cpu.prepare(src, dst, neg, tt, cfg.k, co=cfg.co_occurrence)
+        cpu.advance(src, dst, tt, f32)
+        spent += time.perf_counter() - t0
+        # parity of the CPU restatement with the GPU on this full-size window
+        groups = [pb.src_neighbors, pb.dst_neighbors, pb.neg_neighbors]
+        gids = torch.cat([x.neighbor_ids.cpu() for x in groups])
+        gmask = torch.cat([x.mask.cpu() for x in groups])
+        gfeat = torch.cat([x.edge_feats.float().cpu() for x in groups])
+        gte = torch.cat([x.time_enc.cpu() for x in groups])
+        if not (torch.equal(gids, out["ids"]) and torch.equal(gmask, out["mask"])
+                and torch.equal(gfeat, out["feats"])):
+            raise RuntimeError(f"CPU baseline and GPU disagree at batch {i}")
+        te_err = float((gte.double() - out["te"].double()).abs().max()) if gte.numel() else 0.0
+        if te_err > 2e-6:
+            raise RuntimeError(f"time encodings differ by {te_err} at batch {i}")
+        g.advance(rb.src, rb.dst, rb.time, rb.edge_feat)
+        queries += len(bt["src"]) * cfg.queries_per_event
+        batches += 1
+        i += 1
+    log(f"cpu baseline: {batches} batches, {queries} queries in {spent:.2f}s on {threads} threads")
+    return {"value": queries / spent, "unit": "prepared queries/s", "cores": threads,
+            "kind": "port",
+            "sample": (f"{cfg.name} batches {first}..{first + batches - 1} ({queries} queries, "
+                       f"prepare+advance) from the GPU ring state after batch {first - 1}; "
+                       f"outputs equal to the GPU's"), "batches": batches}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=600)
+    ap.add_argument("--warmup", type=int, default=1400)
+    ap.add_argument("--config", default="c3")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--quiet", action="store_true")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="after timing, run a plain device copy of this size (PMC byte calibration)")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU only: the fused pipeline path has no multi-GPU mode "
+              f"(asked for --gpus {a.gpus}); see DESIGN.md for how it would shard.", file=sys.stderr)
+        sys.exit(2)
+    log = (lambda *x: None) if a.quiet else (lambda *x: print(*x, file=sys.stderr, flush=True))
+
+    import torch
+    sys.path.insert(0, str(ROOT / "tests"))
+    from tgengine_amd.synthetic import CONFIGS, num_batches
+    import stream_check
+    cfg = CONFIGS[a.config]
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    total = min(a.warmup + a.steps, num_batches(cfg))
+    W = min(a.warmup, total - a.steps) if total > a.steps else 0
+    K = total - W
+    t0 = time.time()
+    dev, lens, bts = stage_stream(cfg, 0, total, torch, device)
+    log(f"{cfg.name}: staged {total} batches ({sum(lens)} events) in {time.time() - t0:.1f}s")
+    for bt in bts:
+        from tgengine_amd.synthetic import key_multiplier_ok
+        assert key_multiplier_ok(bt["time"], len(bt["src"]))
+    del bts
+
+    g = stream_check.make_graph(cfg)
+    pipe = stream_check.make_pipeline(cfg, g)
+    from tgengine_amd import RawBatch
+    offs = np.concatenate([[0], np.cumsum(lens)])
+    n_neg = cfg.n_neg
+
+    def raw(i):
+        s, e = int(offs[i]), int(offs[i + 1])
+        neg = dev["neg"][s:e] if n_neg == 1 else dev["neg"][s:e]
+        return RawBatch(src=dev["src"][s:e], dst=dev["dst"][s:e], time=dev["time"][s:e],
+                        edge_feat=dev["feat"][s:e], neg=neg)
+
+    raws = [raw(i) for i in range(total)]
+    timer = EventTimer(torch)
+    g.kernel_timer = timer
+    for i in range(W):
+        pipe.prepare(raws[i])
+        g.advance(raws[i].src, raws[i].dst, raws[i].time, raws[i].edge_feat)
+    torch.cuda.synchronize()
+    log(f"warm-up {W} batches done")
+
+    masks = []
+    timer.active = True
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for i in range(W, total):
+        pb = pipe.prepare(raws[i])
+        masks.append((pb.src_neighbors.mask, pb.dst_neighbors.mask, pb.neg_neighbors.mask))
+        g.advance(raws[i].src, raws[i].dst, raws[i].time, raws[i].edge_feat)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    timer.active = False
+    kern_ms = timer.total_ms()
+    n_launch = len(timer.pairs)
+    st = g.status()
+    if any(st.values()):
+        raise RuntimeError(f"device diagnostics: {st}")
+
+    Qs = [int(sum(m.shape[0] for m in ms)) for ms in masks]
+    Vs = [int(sum(int(m.sum()) for m in ms)) for ms in masks]
+    pairs = [lens[W + j] if cfg.co_occurrence else 0 for j in range(K)]
+    byts = [bytes_per_batch(cfg, Qs[j], Vs[j], pairs[j]) for j in range(K)]
+    total_q = sum(Qs)
+    value = total_q / wall
+    avg_launch_s = kern_ms / 1e3 / n_launch
+    achieved = sum(byts) / n_launch / avg_launch_s / 1e9
+    log(f"timed {K} steps: wall {wall * 1e3:.1f} ms, prepare kernel {kern_ms:.2f} ms "
+        f"({avg_launch_s * 1e6:.1f} us/launch), {achieved:.0f} GB/s, mean V/query "
+        f"{sum(Vs) / total_q:.2f}")
+
+    if a.copy_calibration_mib > 0:
+        n = a.copy_calibration_mib << 20
+        src_buf = torch.ones(n // 4, dtype=torch.float32, device=device)
+        dst_buf = torch.empty_like(src_buf)
+        for _ in range(3):
+            dst_buf.copy_(src_buf)
+        torch.cuda.synchronize()
+        del src_buf, dst_buf
+
+    traffic = None
+    pmc = ROOT / "profiles" / f"{cfg.name}_recent_fused_pmc.json"
+    if pmc.exists():
+        traffic = json.loads(pmc.read_text()).get("traffic_bytes_per_launch")
+
+    cpu = None
+    if not a.no_cpu and total < num_batches(cfg):
+        cpu = cpu_baseline(cfg, g, pipe, total, a.cpu_seconds, torch, log, num_batches(cfg))
+
+    line = {
+        "metric": METRIC, "value": value, "unit": "prepared queries/s", "n_gpus": 1,
+        "steps": K, "warmup": W, "ms_per_step": wall * 1e3 / K, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int64/f64 ids+times, "
+        + ("bf16" if cfg.feat_dtype == "bf16" else "f32") + " rows, f32 time-enc",
+        "data": "synthetic",
+        "config": {"workload": f"{cfg.name}: {cfg.num_nodes} nodes, batch {cfg.batch}, "
+                               f"K={cfg.k}, B={cfg.buffer_size}, d={cfg.feat_dim} {cfg.feat_dtype}, "
+                               f"{cfg.queries_per_event} queries/event, d_t=100"
+                               + (", co-occurrence" if cfg.co_occurrence else ""),
+                   "batches_timed": f"{W}..{total - 1}", "events_per_batch": cfg.batch},
+        "prepare_kernel": {"queries_per_s": total_q / (kern_ms / 1e3), "us_per_launch":
+                           avg_launch_s * 1e6, "mean_valid_per_query": sum(Vs) / total_q,
+                           "bytes_per_launch": sum(byts) / n_launch},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": traffic},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

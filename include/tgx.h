@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define TGX_ABI_VERSION 1
+#define TGX_ABI_VERSION 2
 
 /* status codes */
 #define TGX_OK 0
@@ -96,8 +96,22 @@ typedef struct tgx_csr {
   const int64_t* eids;
 } tgx_csr;
 
+/* One group of queries read in place: query l of the group is node nodes[l]
+ * at time times[l / times_per] (times_per = negatives per event for a (b, n)
+ * row-major negative block, else 1). */
+typedef struct tgx_query_group {
+  const int64_t* nodes;
+  const double* times;
+  int64_t count;
+  int32_t times_per;
+  int32_t reserved;
+} tgx_query_group;
+
+#define TGX_MAX_QUERY_GROUPS 4
+
 typedef struct tgx_recent_args {
-  /* queries */
+  /* queries: either nodes/times, or num_query_groups > 0 groups concatenated
+   * in order (query index = group offset + position in the group) */
   const int64_t* nodes;    /* [Q] node ids; < 0 = padding query */
   const double* times;     /* [Q] query times */
   int64_t num_queries;
@@ -125,6 +139,8 @@ typedef struct tgx_recent_args {
   int32_t* co_c;
   float* co_pair;          /* FREQ only: [P] float count, may be NULL */
   int32_t* status;         /* [TGX_STATUS_WORDS] or NULL */
+  int32_t num_query_groups;                          /* 0 = use nodes/times */
+  tgx_query_group query_groups[TGX_MAX_QUERY_GROUPS];
 } tgx_recent_args;
 
 #define TGX_MAX_SLOTS 64

@@ -44,6 +44,14 @@ class TgxCsr(ctypes.Structure):
                 ("feats", c_vp), ("eids", c_vp)]
 
 
+TGX_MAX_QUERY_GROUPS = 4
+
+
+class TgxQueryGroup(ctypes.Structure):
+    _fields_ = [("nodes", c_vp), ("times", c_vp), ("count", c_i64), ("times_per", c_i32),
+                ("reserved", c_i32)]
+
+
 class TgxRecentArgs(ctypes.Structure):
     _fields_ = [("nodes", c_vp), ("times", c_vp), ("num_queries", c_i64), ("k", c_i32),
                 ("plan", c_vp), ("group", c_i32), ("num_groups", c_i64),
@@ -51,7 +59,8 @@ class TgxRecentArgs(ctypes.Structure):
                 ("out_eids", c_vp),
                 ("d_t", c_i32), ("te_w", c_vp), ("te_b", c_vp), ("dt_mode", c_i32), ("out_te", c_vp),
                 ("co_mode", c_i32), ("co_a", c_vp), ("co_c", c_vp), ("co_pair", c_vp),
-                ("status", c_vp)]
+                ("status", c_vp), ("num_query_groups", c_i32),
+                ("query_groups", TgxQueryGroup * TGX_MAX_QUERY_GROUPS)]
 
 
 # every symbol include/tgx.h declares, with its ctypes signature
@@ -91,7 +100,7 @@ def lib() -> ctypes.CDLL:
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
-        if handle.tgx_abi_version() != 1:
+        if handle.tgx_abi_version() != 2:
             raise RuntimeError("libtgx ABI version mismatch")
         _lib = handle
         return _lib

@@ -99,6 +99,9 @@ class TemporalGraph:
         self._ws: Optional[Tensor] = None
         self._ring_struct: Optional[_lib.TgxRing] = None
         self._csr_struct: Optional[_lib.TgxCsr] = None
+        # optional object with before()/after(), called around each tgx_recent launch
+        # on the launching thread (used to bracket the kernel with HIP events)
+        self.kernel_timer = None
 
     # ------------------------------------------------------------------ ring
     def _ensure_overflow(self) -> None:
@@ -235,23 +238,41 @@ class TemporalGraph:
         self._csr_struct = None
 
     # ------------------------------------------------------------------ queries
-    def _query(self, nodes: Tensor, times: Tensor, k: int, *, plan: Optional[Tensor] = None,
+    def _query(self, nodes: Optional[Tensor], times: Optional[Tensor], k: int, *,
+               groups: Optional[list] = None, plan: Optional[Tensor] = None,
                group: int = 1, num_groups: Optional[int] = None, d_t: int = 0,
                te_w: Optional[Tensor] = None, te_b: Optional[Tensor] = None,
                dt_mode: int = _lib.TGX_DT_DYGFORMER, co_mode: int = _lib.TGX_CO_NONE,
                want_eids: bool = False) -> dict:
-        """One tgx_recent launch; returns the output tensors by name."""
+        """One tgx_recent launch; returns the output tensors by name.
+
+        Queries come either as ``nodes``/``times`` or as ``groups``: a list of
+        (nodes, times, times_per) read in place and concatenated in order.
+        """
         if not self._frozen:
             self.freeze_csr()
         dev = self.device
         k = int(k)
         if not 1 <= k <= _lib.TGX_MAX_K:
             raise ValueError(f"k must be in [1, {_lib.TGX_MAX_K}], got {k}")
-        Q = int(nodes.shape[0])
-        if times.shape[0] != Q:
-            raise ValueError("nodes and times must have the same length")
-        nodes = nodes.to(dev, torch.int64).contiguous()
-        times = times.to(dev, torch.float64).contiguous()
+        qgroups = []
+        if groups is not None:
+            if len(groups) > _lib.TGX_MAX_QUERY_GROUPS:
+                raise ValueError(f"at most {_lib.TGX_MAX_QUERY_GROUPS} query groups")
+            Q = 0
+            for (gn, gt, per) in groups:
+                gn = gn.reshape(-1).to(dev, torch.int64).contiguous()
+                gt = gt.reshape(-1).to(dev, torch.float64).contiguous()
+                if gn.shape[0] != gt.shape[0] * per:
+                    raise ValueError("query group node/time sizes do not match")
+                qgroups.append((gn, gt, per))
+                Q += int(gn.shape[0])
+        else:
+            Q = int(nodes.shape[0])
+            if times.shape[0] != Q:
+                raise ValueError("nodes and times must have the same length")
+            nodes = nodes.to(dev, torch.int64).contiguous()
+            times = times.to(dev, torch.float64).contiguous()
         out = {
             "ids": torch.empty((Q, k), dtype=torch.int32, device=dev),
             "times": torch.empty((Q, k), dtype=torch.float64, device=dev),
@@ -270,7 +291,8 @@ class TemporalGraph:
             out["co_c"] = torch.empty((num_groups, L, 2), dtype=torch.int32, device=dev)
             out["co_pair"] = torch.empty((num_groups,), dtype=torch.float32, device=dev)
         args = _lib.TgxRecentArgs(
-            nodes=nodes.data_ptr() if Q else 0, times=times.data_ptr() if Q else 0, num_queries=Q,
+            nodes=nodes.data_ptr() if (Q and not qgroups) else 0,
+            times=times.data_ptr() if (Q and not qgroups) else 0, num_queries=Q,
             k=k, plan=_lib.ptr(plan), group=group, num_groups=num_groups,
             out_ids=out["ids"].data_ptr(), out_times=out["times"].data_ptr(),
             out_feats=out["feats"].data_ptr(), out_mask=out["mask"].data_ptr(),
@@ -278,17 +300,24 @@ class TemporalGraph:
             d_t=d_t, te_w=_lib.ptr(te_w), te_b=_lib.ptr(te_b), dt_mode=dt_mode,
             out_te=_lib.ptr(out.get("te")), co_mode=co_mode, co_a=_lib.ptr(out.get("co_a")),
             co_c=_lib.ptr(out.get("co_c")), co_pair=_lib.ptr(out.get("co_pair")),
-            status=self._status.data_ptr())
+            status=self._status.data_ptr(), num_query_groups=len(qgroups))
+        for i, (gn, gt, per) in enumerate(qgroups):
+            qg = args.query_groups[i]
+            qg.nodes, qg.times, qg.count, qg.times_per = gn.data_ptr(), gt.data_ptr(), gn.shape[0], per
         if Q > 0:
             ring = self._ring()
             csr = self._csr()
             L_ = _lib.lib()
+            timer = self.kernel_timer
+            if timer is not None:
+                timer.before()
             rc = L_.tgx_recent(ctypes.byref(ring) if ring is not None else None,
                                ctypes.byref(csr) if csr is not None else None,
                                ctypes.byref(args), _stream_handle(dev))
+            if timer is not None:
+                timer.after()
             _lib.check(rc, "tgx_recent")
         out["mask"] = out["mask"].view(torch.bool)
-        out["_keep"] = (nodes, times, plan, te_w, te_b)
         return out
 
     def recent(self, nodes: Tensor, times: Tensor, k: int) -> NeighborData:

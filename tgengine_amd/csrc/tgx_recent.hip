@@ -24,50 +24,13 @@
 // (float4 stores, cosine evaluated in float64 from the exact fp32 argument).
 // A workgroup holds `group` queries so a (src, dst) pair meets in one LDS.
 #include "tgx_internal.h"
+#include "tgx_cos.h"
 
 namespace tgx {
 namespace {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-// cos(x) for an fp32 argument, evaluated in float64.
-// Reduction x = k*pi + r, |r| <= pi/2 (Cody-Waite with a two-term pi), then
-// the Taylor series of cos(r) through r^18 (truncation < 2e-16 on |r| <= pi/2)
-// and cos(x) = (-1)^k cos(r).  Arguments beyond 1e9 use the ocml double cos.
-constexpr double kInvPi = 0.3183098861837907;
-constexpr double kPiHi = 3.141592653589793;
-constexpr double kPiLo = 1.2246467991473532e-16;
-constexpr double kC1 = -0.5;
-constexpr double kC2 = 0.041666666666666664;
-constexpr double kC3 = -0.001388888888888889;
-constexpr double kC4 = 2.48015873015873e-05;
-constexpr double kC5 = -2.755731922398589e-07;
-constexpr double kC6 = 2.08767569878681e-09;
-constexpr double kC7 = -1.1470745597729725e-11;
-constexpr double kC8 = 4.779477332387385e-14;
-constexpr double kC9 = -1.5619206968586225e-16;
-
-__device__ __forceinline__ float cos_f32arg(float x) {
-  const double xd = static_cast<double>(x);
-  if (!(fabs(xd) <= 1.0e9)) return static_cast<float>(cos(xd));
-  const double k = rint(xd * kInvPi);
-  double r = fma(-k, kPiHi, xd);
-  r = fma(-k, kPiLo, r);
-  const double z = r * r;
-  double p = kC9;
-  p = fma(p, z, kC8);
-  p = fma(p, z, kC7);
-  p = fma(p, z, kC6);
-  p = fma(p, z, kC5);
-  p = fma(p, z, kC4);
-  p = fma(p, z, kC3);
-  p = fma(p, z, kC2);
-  p = fma(p, z, kC1);
-  p = fma(p, z, 1.0);
-  const int ki = static_cast<int>(k);
-  return static_cast<float>((ki & 1) ? -p : p);
-}
 
 struct Params {
   // ring
@@ -87,6 +50,11 @@ struct Params {
   // queries
   const int64_t* nodes;
   const double* qtimes;
+  int ngroups;
+  const int64_t* gn[TGX_MAX_QUERY_GROUPS];
+  const double* gt[TGX_MAX_QUERY_GROUPS];
+  int64_t goff[TGX_MAX_QUERY_GROUPS + 1];
+  int gdiv[TGX_MAX_QUERY_GROUPS];
   int64_t Q;
   int K;
   const int32_t* plan;
@@ -158,6 +126,26 @@ __device__ __forceinline__ int64_t query_of(const Params& P, int64_t g, int j) {
   return (q >= 0 && q < P.Q) ? q : -1;
 }
 
+__device__ __forceinline__ void query_load(const Params& P, int64_t q, int64_t& node, double& qt) {
+  if (P.ngroups == 0) {
+    node = P.nodes[q];
+    qt = P.qtimes[q];
+    return;
+  }
+  int g = 0;
+  while (g + 1 < P.ngroups && q >= P.goff[g + 1]) ++g;
+  const int64_t l = q - P.goff[g];
+  node = P.gn[g][l];
+  qt = P.gt[g][P.gdiv[g] == 1 ? l : static_cast<int64_t>(static_cast<uint32_t>(l) / static_cast<uint32_t>(P.gdiv[g]))];
+}
+
+__device__ __forceinline__ int64_t query_node(const Params& P, int64_t q) {
+  int64_t node;
+  double qt;
+  query_load(P, q, node, qt);
+  return node;
+}
+
 template <int VEC>
 __global__ __launch_bounds__(512) void recent_fused(Params P) {
   using VT = typename Vec<VEC>::T;
@@ -187,10 +175,7 @@ __global__ __launch_bounds__(512) void recent_fused(Params P) {
   const bool active = q >= 0;
   int64_t node = -1;
   double qt = 0.0;
-  if (active) {
-    node = P.nodes[q];
-    qt = P.qtimes[q];
-  }
+  if (active) query_load(P, q, node, qt);
   const bool bad = active && node >= P.N;
   if (bad && lane == 0 && P.status != nullptr) atomicAdd(&P.status[TGX_ST_BAD_QUERY_NODE], 1);
   const int64_t ur = node < 0 ? 0 : node;
@@ -338,18 +323,29 @@ __global__ __launch_bounds__(512) void recent_fused(Params P) {
         const int total = K * nq;
         const int sp = kWave / nq, sc = kWave % nq;
         int p = lane / nq, c = lane % nq;
+        const f32x4* w4 = reinterpret_cast<const f32x4*>(s_w);
+        const f32x4* b4 = reinterpret_cast<const f32x4*>(s_b);
+        f32x4* out4 = reinterpret_cast<f32x4*>(tbase);
         for (int idx = lane; idx < total; idx += kWave) {
           f32x4 o = {0.f, 0.f, 0.f, 0.f};
           if (!dyg || pcode[p] >= 0) {
             const float dt = pdt[p];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              float a = dt * s_w[4 * c + j];
-              if (has_b) a = a + s_b[4 * c + j];
-              o[j] = cos_f32arg(a);
+            f32x4 a = dt * w4[c];
+            if (has_b) a = a + b4[c];
+            const float amax = fmaxf(fmaxf(fabsf(a[0]), fabsf(a[1])), fmaxf(fabsf(a[2]), fabsf(a[3])));
+            if (__builtin_expect(amax < kBigArg, 1)) {
+              o[0] = cos_fast(a[0]);
+              o[1] = cos_fast(a[1]);
+              o[2] = cos_fast(a[2]);
+              o[3] = cos_fast(a[3]);
+            } else {
+              o[0] = cos_slow(a[0]);
+              o[1] = cos_slow(a[1]);
+              o[2] = cos_slow(a[2]);
+              o[3] = cos_slow(a[3]);
             }
           }
-          __builtin_nontemporal_store(o, reinterpret_cast<f32x4*>(tbase + static_cast<int64_t>(p) * P.d_t) + c);
+          __builtin_nontemporal_store(o, out4 + idx);
           c += sc;
           p += sp;
           if (c >= nq) {
@@ -365,7 +361,7 @@ __global__ __launch_bounds__(512) void recent_fused(Params P) {
           if (!dyg || pcode[p] >= 0) {
             float a = pdt[p] * s_w[j];
             if (has_b) a = a + s_b[j];
-            o = cos_f32arg(a);
+            o = fabsf(a) < kBigArg ? cos_fast(a) : cos_slow(a);
           }
           tbase[static_cast<int64_t>(p) * P.d_t + j] = o;
         }
@@ -405,8 +401,8 @@ __global__ __launch_bounds__(512) void recent_fused(Params P) {
         if (wv == 0 && lane == 0 && P.co_pair != nullptr) P.co_pair[g] = static_cast<float>(pc);
       } else {
         // DyGFormer counts on A' = [node_a] ++ A, C' = [node_c] ++ C (length K+1)
-        const int32_t na0 = static_cast<int32_t>(P.nodes[qa]);
-        const int32_t nc0 = static_cast<int32_t>(P.nodes[qc]);
+        const int32_t na0 = static_cast<int32_t>(query_node(P, qa));
+        const int32_t nc0 = static_cast<int32_t>(query_node(P, qc));
         const int L = K + 1;
         int32_t* out = wv == 0 ? P.co_a : P.co_c;
         for (int i = lane; i < L; i += kWave) {
@@ -504,8 +500,11 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
   if (a->num_groups >= (int64_t(1) << 31))
     return fail(TGX_ERR_LIMIT, "tgx_recent: too many groups");
   if (a->num_queries == 0 || a->num_groups == 0) return TGX_OK;
-  if (a->nodes == nullptr || a->times == nullptr || a->out_ids == nullptr ||
-      a->out_times == nullptr || a->out_mask == nullptr)
+  if (a->num_query_groups < 0 || a->num_query_groups > TGX_MAX_QUERY_GROUPS)
+    return fail(TGX_ERR_LIMIT, "tgx_recent: %d query groups outside [0, %d]", a->num_query_groups,
+                TGX_MAX_QUERY_GROUPS);
+  if ((a->num_query_groups == 0 && (a->nodes == nullptr || a->times == nullptr)) ||
+      a->out_ids == nullptr || a->out_times == nullptr || a->out_mask == nullptr)
     return fail(TGX_ERR_ARG, "tgx_recent: nodes/times/out_ids/out_times/out_mask must not be NULL");
   if (a->plan == nullptr && a->num_groups * a->group < a->num_queries)
     return fail(TGX_ERR_ARG, "tgx_recent: num_groups*group < num_queries without a plan");
@@ -558,6 +557,24 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
   }
   P.nodes = a->nodes;
   P.qtimes = a->times;
+  P.ngroups = a->num_query_groups;
+  {
+    int64_t off = 0;
+    for (int g = 0; g < a->num_query_groups; ++g) {
+      const tgx_query_group& qg = a->query_groups[g];
+      if (qg.count < 0 || qg.times_per < 1 || (qg.count > 0 && (qg.nodes == nullptr || qg.times == nullptr)))
+        return fail(TGX_ERR_ARG, "tgx_recent: bad query group %d", g);
+      P.gn[g] = qg.nodes;
+      P.gt[g] = qg.times;
+      P.gdiv[g] = qg.times_per;
+      P.goff[g] = off;
+      off += qg.count;
+    }
+    P.goff[a->num_query_groups] = off;
+    if (a->num_query_groups > 0 && off != a->num_queries)
+      return fail(TGX_ERR_ARG, "tgx_recent: query groups hold %lld queries, num_queries is %lld",
+                  (long long)off, (long long)a->num_queries);
+  }
   P.Q = a->num_queries;
   P.K = a->k;
   P.plan = a->plan;

@@ -30,6 +30,18 @@ constexpr int kPlanThreads = 512;
 constexpr int kPlanWaves = kPlanThreads / kWave;
 constexpr int kLdsMaxEntries = 16384;
 
+__device__ __forceinline__ int pad32(int p) { return p + (p >> 5); }
+
+// (write_pos + off) % B for write_pos >= 0, 0 <= off < B; 32-bit arithmetic
+// whenever the value fits (B is usually a power of two)
+__device__ __forceinline__ int64_t ring_slot(int64_t w, int off, int B) {
+  const uint64_t x = static_cast<uint64_t>(w) + static_cast<uint64_t>(off);
+  if ((B & (B - 1)) == 0) return static_cast<int64_t>(x & static_cast<uint64_t>(B - 1));
+  if (x < (uint64_t(1) << 32)) return static_cast<int64_t>(static_cast<uint32_t>(x) % static_cast<uint32_t>(B));
+  return static_cast<int64_t>(x % static_cast<uint64_t>(B));
+}
+
+
 // ---------------------------------------------------------------------------
 // digit counters, one column per thread.
 //   packed: word (d>>1)*T + t holds the 16-bit counters of digits 2j, 2j+1
@@ -263,7 +275,7 @@ __device__ __forceinline__ void plan_body(const int64_t* __restrict__ src,
     int64_t dslot = -1;
     if (u < static_cast<uint32_t>(N) && m >= c - kept) {
       const int64_t w0 = wp[u];
-      const int64_t slot = (w0 + (m - (c - kept))) % B;
+      const int64_t slot = ring_slot(w0, m - (c - kept), B);
       dslot = static_cast<int64_t>(u) * B + slot;
     }
     dest[idx] = dslot;
@@ -281,19 +293,254 @@ __device__ __forceinline__ void plan_body(const int64_t* __restrict__ src,
   }
 }
 
-__global__ __launch_bounds__(kPlanThreads) void ring_plan_lds(
+// ---------------------------------------------------------------------------
+// Fast plan for n <= 16384 entries: one workgroup of 1024 threads, each
+// owning 16 consecutive positions of the array in registers ("blocked"
+// arrangement).  Per 4-bit pass: digits and in-thread ranks in registers
+// (8-bit counters packed in two u64), one block-wide scan of the 16 digit
+// counts (16-bit fields packed in four u64), a scatter of (key, index) into
+// LDS and a gather back into registers.  Only the exchange arrays and the
+// per-thread digit offsets live in LDS (64 + 32 + 32 KB).
+// ---------------------------------------------------------------------------
+constexpr int kFT = 512;              // threads
+constexpr int kFW = kFT / kWave;      // waves
+constexpr int kFE = 32;               // items per thread
+
+__device__ __forceinline__ uint64_t shfl_up_u64(uint64_t x, int off) {
+  const uint32_t lo = __shfl_up(static_cast<uint32_t>(x), off, kWave);
+  const uint32_t hi = __shfl_up(static_cast<uint32_t>(x >> 32), off, kWave);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+template <int NW>
+__device__ __forceinline__ int block_excl_max_n(int v, int* sh, int t) {
+  const int lane = t & (kWave - 1), wv = t / kWave;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int y = __shfl_up(x, off, kWave);
+    if (lane >= off) x = max(x, y);
+  }
+  if (lane == kWave - 1) sh[wv] = x;
+  __syncthreads();
+  int carry = -1;
+  for (int w2 = 0; w2 < wv; ++w2) carry = max(carry, sh[w2]);
+  int ex = __shfl_up(x, 1, kWave);
+  if (lane == 0) ex = -1;
+  __syncthreads();
+  return max(carry, ex);
+}
+
+template <int NW>
+__device__ __forceinline__ int block_excl_min_rev_n(int v, int* sh, int t, int identity) {
+  const int lane = t & (kWave - 1), wv = t / kWave;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int y = __shfl_down(x, off, kWave);
+    if (lane + off < kWave) x = min(x, y);
+  }
+  if (lane == 0) sh[wv] = x;
+  __syncthreads();
+  int carry = identity;
+  for (int w2 = wv + 1; w2 < NW; ++w2) carry = min(carry, sh[w2]);
+  int ex = __shfl_down(x, 1, kWave);
+  if (lane == kWave - 1) ex = identity;
+  __syncthreads();
+  return min(carry, ex);
+}
+
+__global__ __launch_bounds__(kFT) void ring_plan_fast(
     const int64_t* __restrict__ src, const int64_t* __restrict__ dst,
     const double* __restrict__ time, int n, int b, int64_t N, int B, int64_t* __restrict__ wp,
     int64_t* __restrict__ dest, int32_t* status) {
-  __shared__ uint32_t keys[kLdsMaxEntries];
-  __shared__ uint16_t pa[kLdsMaxEntries];
-  __shared__ uint16_t pb[kLdsMaxEntries];
-  __shared__ uint32_t cnt[8 * kPlanThreads];
-  __shared__ uint32_t wsum[kPlanWaves * 16];
-  __shared__ int ish[kPlanWaves];
-  __shared__ double dsh[kPlanWaves];
-  plan_body<uint16_t, true>(src, dst, time, n, b, N, B, wp, dest, keys, pa, pb, cnt, wsum, ish,
-                            dsh, status);
+  // exchange arrays, padded by one entry per 32 (index p + p/32) so the
+  // blocked reads t*E + e spread over the LDS banks
+  __shared__ uint32_t xk[kFT * kFE + kFT * kFE / 32];
+  __shared__ uint16_t xv[kFT * kFE + kFT * kFE / 32];
+  __shared__ uint16_t offs[16 * kFT];
+  __shared__ uint64_t wsum[kFW * 4];
+  __shared__ int ish[kFW];
+  __shared__ double dsh[kFW];
+  const int t = threadIdx.x;
+  const int lane = t & (kWave - 1), wv = t / kWave;
+  const int E = (n + kFT - 1) / kFT;
+  const uint32_t kInvalid = static_cast<uint32_t>(N);
+  const uint32_t kPad = static_cast<uint32_t>(N) + 1u;
+
+  uint32_t k[kFE], v[kFE];
+  int bad = 0;
+#pragma unroll
+  for (int e = 0; e < kFE; ++e) {
+    const int p = t * E + e;
+    k[e] = kPad;
+    v[e] = static_cast<uint32_t>(p);
+    if (e < E && p < n) {
+      const int64_t u = p < b ? src[p] : dst[p - b];
+      if (u < 0 || u >= N) {
+        k[e] = kInvalid;
+        ++bad;
+      } else {
+        k[e] = static_cast<uint32_t>(u);
+      }
+    }
+  }
+  double mx = -__builtin_inf();
+  for (int i = t; i < b; i += kFT) mx = fmax(mx, time[i]);
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    bad += __shfl_xor(bad, off, kWave);
+    mx = fmax(mx, __shfl_xor(mx, off, kWave));
+  }
+  if (lane == 0) {
+    ish[wv] = bad;
+    dsh[wv] = mx;
+  }
+  __syncthreads();
+  if (t == 0 && status != nullptr) {
+    int tb = 0;
+    double tm = -__builtin_inf();
+    for (int w2 = 0; w2 < kFW; ++w2) {
+      tb += ish[w2];
+      tm = fmax(tm, dsh[w2]);
+    }
+    if (tb) atomicAdd(&status[TGX_ST_BAD_EVENT_NODE], tb);
+    if (!(trunc(tm) > static_cast<double>(n - 3))) atomicAdd(&status[TGX_ST_KEY_COLLISION], 1);
+  }
+  __syncthreads();
+
+  const int nbits = 32 - __clz(kPad);
+  for (int shift = 0; shift < nbits; shift += 4) {
+    // per-thread digit counts (8-bit fields: digits 0-7 in c0, 8-15 in c1)
+    uint64_t c0 = 0, c1 = 0;
+#pragma unroll
+    for (int e = 0; e < kFE; ++e) {
+      if (e < E) {
+        const uint32_t d = (k[e] >> shift) & 15u;
+        const uint64_t inc = uint64_t(1) << ((d & 7u) * 8u);
+        if (d < 8u) c0 += inc; else c1 += inc;
+      }
+    }
+    // counts as four u64 of 16-bit fields (digits 4j..4j+3)
+    uint64_t q[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint64_t c = j < 2 ? c0 : c1;
+      const int b0 = (j & 1) * 32;
+      q[j] = ((c >> b0) & 0xFFu) | (((c >> (b0 + 8)) & 0xFFu) << 16) |
+             (((c >> (b0 + 16)) & 0xFFu) << 32) | (((c >> (b0 + 24)) & 0xFFu) << 48);
+    }
+    uint64_t x[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      x[j] = q[j];
+#pragma unroll
+      for (int off = 1; off < kWave; off <<= 1) {
+        const uint64_t y = shfl_up_u64(x[j], off);
+        if (lane >= off) x[j] += y;
+      }
+    }
+    if (lane == kWave - 1) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wsum[wv * 4 + j] = x[j];
+    }
+    __syncthreads();
+    uint64_t tot[4] = {0, 0, 0, 0};
+    for (int w2 = 0; w2 < kFW; ++w2) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint64_t s2 = wsum[w2 * 4 + j];
+        if (w2 < wv) x[j] += s2;
+        tot[j] += s2;
+      }
+    }
+    uint32_t run = 0;
+#pragma unroll
+    for (int d = 0; d < 16; ++d) {
+      const uint32_t ex = static_cast<uint32_t>(((x[d >> 2] - q[d >> 2]) >> ((d & 3) * 16)) & 0xFFFFu);
+      offs[d * kFT + t] = static_cast<uint16_t>(run + ex);
+      run += static_cast<uint32_t>((tot[d >> 2] >> ((d & 3) * 16)) & 0xFFFFu);
+    }
+    // scatter; in-thread ranks are recounted in the same order
+    c0 = 0;
+    c1 = 0;
+#pragma unroll
+    for (int e = 0; e < kFE; ++e) {
+      if (e < E) {
+        const uint32_t d = (k[e] >> shift) & 15u;
+        const uint32_t sh = (d & 7u) * 8u;
+        const uint64_t c = d < 8u ? c0 : c1;
+        const uint32_t rk = static_cast<uint32_t>((c >> sh) & 0xFFu);
+        const uint64_t cn = c + (uint64_t(1) << sh);
+        if (d < 8u) c0 = cn; else c1 = cn;
+        const uint32_t pos = static_cast<uint32_t>(offs[d * kFT + t]) + rk;
+        xk[pad32(pos)] = k[e];
+        xv[pad32(pos)] = static_cast<uint16_t>(v[e]);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < kFE; ++e) {
+      if (e < E) {
+        k[e] = xk[pad32(t * E + e)];
+        v[e] = xv[pad32(t * E + e)];
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- runs of equal keys over the sorted positions ----
+  const int L = kFT * E;
+  int last_head = -1, first_head = L;
+  uint32_t prevk = (t == 0) ? 0xFFFFFFFFu : xk[pad32(t * E - 1)];
+  uint32_t heads = 0;  // bit e: position t*E+e starts a run
+#pragma unroll
+  for (int e = 0; e < kFE; ++e) {
+    if (e < E) {
+      const int p = t * E + e;
+      if (p == 0 || k[e] != prevk) {
+        heads |= 1u << e;
+        last_head = p;
+        if (first_head == L) first_head = p;
+      }
+      prevk = k[e];
+    }
+  }
+  int start = block_excl_max_n<kFW>(last_head, ish, t);
+  const int next_after = block_excl_min_rev_n<kFW>(first_head, ish, t, L);
+  int st[kFE];
+#pragma unroll
+  for (int e = 0; e < kFE; ++e) {
+    if (e < E && ((heads >> e) & 1u)) start = t * E + e;
+    st[e] = start;
+  }
+  int run_end = next_after;
+#pragma unroll
+  for (int e = kFE - 1; e >= 0; --e) {
+    if (e < E) {
+      const int p = t * E + e;
+      const int c = run_end - st[e];
+      const int kept = min(c, B);
+      const int m = p - st[e];
+      if (static_cast<int>(v[e]) < n) {
+        int64_t dslot = -1;
+        if (k[e] < kInvalid && m >= c - kept) {
+          const int64_t slot = ring_slot(wp[k[e]], m - (c - kept), B);
+          dslot = static_cast<int64_t>(k[e]) * B + slot;
+        }
+        dest[v[e]] = dslot;
+      }
+      if ((heads >> e) & 1u) {
+        xv[pad32(p)] = static_cast<uint16_t>(kept);  // the sorted indices now live in registers
+        run_end = p;
+      }
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < kFE; ++e) {
+    if (e < E && ((heads >> e) & 1u) && k[e] < kInvalid) wp[k[e]] += xv[pad32(t * E + e)];
+  }
 }
 
 __global__ __launch_bounds__(kPlanThreads) void ring_plan_global(
@@ -401,7 +648,7 @@ extern "C" int tgx_ring_append(const tgx_ring* ring, const int64_t* src, const i
   int64_t* dest = reinterpret_cast<int64_t*>(ws);
 
   if (n <= kLdsMaxEntries) {
-    hipLaunchKernelGGL(ring_plan_lds, dim3(1), dim3(kPlanThreads), 0, stream, src, dst, time,
+    hipLaunchKernelGGL(ring_plan_fast, dim3(1), dim3(kFT), 0, stream, src, dst, time,
                        static_cast<int>(n), static_cast<int>(b), ring->num_nodes, ring->slots,
                        ring->write_pos, dest, status);
   } else {

@@ -85,30 +85,23 @@ class DataPipeline:
         device = raw_batch.device
         b = raw_batch.src.shape[0]
 
-        names, node_groups, time_groups, sizes, per_event = [], [], [], [], []
+        # query groups in the reference order [src, dst, neg (row-major), neg_src],
+        # read in place by the kernel: (nodes, times, negatives per event)
+        names, qgroups, sizes, per_event = [], [], [], []
         if "src" in fn:
-            names.append("src"); node_groups.append(raw_batch.src); time_groups.append(raw_batch.time)
+            names.append("src"); qgroups.append((raw_batch.src, raw_batch.time, 1))
             sizes.append(b); per_event.append(1)
         if "dst" in fn:
-            names.append("dst"); node_groups.append(raw_batch.dst); time_groups.append(raw_batch.time)
+            names.append("dst"); qgroups.append((raw_batch.dst, raw_batch.time, 1))
             sizes.append(b); per_event.append(1)
         if "neg" in fn and raw_batch.neg is not None:
             neg = raw_batch.neg
-            if neg.ndim > 1:
-                node_groups.append(neg.reshape(-1))
-                time_groups.append(raw_batch.time.unsqueeze(1).expand_as(neg).reshape(-1))
-                per_event.append(neg.shape[1])
-            else:
-                node_groups.append(neg)
-                time_groups.append(raw_batch.time)
-                per_event.append(1)
-            names.append("neg"); sizes.append(node_groups[-1].shape[0])
+            per = neg.shape[1] if neg.ndim > 1 else 1
+            names.append("neg"); qgroups.append((neg.reshape(-1), raw_batch.time, per))
+            sizes.append(neg.numel()); per_event.append(per)
         if "neg" in fn and raw_batch.neg_src is not None:
-            names.append("neg_src"); node_groups.append(raw_batch.neg_src)
-            time_groups.append(raw_batch.time); sizes.append(b); per_event.append(1)
-
-        all_nodes = torch.cat(node_groups)
-        all_times = torch.cat(time_groups)
+            names.append("neg_src"); qgroups.append((raw_batch.neg_src, raw_batch.time, 1))
+            sizes.append(b); per_event.append(1)
 
         want_co = spec.co_occurrence and "src" in names and "dst" in names
         co_mode = _CO_MODES[spec.co_occurrence_mode] if want_co else _lib.TGX_CO_NONE
@@ -119,18 +112,19 @@ class DataPipeline:
         dt_mode = _DT_MODES[spec.dt_mode]
 
         if k2 > 0:
+            all_nodes = torch.cat([g[0].reshape(-1) for g in qgroups])
+            all_times = torch.cat([g[1].repeat_interleave(g[2]) if g[2] > 1 else g[1]
+                                   for g in qgroups])
             hop = self.graph.recent_2hop(all_nodes, all_times, k, k2)
             out = {"ids": hop.neighbor_ids, "times": hop.timestamps, "feats": hop.edge_feats,
                    "mask": hop.mask, "eids": hop.edge_ids}
             extra = {"hop2_ids": hop.hop2_ids, "hop2_times": hop.hop2_times,
                      "hop2_feats": hop.hop2_feats, "hop2_mask": hop.hop2_mask}
             if d_t > 0 or want_co:
-                o2 = self._fused(all_nodes, all_times, k, b, per_event, names, d_t, te_w, te_b,
-                                 dt_mode, co_mode)
+                o2 = self._fused(qgroups, k, b, per_event, d_t, te_w, te_b, dt_mode, co_mode)
                 out.update({kk: o2[kk] for kk in ("te", "co_a", "co_c", "co_pair") if kk in o2})
         else:
-            out = self._fused(all_nodes, all_times, k, b, per_event, names, d_t, te_w, te_b,
-                              dt_mode, co_mode)
+            out = self._fused(qgroups, k, b, per_event, d_t, te_w, te_b, dt_mode, co_mode)
             extra = {}
 
         def split(t):
@@ -167,8 +161,7 @@ class DataPipeline:
             node_labels=raw_batch.node_labels, edge_labels=raw_batch.edge_labels,
             node_feat=raw_batch.node_feat, co_occurrence_freq=co_freq)
 
-    def _fused(self, all_nodes, all_times, k, b, per_event, names, d_t, te_w, te_b, dt_mode,
-               co_mode) -> dict:
+    def _fused(self, qgroups, k, b, per_event, d_t, te_w, te_b, dt_mode, co_mode) -> dict:
         g = self.graph
         if co_mode != _lib.TGX_CO_NONE:
             # event-major groups: event p -> [src p, dst p, its negatives, neg_src p]
@@ -180,11 +173,11 @@ class DataPipeline:
             if G > _lib.TGX_MAX_GROUP:
                 raise ValueError(f"{G} queries per event exceed the fused group limit {_lib.TGX_MAX_GROUP}")
             plan = self._plan(("ev", b, tuple(per_event)), b, offs)
-            return g._query(all_nodes, all_times, k, plan=plan, group=G, num_groups=b, d_t=d_t,
-                            te_w=te_w, te_b=te_b, dt_mode=dt_mode, co_mode=co_mode,
+            return g._query(None, None, k, groups=qgroups, plan=plan, group=G, num_groups=b,
+                            d_t=d_t, te_w=te_w, te_b=te_b, dt_mode=dt_mode, co_mode=co_mode,
                             want_eids=self.spec.edge_ids)
-        return g._query(all_nodes, all_times, k, d_t=d_t, te_w=te_w, te_b=te_b, dt_mode=dt_mode,
-                        want_eids=self.spec.edge_ids)
+        return g._query(None, None, k, groups=qgroups, d_t=d_t, te_w=te_w, te_b=te_b,
+                        dt_mode=dt_mode, want_eids=self.spec.edge_ids)
 
     @staticmethod
     def _co_occur_from_neighbors(src_nbrs: NeighborData, dst_nbrs: NeighborData) -> Tensor:
