@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define TGX_ABI_VERSION 2
+#define TGX_ABI_VERSION 3
 
 /* status codes */
 #define TGX_OK 0
@@ -67,7 +67,12 @@ extern "C" {
 
 /* Per-node ring of `slots` entries (reference: temporal_graph.py:89-102).
  * ids int32 [N,B] (-1 empty), times float64 [N,B], feats [N,B,feat_dim] of
- * feat_dtype, write_pos int64 [N], eids int64 [N,B] (optional, may be NULL). */
+ * feat_dtype, write_pos int64 [N], eids int64 [N,B] (optional, may be NULL).
+ * scratch: tgx_ring_scratch_size(N) bytes of device memory, zero-filled once by
+ * the caller before the first append and otherwise left to the library: its
+ * first N int32 are per-node counters that every tgx_ring_append restores to
+ * zero, the rest is rewritten before each use.  Needed by tgx_ring_append only
+ * (tgx_recent ignores it). */
 typedef struct tgx_ring {
   int64_t num_nodes;
   int32_t slots;
@@ -79,6 +84,7 @@ typedef struct tgx_ring {
   void* feats;
   int64_t* write_pos;
   int64_t* eids;
+  int32_t* scratch;
 } tgx_ring;
 
 /* Frozen CSR (reference: temporal_graph.py:133-181): offsets int64 [N+1],
@@ -137,7 +143,7 @@ typedef struct tgx_recent_args {
   int32_t co_mode;         /* TGX_CO_* */
   int32_t* co_a;           /* FREQ: [P,K,2]; DYGFORMER: [P,1+K,2] */
   int32_t* co_c;
-  float* co_pair;          /* FREQ only: [P] float count, may be NULL */
+  float* co_pair;          /* [P] float shared-neighbour count (both modes), may be NULL */
   int32_t* status;         /* [TGX_STATUS_WORDS] or NULL */
   int32_t num_query_groups;                          /* 0 = use nodes/times */
   tgx_query_group query_groups[TGX_MAX_QUERY_GROUPS];
@@ -154,11 +160,13 @@ typedef struct tgx_recent_args {
  * (write_pos + m) % B, m = 0.., and write_pos grows by min(c, B).
  * feat: [b, feat_dim] in ring->feat_dtype, or NULL for zero features.
  * eids (if the ring has them) receive eid_base + event index.
- * workspace: tgx_ring_append_workspace_size(b) bytes of device memory. */
+ * workspace: tgx_ring_append_workspace_size(b) bytes of device memory (no
+ * initialisation needed).  Calls on one ring must be ordered (one stream). */
 int tgx_ring_append(const tgx_ring* ring, const int64_t* src, const int64_t* dst,
                     const double* time, const void* feat, int64_t b, int64_t eid_base,
                     void* workspace, size_t workspace_bytes, int32_t* status, void* stream);
 size_t tgx_ring_append_workspace_size(int64_t b);
+size_t tgx_ring_scratch_size(int64_t num_nodes);
 
 /* Fused most-recent-K gather (+ time encoding, + co-occurrence) (kernels b, c).
  * ring and/or csr may be NULL (no candidates from that store). */

@@ -35,7 +35,7 @@ c_i32, c_i64, c_vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p
 class TgxRing(ctypes.Structure):
     _fields_ = [("num_nodes", c_i64), ("slots", c_i32), ("feat_dim", c_i32),
                 ("feat_dtype", c_i32), ("reserved", c_i32), ("ids", c_vp), ("times", c_vp),
-                ("feats", c_vp), ("write_pos", c_vp), ("eids", c_vp)]
+                ("feats", c_vp), ("write_pos", c_vp), ("eids", c_vp), ("scratch", c_vp)]
 
 
 class TgxCsr(ctypes.Structure):
@@ -68,6 +68,7 @@ SIGNATURES = {
     "tgx_ring_append": (c_i32, [ctypes.POINTER(TgxRing), c_vp, c_vp, c_vp, c_vp, c_i64, c_i64,
                                 c_vp, ctypes.c_size_t, c_vp, c_vp]),
     "tgx_ring_append_workspace_size": (ctypes.c_size_t, [c_i64]),
+    "tgx_ring_scratch_size": (ctypes.c_size_t, [c_i64]),
     "tgx_recent": (c_i32, [ctypes.POINTER(TgxRing), ctypes.POINTER(TgxCsr),
                            ctypes.POINTER(TgxRecentArgs), c_vp]),
     "tgx_co_occurrence": (c_i32, [c_vp, c_vp, c_i64, c_i32, c_vp, c_vp, c_vp, c_vp]),
@@ -100,7 +101,7 @@ def lib() -> ctypes.CDLL:
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
-        if handle.tgx_abi_version() != 2:
+        if handle.tgx_abi_version() != 3:
             raise RuntimeError("libtgx ABI version mismatch")
         _lib = handle
         return _lib

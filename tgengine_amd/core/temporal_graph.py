@@ -94,6 +94,7 @@ class TemporalGraph:
         self._ov_feats: Optional[Tensor] = None
         self._ov_write_pos: Optional[Tensor] = None
         self._ov_eids: Optional[Tensor] = None
+        self._ov_scratch: Optional[Tensor] = None
 
         self._status = torch.zeros(_lib.TGX_STATUS_WORDS, dtype=torch.int32, device=self.device)
         self._ws: Optional[Tensor] = None
@@ -115,6 +116,9 @@ class TemporalGraph:
         self._ov_write_pos = torch.zeros(N, dtype=torch.int64, device=dev)
         if self.track_edge_ids:
             self._ov_eids = torch.full((N, B), -1, dtype=torch.int64, device=dev)
+        # per-node counters of tgx_ring_append (zero between calls)
+        nscr = int(_lib.lib().tgx_ring_scratch_size(N)) // 4
+        self._ov_scratch = torch.zeros(nscr, dtype=torch.int32, device=dev)
         self._ring_struct = None
 
     def _ring(self) -> Optional[_lib.TgxRing]:
@@ -126,7 +130,7 @@ class TemporalGraph:
                 feat_dtype=_DTYPES[self.feat_dtype], reserved=0,
                 ids=self._ov_ids.data_ptr(), times=self._ov_times.data_ptr(),
                 feats=self._ov_feats.data_ptr(), write_pos=self._ov_write_pos.data_ptr(),
-                eids=_lib.ptr(self._ov_eids))
+                eids=_lib.ptr(self._ov_eids), scratch=self._ov_scratch.data_ptr())
         return self._ring_struct
 
     def _csr(self) -> Optional[_lib.TgxCsr]:
@@ -360,6 +364,7 @@ class TemporalGraph:
         self._build = []
         self._offsets = self._nbr_ids = self._nbr_times = self._nbr_feats = self._nbr_eids = None
         self._ov_ids = self._ov_times = self._ov_feats = self._ov_write_pos = self._ov_eids = None
+        self._ov_scratch = None
         self._ring_struct = None
         self._csr_struct = None
         self._num_edges = 0

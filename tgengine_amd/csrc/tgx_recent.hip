@@ -405,6 +405,18 @@ __global__ __launch_bounds__(512) void recent_fused(Params P) {
         const int32_t nc0 = static_cast<int32_t>(query_node(P, qc));
         const int L = K + 1;
         int32_t* out = wv == 0 ? P.co_a : P.co_c;
+        if (wv == 0 && P.co_pair != nullptr) {
+          // (B,) count over the K sequences, as in FREQ mode
+          int pc = 0;
+          for (int i0 = 0; i0 < K; i0 += kWave) {
+            const int i = i0 + lane;
+            bool hit = false;
+            if (i < K && A[i] != -1)
+              for (int j = 0; j < K && !hit; ++j) hit = Cc[j] == A[i];
+            pc += __popcll(__ballot(hit));
+          }
+          if (lane == 0) P.co_pair[g] = static_cast<float>(pc);
+        }
         for (int i = lane; i < L; i += kWave) {
           const int32_t ai = i == 0 ? na0 : A[i - 1];
           const int32_t ci = i == 0 ? nc0 : Cc[i - 1];

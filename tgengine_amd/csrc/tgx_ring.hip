@@ -5,555 +5,54 @@
 // directed entries in concatenation order i = [src->dst for every event,
 // dst->src for every event].  Grouped by `from` node in that order, each node
 // with c entries keeps its last min(c, B); the m-th kept entry goes to slot
-// (write_pos + m) % B and write_pos grows by min(c, B).
+// (write_pos + m) % B and write_pos grows by min(c, B).  Equivalently, the
+// entry with e later same-node entries is kept iff e < kept = min(c, B) and
+// lands in slot (write_pos + kept - 1 - e) % B.
 //
-// Design.  Two launches on the caller's stream:
-//   1. ring_plan: ONE workgroup of 512 threads.  A stable LSD radix sort with
-//      4-bit digits orders the entry indices by node id (stable, so concat
-//      order survives inside a node); two block scans find every run's start
-//      and end; each entry gets its destination slot u*B + s (or -1 when it is
-//      not among the last B of its node), and every run head advances
-//      write_pos.  For n <= 16384 the keys (64 KB) and the two index buffers
-//      (2 x 32 KB, uint16) live in LDS; larger batches use the same code on a
-//      global-memory workspace.
-//   2. ring_write: wide copy of ids / times / edge ids / feature rows into
-//      the planned slots, 16-byte vector accesses when the row allows it.
-// The sort is integer work on one CU by design: a batch holds at most a few
-// thousand distinct nodes, while a device-wide sort would cost several
-// launches; the feature bytes move in the wide kernel.
+// Design: four launches on the caller's stream, all spread over the device.
+//   1. count  : per-node tickets from node-indexed counters owned by the ring
+//               (zero between calls); equal nodes inside a wavefront are
+//               matched first so a hot node costs one atomic per wavefront.
+//   2. groups : the ticket-0 entry of every node seen more than once reserves
+//               a contiguous list of c slots and a group id, small (c <= 64)
+//               or large (one atomic per wave, offsets by a wave scan).
+//   3. fill   : list[base[u] + ticket] = entry index.
+//   4. commit : singletons (c == 1) are written directly; a small group is
+//               ranked by one wavefront in registers, a large group by a whole
+//               workgroup over LDS bitmaps of 8192-index windows walked down
+//               from the top of the batch; kept entries are written, count[u]
+//               is restored to zero and write_pos advances.
+// Feature rows move as 16-byte vectors when the row allows it.
 #include "tgx_internal.h"
 
 namespace tgx {
 namespace {
 
-constexpr int kPlanThreads = 512;
-constexpr int kPlanWaves = kPlanThreads / kWave;
-constexpr int kLdsMaxEntries = 16384;
+constexpr int kThreads = 256;
+constexpr int kCommitWaves = kThreads / kWave;
+constexpr int kWinBits = 8192;                 // bitmap window (indices)
+constexpr int kWinWords = kWinBits / 32;       // 256 words = 1 KB
+static_assert(kWinWords == kThreads, "one bitmap word per thread");
+enum { kCtlCursor = 0, kCtlGroups = 1, kCtlTimeOk = 2, kCtlLarge = 3 };
 
-__device__ __forceinline__ int pad32(int p) { return p + (p >> 5); }
-
-// (write_pos + off) % B for write_pos >= 0, 0 <= off < B; 32-bit arithmetic
-// whenever the value fits (B is usually a power of two)
+// (write_pos + off) % B for write_pos >= 0, 0 <= off < B
 __device__ __forceinline__ int64_t ring_slot(int64_t w, int off, int B) {
   const uint64_t x = static_cast<uint64_t>(w) + static_cast<uint64_t>(off);
   if ((B & (B - 1)) == 0) return static_cast<int64_t>(x & static_cast<uint64_t>(B - 1));
-  if (x < (uint64_t(1) << 32)) return static_cast<int64_t>(static_cast<uint32_t>(x) % static_cast<uint32_t>(B));
+  if (x < (uint64_t(1) << 32))
+    return static_cast<int64_t>(static_cast<uint32_t>(x) % static_cast<uint32_t>(B));
   return static_cast<int64_t>(x % static_cast<uint64_t>(B));
 }
 
-
-// ---------------------------------------------------------------------------
-// digit counters, one column per thread.
-//   packed: word (d>>1)*T + t holds the 16-bit counters of digits 2j, 2j+1
-//   wide:   word d*T + t holds the 32-bit counter of digit d
-// ---------------------------------------------------------------------------
-template <bool kPacked>
-struct Counters {
-  static constexpr int kWords = kPacked ? 8 : 16;
-  uint32_t* w;
-  __device__ __forceinline__ void zero_own(int t) {
-#pragma unroll
-    for (int j = 0; j < kWords; ++j) w[j * kPlanThreads + t] = 0u;
-  }
-  __device__ __forceinline__ void add1(uint32_t d, int t) {
-    if (kPacked)
-      atomicAdd(&w[(d >> 1) * kPlanThreads + t], 1u << ((d & 1u) * 16u));
-    else
-      atomicAdd(&w[d * kPlanThreads + t], 1u);
-  }
-  __device__ __forceinline__ uint32_t fetch_add1(uint32_t d, int t) {
-    if (kPacked) {
-      const uint32_t sh = (d & 1u) * 16u;
-      const uint32_t old = atomicAdd(&w[(d >> 1) * kPlanThreads + t], 1u << sh);
-      return (old >> sh) & 0xFFFFu;
-    } else {
-      return atomicAdd(&w[d * kPlanThreads + t], 1u);
-    }
-  }
-};
-
-__device__ __forceinline__ uint32_t wave_incl_scan_add(uint32_t x, int lane) {
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const uint32_t y = __shfl_up(x, off, kWave);
-    if (lane >= off) x += y;
-  }
-  return x;
+__device__ __forceinline__ int64_t entry_node(const int64_t* src, const int64_t* dst, int64_t i,
+                                              int64_t b) {
+  return i < b ? src[i] : dst[i - b];
 }
 
-// Block-wide exclusive scan of the per-(digit, thread) counters in digit-major
-// order; the counters are replaced by the scatter offsets.
-template <bool kPacked>
-__device__ __forceinline__ void scan_counters(Counters<kPacked> cnt, uint32_t* wsum, int t) {
-  constexpr int W = Counters<kPacked>::kWords;
-  const int lane = t & (kWave - 1), wv = t / kWave;
-  uint32_t c[W], x[W];
-#pragma unroll
-  for (int j = 0; j < W; ++j) {
-    c[j] = cnt.w[j * kPlanThreads + t];
-    x[j] = wave_incl_scan_add(c[j], lane);
-  }
-  if (lane == kWave - 1) {
-#pragma unroll
-    for (int j = 0; j < W; ++j) wsum[wv * W + j] = x[j];
-  }
-  __syncthreads();
-  uint32_t tot[W];
-#pragma unroll
-  for (int j = 0; j < W; ++j) tot[j] = 0u;
-  for (int w2 = 0; w2 < kPlanWaves; ++w2) {
-#pragma unroll
-    for (int j = 0; j < W; ++j) {
-      const uint32_t s = wsum[w2 * W + j];
-      if (w2 < wv) x[j] += s;
-      tot[j] += s;
-    }
-  }
-  // digit totals -> exclusive digit bases
-  uint32_t base[16];
-  uint32_t run = 0;
-#pragma unroll
-  for (int d = 0; d < 16; ++d) {
-    base[d] = run;
-    const uint32_t td = kPacked ? ((tot[d >> 1] >> ((d & 1) * 16)) & 0xFFFFu) : tot[d];
-    run += td;
-  }
-#pragma unroll
-  for (int j = 0; j < W; ++j) {
-    const uint32_t ex = x[j] - c[j];  // fieldwise exclusive (no borrow: x >= c per field)
-    if (kPacked) {
-      const uint32_t lo = base[2 * j] + (ex & 0xFFFFu);
-      const uint32_t hi = base[2 * j + 1] + (ex >> 16);
-      cnt.w[j * kPlanThreads + t] = lo | (hi << 16);
-    } else {
-      cnt.w[j * kPlanThreads + t] = base[j] + ex;
-    }
-  }
-}
-
-// exclusive max-scan (forward) of one int per thread
-__device__ __forceinline__ int block_excl_max(int v, int* sh, int t) {
-  const int lane = t & (kWave - 1), wv = t / kWave;
-  int x = v;
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const int y = __shfl_up(x, off, kWave);
-    if (lane >= off) x = max(x, y);
-  }
-  if (lane == kWave - 1) sh[wv] = x;
-  __syncthreads();
-  int carry = -1;
-  for (int w2 = 0; w2 < wv; ++w2) carry = max(carry, sh[w2]);
-  int ex = __shfl_up(x, 1, kWave);
-  if (lane == 0) ex = -1;
-  __syncthreads();
-  return max(carry, ex);
-}
-
-// exclusive min-scan from the right (carry = min over threads > t)
-__device__ __forceinline__ int block_excl_min_rev(int v, int* sh, int t, int identity) {
-  const int lane = t & (kWave - 1), wv = t / kWave;
-  int x = v;
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const int y = __shfl_down(x, off, kWave);
-    if (lane + off < kWave) x = min(x, y);
-  }
-  if (lane == 0) sh[wv] = x;
-  __syncthreads();
-  int carry = identity;
-  for (int w2 = wv + 1; w2 < kPlanWaves; ++w2) carry = min(carry, sh[w2]);
-  int ex = __shfl_down(x, 1, kWave);
-  if (lane == kWave - 1) ex = identity;
-  __syncthreads();
-  return min(carry, ex);
-}
-
-template <typename IdxT, bool kPacked>
-__device__ __forceinline__ void plan_body(const int64_t* __restrict__ src,
-                                          const int64_t* __restrict__ dst,
-                                          const double* __restrict__ time, int n, int b,
-                                          int64_t N, int B, int64_t* __restrict__ wp,
-                                          int64_t* __restrict__ dest, uint32_t* keys, IdxT* pa,
-                                          IdxT* pb, uint32_t* cnt_words, uint32_t* wsum,
-                                          int* ish, double* dsh, int32_t* status) {
-  const int t = threadIdx.x;
-  const int lane = t & (kWave - 1), wv = t / kWave;
-  Counters<kPacked> cnt{cnt_words};
-
-  // ---- keys (node id, N = invalid sentinel) and diagnostics ----
-  int bad = 0;
-  for (int i = t; i < n; i += kPlanThreads) {
-    const int64_t u = i < b ? src[i] : dst[i - b];
-    uint32_t k;
-    if (u < 0 || u >= N) {
-      k = static_cast<uint32_t>(N);
-      ++bad;
-    } else {
-      k = static_cast<uint32_t>(u);
-    }
-    keys[i] = k;
-    pa[i] = static_cast<IdxT>(i);
-  }
-  double mx = -__builtin_inf();
-  for (int i = t; i < b; i += kPlanThreads) mx = fmax(mx, time[i]);
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off >>= 1) {
-    bad += __shfl_xor(bad, off, kWave);
-    mx = fmax(mx, __shfl_xor(mx, off, kWave));
-  }
-  if (lane == 0) {
-    ish[wv] = bad;
-    dsh[wv] = mx;
-  }
-  __syncthreads();
-  if (t == 0 && status != nullptr) {
-    int tb = 0;
-    double tm = -__builtin_inf();
-    for (int w2 = 0; w2 < kPlanWaves; ++w2) {
-      tb += ish[w2];
-      tm = fmax(tm, dsh[w2]);
-    }
-    if (tb) atomicAdd(&status[TGX_ST_BAD_EVENT_NODE], tb);
-    // reference key from*(int(max t)+2)+i is lexicographic iff int(max t)+2 > n-1
-    if (!(trunc(tm) > static_cast<double>(n - 3))) atomicAdd(&status[TGX_ST_KEY_COLLISION], 1);
-  }
-  __syncthreads();
-
-  // ---- stable LSD radix sort of entry indices by key, 4-bit digits ----
-  const int nbits = 32 - __clz(static_cast<uint32_t>(N));  // covers the sentinel N
-  const int passes = (nbits + 3) / 4;
-  const int E = (n + kPlanThreads - 1) / kPlanThreads;
-  const int beg = min(n, t * E);
-  const int end = min(n, beg + E);
-  IdxT* in = pa;
-  IdxT* out = pb;
-  for (int ps = 0; ps < passes; ++ps) {
-    const int shift = ps * 4;
-    cnt.zero_own(t);
-    for (int p = beg; p < end; ++p) cnt.add1((keys[in[p]] >> shift) & 15u, t);
-    __syncthreads();
-    scan_counters<kPacked>(cnt, wsum, t);
-    __syncthreads();
-    for (int p = beg; p < end; ++p) {
-      const IdxT v = in[p];
-      const uint32_t pos = cnt.fetch_add1((keys[v] >> shift) & 15u, t);
-      out[pos] = v;
-    }
-    __syncthreads();
-    IdxT* tmp = in;
-    in = out;
-    out = tmp;
-  }
-  // `in` = sorted permutation, `out` = free buffer
-
-  // ---- run starts (forward) ----
-  int last_head = -1, first_head = n;
-  for (int p = beg; p < end; ++p) {
-    const bool head = (p == 0) || (keys[in[p]] != keys[in[p - 1]]);
-    if (head) {
-      last_head = p;
-      if (first_head == n) first_head = p;
-    }
-  }
-  int start = block_excl_max(last_head, ish, t);
-  const int next_head_after = block_excl_min_rev(first_head, ish, t, n);
-  for (int p = beg; p < end; ++p) {
-    const bool head = (p == 0) || (keys[in[p]] != keys[in[p - 1]]);
-    if (head) start = p;
-    out[p] = static_cast<IdxT>(start);
-  }
-  // ---- run ends (backward) and destinations ----
-  int run_end = next_head_after;
-  for (int p = end - 1; p >= beg; --p) {
-    const int s = static_cast<int>(out[p]);
-    const uint32_t u = keys[in[p]];
-    const int idx = static_cast<int>(in[p]);
-    const int c = run_end - s;
-    const int kept = min(c, B);
-    const int m = p - s;
-    int64_t dslot = -1;
-    if (u < static_cast<uint32_t>(N) && m >= c - kept) {
-      const int64_t w0 = wp[u];
-      const int64_t slot = ring_slot(w0, m - (c - kept), B);
-      dslot = static_cast<int64_t>(u) * B + slot;
-    }
-    dest[idx] = dslot;
-    if (p == s) {
-      out[p] = static_cast<IdxT>(kept);  // run head keeps the kept count
-      run_end = s;
-    }
-  }
-  __syncthreads();
-  // ---- advance write_pos once per node ----
-  for (int p = beg; p < end; ++p) {
-    const uint32_t u = keys[in[p]];
-    const bool head = (p == 0) || (u != keys[in[p - 1]]);
-    if (head && u < static_cast<uint32_t>(N)) wp[u] += static_cast<int64_t>(out[p]);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Fast plan for n <= 16384 entries: one workgroup of 1024 threads, each
-// owning 16 consecutive positions of the array in registers ("blocked"
-// arrangement).  Per 4-bit pass: digits and in-thread ranks in registers
-// (8-bit counters packed in two u64), one block-wide scan of the 16 digit
-// counts (16-bit fields packed in four u64), a scatter of (key, index) into
-// LDS and a gather back into registers.  Only the exchange arrays and the
-// per-thread digit offsets live in LDS (64 + 32 + 32 KB).
-// ---------------------------------------------------------------------------
-constexpr int kFT = 512;              // threads
-constexpr int kFW = kFT / kWave;      // waves
-constexpr int kFE = 32;               // items per thread
-
-__device__ __forceinline__ uint64_t shfl_up_u64(uint64_t x, int off) {
-  const uint32_t lo = __shfl_up(static_cast<uint32_t>(x), off, kWave);
-  const uint32_t hi = __shfl_up(static_cast<uint32_t>(x >> 32), off, kWave);
-  return (static_cast<uint64_t>(hi) << 32) | lo;
-}
-
-template <int NW>
-__device__ __forceinline__ int block_excl_max_n(int v, int* sh, int t) {
-  const int lane = t & (kWave - 1), wv = t / kWave;
-  int x = v;
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const int y = __shfl_up(x, off, kWave);
-    if (lane >= off) x = max(x, y);
-  }
-  if (lane == kWave - 1) sh[wv] = x;
-  __syncthreads();
-  int carry = -1;
-  for (int w2 = 0; w2 < wv; ++w2) carry = max(carry, sh[w2]);
-  int ex = __shfl_up(x, 1, kWave);
-  if (lane == 0) ex = -1;
-  __syncthreads();
-  return max(carry, ex);
-}
-
-template <int NW>
-__device__ __forceinline__ int block_excl_min_rev_n(int v, int* sh, int t, int identity) {
-  const int lane = t & (kWave - 1), wv = t / kWave;
-  int x = v;
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const int y = __shfl_down(x, off, kWave);
-    if (lane + off < kWave) x = min(x, y);
-  }
-  if (lane == 0) sh[wv] = x;
-  __syncthreads();
-  int carry = identity;
-  for (int w2 = wv + 1; w2 < NW; ++w2) carry = min(carry, sh[w2]);
-  int ex = __shfl_down(x, 1, kWave);
-  if (lane == kWave - 1) ex = identity;
-  __syncthreads();
-  return min(carry, ex);
-}
-
-__global__ __launch_bounds__(kFT) void ring_plan_fast(
-    const int64_t* __restrict__ src, const int64_t* __restrict__ dst,
-    const double* __restrict__ time, int n, int b, int64_t N, int B, int64_t* __restrict__ wp,
-    int64_t* __restrict__ dest, int32_t* status) {
-  // exchange arrays, padded by one entry per 32 (index p + p/32) so the
-  // blocked reads t*E + e spread over the LDS banks
-  __shared__ uint32_t xk[kFT * kFE + kFT * kFE / 32];
-  __shared__ uint16_t xv[kFT * kFE + kFT * kFE / 32];
-  __shared__ uint16_t offs[16 * kFT];
-  __shared__ uint64_t wsum[kFW * 4];
-  __shared__ int ish[kFW];
-  __shared__ double dsh[kFW];
-  const int t = threadIdx.x;
-  const int lane = t & (kWave - 1), wv = t / kWave;
-  const int E = (n + kFT - 1) / kFT;
-  const uint32_t kInvalid = static_cast<uint32_t>(N);
-  const uint32_t kPad = static_cast<uint32_t>(N) + 1u;
-
-  uint32_t k[kFE], v[kFE];
-  int bad = 0;
-#pragma unroll
-  for (int e = 0; e < kFE; ++e) {
-    const int p = t * E + e;
-    k[e] = kPad;
-    v[e] = static_cast<uint32_t>(p);
-    if (e < E && p < n) {
-      const int64_t u = p < b ? src[p] : dst[p - b];
-      if (u < 0 || u >= N) {
-        k[e] = kInvalid;
-        ++bad;
-      } else {
-        k[e] = static_cast<uint32_t>(u);
-      }
-    }
-  }
-  double mx = -__builtin_inf();
-  for (int i = t; i < b; i += kFT) mx = fmax(mx, time[i]);
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off >>= 1) {
-    bad += __shfl_xor(bad, off, kWave);
-    mx = fmax(mx, __shfl_xor(mx, off, kWave));
-  }
-  if (lane == 0) {
-    ish[wv] = bad;
-    dsh[wv] = mx;
-  }
-  __syncthreads();
-  if (t == 0 && status != nullptr) {
-    int tb = 0;
-    double tm = -__builtin_inf();
-    for (int w2 = 0; w2 < kFW; ++w2) {
-      tb += ish[w2];
-      tm = fmax(tm, dsh[w2]);
-    }
-    if (tb) atomicAdd(&status[TGX_ST_BAD_EVENT_NODE], tb);
-    if (!(trunc(tm) > static_cast<double>(n - 3))) atomicAdd(&status[TGX_ST_KEY_COLLISION], 1);
-  }
-  __syncthreads();
-
-  const int nbits = 32 - __clz(kPad);
-  for (int shift = 0; shift < nbits; shift += 4) {
-    // per-thread digit counts (8-bit fields: digits 0-7 in c0, 8-15 in c1)
-    uint64_t c0 = 0, c1 = 0;
-#pragma unroll
-    for (int e = 0; e < kFE; ++e) {
-      if (e < E) {
-        const uint32_t d = (k[e] >> shift) & 15u;
-        const uint64_t inc = uint64_t(1) << ((d & 7u) * 8u);
-        if (d < 8u) c0 += inc; else c1 += inc;
-      }
-    }
-    // counts as four u64 of 16-bit fields (digits 4j..4j+3)
-    uint64_t q[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint64_t c = j < 2 ? c0 : c1;
-      const int b0 = (j & 1) * 32;
-      q[j] = ((c >> b0) & 0xFFu) | (((c >> (b0 + 8)) & 0xFFu) << 16) |
-             (((c >> (b0 + 16)) & 0xFFu) << 32) | (((c >> (b0 + 24)) & 0xFFu) << 48);
-    }
-    uint64_t x[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      x[j] = q[j];
-#pragma unroll
-      for (int off = 1; off < kWave; off <<= 1) {
-        const uint64_t y = shfl_up_u64(x[j], off);
-        if (lane >= off) x[j] += y;
-      }
-    }
-    if (lane == kWave - 1) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) wsum[wv * 4 + j] = x[j];
-    }
-    __syncthreads();
-    uint64_t tot[4] = {0, 0, 0, 0};
-    for (int w2 = 0; w2 < kFW; ++w2) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint64_t s2 = wsum[w2 * 4 + j];
-        if (w2 < wv) x[j] += s2;
-        tot[j] += s2;
-      }
-    }
-    uint32_t run = 0;
-#pragma unroll
-    for (int d = 0; d < 16; ++d) {
-      const uint32_t ex = static_cast<uint32_t>(((x[d >> 2] - q[d >> 2]) >> ((d & 3) * 16)) & 0xFFFFu);
-      offs[d * kFT + t] = static_cast<uint16_t>(run + ex);
-      run += static_cast<uint32_t>((tot[d >> 2] >> ((d & 3) * 16)) & 0xFFFFu);
-    }
-    // scatter; in-thread ranks are recounted in the same order
-    c0 = 0;
-    c1 = 0;
-#pragma unroll
-    for (int e = 0; e < kFE; ++e) {
-      if (e < E) {
-        const uint32_t d = (k[e] >> shift) & 15u;
-        const uint32_t sh = (d & 7u) * 8u;
-        const uint64_t c = d < 8u ? c0 : c1;
-        const uint32_t rk = static_cast<uint32_t>((c >> sh) & 0xFFu);
-        const uint64_t cn = c + (uint64_t(1) << sh);
-        if (d < 8u) c0 = cn; else c1 = cn;
-        const uint32_t pos = static_cast<uint32_t>(offs[d * kFT + t]) + rk;
-        xk[pad32(pos)] = k[e];
-        xv[pad32(pos)] = static_cast<uint16_t>(v[e]);
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int e = 0; e < kFE; ++e) {
-      if (e < E) {
-        k[e] = xk[pad32(t * E + e)];
-        v[e] = xv[pad32(t * E + e)];
-      }
-    }
-    __syncthreads();
-  }
-
-  // ---- runs of equal keys over the sorted positions ----
-  const int L = kFT * E;
-  int last_head = -1, first_head = L;
-  uint32_t prevk = (t == 0) ? 0xFFFFFFFFu : xk[pad32(t * E - 1)];
-  uint32_t heads = 0;  // bit e: position t*E+e starts a run
-#pragma unroll
-  for (int e = 0; e < kFE; ++e) {
-    if (e < E) {
-      const int p = t * E + e;
-      if (p == 0 || k[e] != prevk) {
-        heads |= 1u << e;
-        last_head = p;
-        if (first_head == L) first_head = p;
-      }
-      prevk = k[e];
-    }
-  }
-  int start = block_excl_max_n<kFW>(last_head, ish, t);
-  const int next_after = block_excl_min_rev_n<kFW>(first_head, ish, t, L);
-  int st[kFE];
-#pragma unroll
-  for (int e = 0; e < kFE; ++e) {
-    if (e < E && ((heads >> e) & 1u)) start = t * E + e;
-    st[e] = start;
-  }
-  int run_end = next_after;
-#pragma unroll
-  for (int e = kFE - 1; e >= 0; --e) {
-    if (e < E) {
-      const int p = t * E + e;
-      const int c = run_end - st[e];
-      const int kept = min(c, B);
-      const int m = p - st[e];
-      if (static_cast<int>(v[e]) < n) {
-        int64_t dslot = -1;
-        if (k[e] < kInvalid && m >= c - kept) {
-          const int64_t slot = ring_slot(wp[k[e]], m - (c - kept), B);
-          dslot = static_cast<int64_t>(k[e]) * B + slot;
-        }
-        dest[v[e]] = dslot;
-      }
-      if ((heads >> e) & 1u) {
-        xv[pad32(p)] = static_cast<uint16_t>(kept);  // the sorted indices now live in registers
-        run_end = p;
-      }
-    }
-  }
-  __syncthreads();
-#pragma unroll
-  for (int e = 0; e < kFE; ++e) {
-    if (e < E && ((heads >> e) & 1u) && k[e] < kInvalid) wp[k[e]] += xv[pad32(t * E + e)];
-  }
-}
-
-__global__ __launch_bounds__(kPlanThreads) void ring_plan_global(
-    const int64_t* __restrict__ src, const int64_t* __restrict__ dst,
-    const double* __restrict__ time, int n, int b, int64_t N, int B, int64_t* __restrict__ wp,
-    int64_t* __restrict__ dest, uint32_t* gkeys, uint32_t* gpa, uint32_t* gpb,
-    int32_t* status) {
-  __shared__ uint32_t cnt[16 * kPlanThreads];
-  __shared__ uint32_t wsum[kPlanWaves * 16];
-  __shared__ int ish[kPlanWaves];
-  __shared__ double dsh[kPlanWaves];
-  plan_body<uint32_t, false>(src, dst, time, n, b, N, B, wp, dest, gkeys, gpa, gpb, cnt, wsum,
-                             ish, dsh, status);
+__device__ __forceinline__ void wave_sync_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 template <int VEC>
@@ -571,34 +70,294 @@ struct VecT<2> {
   using T = uint16_t;
 };
 
-template <int VEC>
-__global__ __launch_bounds__(256) void ring_write(
-    const int64_t* __restrict__ src, const int64_t* __restrict__ dst,
-    const double* __restrict__ time, const uint8_t* __restrict__ feat, int64_t b,
-    int64_t eid_base, int64_t row_bytes, const int64_t* __restrict__ dest,
-    int32_t* __restrict__ ids, double* __restrict__ times, uint8_t* __restrict__ feats,
-    int64_t* __restrict__ eids, int tpe_log2) {
-  using V = typename VecT<VEC>::T;
-  const int tpe = 1 << tpe_log2;
-  const int epb = 256 >> tpe_log2;
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * epb + (threadIdx.x >> tpe_log2);
-  const int l = threadIdx.x & (tpe - 1);
-  if (i >= 2 * b) return;
-  const int64_t slot = dest[i];
-  if (slot < 0) return;
-  const int64_t e = i < b ? i : i - b;
-  if (l == 0) {
-    ids[slot] = static_cast<int32_t>(i < b ? dst[e] : src[e]);
-    times[slot] = time[e];
-    if (eids != nullptr) eids[slot] = eid_base + e;
+struct AppendParams {
+  const int64_t* src;
+  const int64_t* dst;
+  const double* time;
+  const uint8_t* feat;  // [b, row_bytes] or null (zero rows)
+  int64_t b;
+  int64_t n;
+  int64_t N;
+  int B;
+  int64_t row_bytes;
+  int64_t eid_base;
+  int32_t* ids;
+  double* times;
+  uint8_t* feats;
+  int64_t* wp;
+  int64_t* eids;
+  int32_t* cnt;     // [N] per-node counters (zero between calls)
+  int32_t* nbase;   // [N] list base of multi-entry nodes
+  int32_t* ctl;     // [16] cursor, group count, time flag
+  int32_t* ticket;  // [n]
+  int32_t* list;    // [n]
+  int32_t* groups;  // [n/2 + 1] small groups
+  int32_t* large;   // [n/65 + 1] large groups
+  int32_t* status;
+  int tpe_log2;     // lanes per entry (singleton copy)
+  int ga;           // blocks of the singleton role in commit
+  int gb;           // blocks of the small-group role
+};
+
+// ---- 1. count -------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void append_count(AppendParams P) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  const int lane = threadIdx.x & (kWave - 1);
+  if (i == 0) {
+    P.ctl[kCtlCursor] = 0;
+    P.ctl[kCtlGroups] = 0;
+    P.ctl[kCtlLarge] = 0;
   }
-  const int64_t nv = row_bytes / VEC;
-  V* drow = reinterpret_cast<V*>(feats + slot * row_bytes);
-  if (feat != nullptr) {
-    const V* srow = reinterpret_cast<const V*>(feat + e * row_bytes);
-    for (int64_t c = l; c < nv; c += tpe) drow[c] = srow[c];
-  } else {
-    for (int64_t c = l; c < nv; c += tpe) drow[c] = V{};
+  int bad = 0;
+  bool time_ok = false;
+  int32_t u = -1;
+  if (i < P.n) {
+    const int64_t uu = entry_node(P.src, P.dst, i, P.b);
+    if (uu < 0 || uu >= P.N)
+      bad = 1;
+    else
+      u = static_cast<int32_t>(uu);
+    // reference key from*(int(max t)+2)+i is lexicographic iff int(max t)+2 > n-1
+    if (i < P.b) time_ok = trunc(P.time[i]) > static_cast<double>(P.n - 3);
+  }
+  // match equal nodes inside the wavefront: one atomic per distinct node
+  const uint64_t active = __ballot(u >= 0);
+  uint64_t todo = active;
+  uint64_t peers = 0;
+  while (todo) {
+    const int j = __ffsll(static_cast<unsigned long long>(todo)) - 1;
+    const int32_t uj = __shfl(u, j, kWave);
+    const uint64_t m = __ballot(u == uj) & active;
+    if ((m >> lane) & 1) peers = m;
+    todo &= ~m;
+  }
+  if (u >= 0) {
+    const int leader = __ffsll(static_cast<unsigned long long>(peers)) - 1;
+    const int rank = __popcll(peers & ((uint64_t(1) << lane) - 1));
+    int base = 0;
+    if (lane == leader) base = atomicAdd(&P.cnt[u], __popcll(peers));
+    // leader lanes publish their base; every lane reads its leader's
+    base = __shfl(base, leader, kWave);
+    P.ticket[i] = base + rank;
+  } else if (i < P.n) {
+    P.ticket[i] = -1;
+  }
+  const uint64_t bm = __ballot(bad);
+  const uint64_t tm = __ballot(time_ok);
+  if (lane == 0) {
+    if (bm && P.status != nullptr) atomicAdd(&P.status[TGX_ST_BAD_EVENT_NODE], __popcll(bm));
+    if (tm) atomicOr(&P.ctl[kCtlTimeOk], 1);
+  }
+}
+
+// ---- 2. groups --------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void append_groups(AppendParams P) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  const int lane = threadIdx.x & (kWave - 1);
+  if (i == 0) {
+    if (P.ctl[kCtlTimeOk] == 0 && P.status != nullptr)
+      atomicAdd(&P.status[TGX_ST_KEY_COLLISION], 1);
+    P.ctl[kCtlTimeOk] = 0;
+  }
+  int64_t u = -1;
+  int c = 0;
+  if (i < P.n && P.ticket[i] == 0) {
+    u = entry_node(P.src, P.dst, i, P.b);
+    c = P.cnt[u];
+  }
+  const bool grp = c > 1;
+  const bool big = c > kWave;
+  // wave-aggregated reservation of group ids and list space
+  const uint64_t sm = __ballot(grp && !big);
+  const uint64_t lm = __ballot(big);
+  const int sum = grp ? c : 0;
+  int incl = sum;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int y = __shfl_up(incl, off, kWave);
+    if (lane >= off) incl += y;
+  }
+  const int total = __shfl(incl, kWave - 1, kWave);
+  int sbase = 0, lgbase = 0, lbase = 0;
+  if ((sm | lm) != 0) {
+    if (lane == 0) {
+      if (sm) sbase = atomicAdd(&P.ctl[kCtlGroups], __popcll(sm));
+      if (lm) lgbase = atomicAdd(&P.ctl[kCtlLarge], __popcll(lm));
+      lbase = atomicAdd(&P.ctl[kCtlCursor], total);
+    }
+    sbase = __shfl(sbase, 0, kWave);
+    lgbase = __shfl(lgbase, 0, kWave);
+    lbase = __shfl(lbase, 0, kWave);
+  }
+  const uint64_t below = (uint64_t(1) << lane) - 1;
+  if (grp && !big) P.groups[sbase + __popcll(sm & below)] = static_cast<int32_t>(u);
+  if (big) P.large[lgbase + __popcll(lm & below)] = static_cast<int32_t>(u);
+  if (grp) P.nbase[u] = lbase + incl - sum;
+}
+
+// ---- 3. fill ----------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void append_fill(AppendParams P) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= P.n) return;
+  const int t = P.ticket[i];
+  if (t < 0) return;
+  const int64_t u = entry_node(P.src, P.dst, i, P.b);
+  if (P.cnt[u] > 1) P.list[P.nbase[u] + t] = static_cast<int32_t>(i);
+}
+
+// write id / time / edge id of entry i into ring slot `slot` (global index)
+__device__ __forceinline__ void write_entry_meta(const AppendParams& P, int64_t i, int64_t slot) {
+  const int64_t e = i < P.b ? i : i - P.b;
+  P.ids[slot] = static_cast<int32_t>(i < P.b ? P.dst[e] : P.src[e]);
+  P.times[slot] = P.time[e];
+  if (P.eids != nullptr) P.eids[slot] = P.eid_base + e;
+}
+
+// copy the kept rows R[0..kept) of node u (row r -> slot (w + kept - 1 - r) % B);
+// threads t = first, first + stride, ... of the caller share the work
+template <int VEC>
+__device__ __forceinline__ void write_kept(const AppendParams& P, const int32_t* R, int64_t u,
+                                           int kept, int64_t w, int first, int stride) {
+  using V = typename VecT<VEC>::T;
+  const int nv = static_cast<int>(P.row_bytes / VEC);
+  for (int r = first; r < kept; r += stride)
+    write_entry_meta(P, R[r], u * P.B + ring_slot(w, kept - 1 - r, P.B));
+  const int total = kept * nv;
+  for (int f = first; f < total; f += stride) {
+    const int r = f / nv;
+    const int cch = f - r * nv;
+    const int64_t i = R[r];
+    const int64_t e = i < P.b ? i : i - P.b;
+    const int64_t slot = u * P.B + ring_slot(w, kept - 1 - r, P.B);
+    V* drow = reinterpret_cast<V*>(P.feats + slot * P.row_bytes);
+    drow[cch] = P.feat != nullptr ? reinterpret_cast<const V*>(P.feat + e * P.row_bytes)[cch] : V{};
+  }
+}
+
+// ---- 4. commit --------------------------------------------------------------
+// blocks [0, ga): singletons; [ga, ga+gb): small groups, one per wavefront;
+// [ga+gb, ...): large groups, one per workgroup
+template <int VEC>
+__global__ __launch_bounds__(kThreads) void append_commit(AppendParams P) {
+  using V = typename VecT<VEC>::T;
+  __shared__ uint32_t bitmap[kWinWords];
+  __shared__ int32_t sfx[kWinWords];                     // set bits in later words
+  __shared__ int32_t rows[kCommitWaves][TGX_MAX_SLOTS];  // kept entry index by e
+  __shared__ int32_t wsum[kCommitWaves];
+  const int nv = static_cast<int>(P.row_bytes / VEC);
+  const int blk = static_cast<int>(blockIdx.x);
+
+  if (blk < P.ga) {
+    // singletons: tpe lanes per entry
+    const int tpe = 1 << P.tpe_log2;
+    const int epb = kThreads >> P.tpe_log2;
+    const int64_t i = static_cast<int64_t>(blk) * epb + (threadIdx.x >> P.tpe_log2);
+    const int l = threadIdx.x & (tpe - 1);
+    if (i >= P.n) return;
+    if (P.ticket[i] != 0) return;
+    const int64_t u = entry_node(P.src, P.dst, i, P.b);
+    if (P.cnt[u] != 1) return;
+    const int64_t w = P.wp[u];
+    const int64_t slot = u * P.B + ring_slot(w, 0, P.B);
+    const int64_t e = i < P.b ? i : i - P.b;
+    V* drow = reinterpret_cast<V*>(P.feats + slot * P.row_bytes);
+    if (P.feat != nullptr) {
+      const V* srow = reinterpret_cast<const V*>(P.feat + e * P.row_bytes);
+      for (int c = l; c < nv; c += tpe) drow[c] = srow[c];
+    } else {
+      for (int c = l; c < nv; c += tpe) drow[c] = V{};
+    }
+    if (l == 0) {
+      write_entry_meta(P, i, slot);
+      P.wp[u] = w + 1;
+      P.cnt[u] = 0;
+    }
+    return;
+  }
+
+  const int wv = threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  if (blk < P.ga + P.gb) {
+    // small group (2 <= c <= 64): ranks by comparing list entries in registers
+    const int64_t gid = static_cast<int64_t>(blk - P.ga) * kCommitWaves + wv;
+    if (gid >= P.ctl[kCtlGroups]) return;  // wave-uniform
+    const int64_t u = P.groups[gid];
+    const int c = P.cnt[u];
+    const int base = P.nbase[u];
+    const int kept = c < P.B ? c : P.B;
+    int32_t* R = rows[wv];
+    const int32_t idx = lane < c ? P.list[base + lane] : -1;
+    int e = 0;
+    for (int j = 0; j < c; ++j) e += __shfl(idx, j, kWave) > idx;
+    if (lane < c && e < kept) R[e] = idx;
+    wave_sync_lds();
+    const int64_t w = P.wp[u];
+    write_kept<VEC>(P, R, u, kept, w, lane, kWave);
+    if (lane == 0) {
+      P.wp[u] = w + kept;
+      P.cnt[u] = 0;
+    }
+    return;
+  }
+
+  // large group (c > 64): the workgroup ranks the list over bitmap windows of
+  // kWinBits entry indices, from the top of the batch down, until `kept`
+  // entries are found
+  const int64_t gid = blk - P.ga - P.gb;
+  if (gid >= P.ctl[kCtlLarge]) return;  // workgroup-uniform
+  const int t = threadIdx.x;
+  const int64_t u = P.large[gid];
+  const int c = P.cnt[u];
+  const int base = P.nbase[u];
+  const int kept = c < P.B ? c : P.B;
+  int32_t* R = rows[0];
+  int64_t hi = P.n;
+  int carry = 0;
+  while (carry < kept && hi > 0) {  // uniform across the workgroup
+    const int64_t lo = hi > kWinBits ? hi - kWinBits : 0;
+    for (int q = t; q < kWinWords; q += kThreads) bitmap[q] = 0u;
+    __syncthreads();
+    for (int j = t; j < c; j += kThreads) {
+      const int64_t x = P.list[base + j];
+      if (x >= lo && x < hi) atomicOr(&bitmap[(x - lo) >> 5], 1u << ((x - lo) & 31));
+    }
+    __syncthreads();
+    // exclusive suffix over words: thread t owns word t (kWinWords == kThreads)
+    const int own = __popc(bitmap[t]);
+    int suf = own;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const int y = __shfl_down(suf, off, kWave);
+      if (lane + off < kWave) suf += y;
+    }
+    if (lane == 0) wsum[wv] = suf;
+    __syncthreads();
+    int later = 0, win_total = 0;
+    for (int w2 = 0; w2 < kCommitWaves; ++w2) {
+      if (w2 > wv) later += wsum[w2];
+      win_total += wsum[w2];
+    }
+    sfx[t] = later + suf - own;
+    __syncthreads();
+    for (int j = t; j < c; j += kThreads) {
+      const int64_t x = P.list[base + j];
+      if (x >= lo && x < hi) {
+        const int rel = static_cast<int>(x - lo);
+        const int word = rel >> 5;
+        const int e = carry + (__popc(bitmap[word] >> (rel & 31)) - 1) + sfx[word];
+        if (e < kept) R[e] = static_cast<int32_t>(x);
+      }
+    }
+    carry += win_total;
+    hi = lo;
+    __syncthreads();
+  }
+  const int64_t w = P.wp[u];
+  write_kept<VEC>(P, R, u, kept, w, t, kThreads);
+  __syncthreads();
+  if (t == 0) {
+    P.wp[u] = w + kept;
+    P.cnt[u] = 0;
   }
 }
 
@@ -611,10 +370,13 @@ using namespace tgx;
 
 extern "C" size_t tgx_ring_append_workspace_size(int64_t b) {
   if (b <= 0) return 256;
-  const int64_t n = 2 * b;
-  size_t bytes = align256(static_cast<size_t>(n) * sizeof(int64_t));
-  if (n > kLdsMaxEntries) bytes += 3 * align256(static_cast<size_t>(n) * sizeof(uint32_t));
-  return bytes;
+  const size_t n = static_cast<size_t>(2 * b);
+  return 2 * align256(n * 4) + align256((n / 2 + 1) * 4) + align256((n / 65 + 1) * 4);
+}
+
+extern "C" size_t tgx_ring_scratch_size(int64_t num_nodes) {
+  if (num_nodes < 0) return 0;
+  return static_cast<size_t>(2 * num_nodes + 16) * sizeof(int32_t);
 }
 
 extern "C" int tgx_ring_append(const tgx_ring* ring, const int64_t* src, const int64_t* dst,
@@ -628,15 +390,17 @@ extern "C" int tgx_ring_append(const tgx_ring* ring, const int64_t* src, const i
   if (src == nullptr || dst == nullptr || time == nullptr)
     return fail(TGX_ERR_ARG, "tgx_ring_append: src/dst/time must not be NULL");
   if (ring->ids == nullptr || ring->times == nullptr || ring->write_pos == nullptr ||
-      (ring->feats == nullptr && ring->feat_dim > 0))
-    return fail(TGX_ERR_ARG, "tgx_ring_append: ring arrays must not be NULL");
+      ring->scratch == nullptr || (ring->feats == nullptr && ring->feat_dim > 0))
+    return fail(TGX_ERR_ARG,
+                "tgx_ring_append: ring arrays (ids, times, feats, write_pos, scratch) must not be NULL");
   const int esz = feat_elem_bytes(ring->feat_dtype);
   if (esz == 0) return fail(TGX_ERR_DTYPE, "tgx_ring_append: unsupported feat dtype %d", ring->feat_dtype);
   if (ring->num_nodes <= 0 || ring->num_nodes >= (int64_t(1) << 31))
     return fail(TGX_ERR_LIMIT, "tgx_ring_append: num_nodes %lld outside [1, 2^31)",
                 (long long)ring->num_nodes);
-  if (ring->slots <= 0 || ring->slots > (1 << 15))
-    return fail(TGX_ERR_LIMIT, "tgx_ring_append: slots %d outside [1, 32768]", ring->slots);
+  if (ring->slots < 1 || ring->slots > TGX_MAX_SLOTS)
+    return fail(TGX_ERR_LIMIT, "tgx_ring_append: slots %d outside [1, %d]", ring->slots,
+                TGX_MAX_SLOTS);
   if (ring->feat_dim < 0) return fail(TGX_ERR_ARG, "tgx_ring_append: negative feat_dim");
   const int64_t n = 2 * b;
   if (n >= (int64_t(1) << 30)) return fail(TGX_ERR_LIMIT, "tgx_ring_append: batch too large");
@@ -644,54 +408,68 @@ extern "C" int tgx_ring_append(const tgx_ring* ring, const int64_t* src, const i
   if (workspace == nullptr || workspace_bytes < need)
     return fail(TGX_ERR_ARG, "tgx_ring_append: workspace of %zu bytes needed, got %zu", need,
                 workspace_bytes);
+
+  AppendParams P{};
+  P.src = src;
+  P.dst = dst;
+  P.time = time;
+  P.feat = static_cast<const uint8_t*>(feat);
+  P.b = b;
+  P.n = n;
+  P.N = ring->num_nodes;
+  P.B = ring->slots;
+  P.row_bytes = static_cast<int64_t>(ring->feat_dim) * esz;
+  P.eid_base = eid_base;
+  P.ids = ring->ids;
+  P.times = ring->times;
+  P.feats = static_cast<uint8_t*>(ring->feats);
+  P.wp = ring->write_pos;
+  P.eids = ring->eids;
+  P.cnt = ring->scratch;
+  P.nbase = ring->scratch + ring->num_nodes;
+  P.ctl = ring->scratch + 2 * ring->num_nodes;
   uint8_t* ws = static_cast<uint8_t*>(workspace);
-  int64_t* dest = reinterpret_cast<int64_t*>(ws);
+  P.ticket = reinterpret_cast<int32_t*>(ws);
+  P.list = reinterpret_cast<int32_t*>(ws + align256(static_cast<size_t>(n) * 4));
+  P.groups = reinterpret_cast<int32_t*>(ws + 2 * align256(static_cast<size_t>(n) * 4));
+  P.large = reinterpret_cast<int32_t*>(ws + 2 * align256(static_cast<size_t>(n) * 4) +
+                                       align256(static_cast<size_t>(n / 2 + 1) * 4));
+  P.status = status;
 
-  if (n <= kLdsMaxEntries) {
-    hipLaunchKernelGGL(ring_plan_fast, dim3(1), dim3(kFT), 0, stream, src, dst, time,
-                       static_cast<int>(n), static_cast<int>(b), ring->num_nodes, ring->slots,
-                       ring->write_pos, dest, status);
-  } else {
-    uint8_t* p = ws + align256(static_cast<size_t>(n) * sizeof(int64_t));
-    uint32_t* gkeys = reinterpret_cast<uint32_t*>(p);
-    p += align256(static_cast<size_t>(n) * 4);
-    uint32_t* gpa = reinterpret_cast<uint32_t*>(p);
-    p += align256(static_cast<size_t>(n) * 4);
-    uint32_t* gpb = reinterpret_cast<uint32_t*>(p);
-    hipLaunchKernelGGL(ring_plan_global, dim3(1), dim3(kPlanThreads), 0, stream, src, dst, time,
-                       static_cast<int>(n), static_cast<int>(b), ring->num_nodes, ring->slots,
-                       ring->write_pos, dest, gkeys, gpa, gpb, status);
-  }
-  int rc = check_launch("ring_plan");
-  if (rc) return rc;
-
-  const int64_t row_bytes = static_cast<int64_t>(ring->feat_dim) * esz;
   int vec = 2;
-  if (row_bytes % 16 == 0 && aligned16(ring->feats) && (feat == nullptr || aligned16(feat)))
+  if (P.row_bytes % 16 == 0 && aligned16(ring->feats) && (feat == nullptr || aligned16(feat)))
     vec = 16;
-  else if (row_bytes % 4 == 0 && (reinterpret_cast<uintptr_t>(ring->feats) & 3u) == 0 &&
+  else if (P.row_bytes % 4 == 0 && (reinterpret_cast<uintptr_t>(ring->feats) & 3u) == 0 &&
            (feat == nullptr || (reinterpret_cast<uintptr_t>(feat) & 3u) == 0))
     vec = 4;
-  const int64_t nchunks = row_bytes / vec;
+  const int64_t nchunks = P.row_bytes / vec;
   int tpe_log2 = 0;
   while ((int64_t(1) << tpe_log2) < nchunks && tpe_log2 < 6) ++tpe_log2;
-  const int epb = 256 >> tpe_log2;
-  const int64_t grid = (n + epb - 1) / epb;
-  const uint8_t* fb = static_cast<const uint8_t*>(feat);
-  uint8_t* rf = static_cast<uint8_t*>(ring->feats);
+  P.tpe_log2 = tpe_log2;
+  const int64_t epb = kThreads >> tpe_log2;
+  P.ga = static_cast<int>((n + epb - 1) / epb);
+  P.gb = static_cast<int>((n / 2 + kCommitWaves) / kCommitWaves);  // at most n/2 groups
+  const int64_t gc = n / (kWave + 1) + 1;                              // at most n/65 large
+  const dim3 grid1(static_cast<unsigned>((n + kThreads - 1) / kThreads));
+  const dim3 grid4(static_cast<unsigned>(P.ga + P.gb + gc));
+
+  hipLaunchKernelGGL(append_count, grid1, dim3(kThreads), 0, stream, P);
+  int rc = check_launch("append_count");
+  if (rc) return rc;
+  hipLaunchKernelGGL(append_groups, grid1, dim3(kThreads), 0, stream, P);
+  if ((rc = check_launch("append_groups"))) return rc;
+  hipLaunchKernelGGL(append_fill, grid1, dim3(kThreads), 0, stream, P);
+  if ((rc = check_launch("append_fill"))) return rc;
   switch (vec) {
     case 16:
-      hipLaunchKernelGGL(ring_write<16>, dim3(grid), dim3(256), 0, stream, src, dst, time, fb, b,
-                         eid_base, row_bytes, dest, ring->ids, ring->times, rf, ring->eids, tpe_log2);
+      hipLaunchKernelGGL(append_commit<16>, grid4, dim3(kThreads), 0, stream, P);
       break;
     case 4:
-      hipLaunchKernelGGL(ring_write<4>, dim3(grid), dim3(256), 0, stream, src, dst, time, fb, b,
-                         eid_base, row_bytes, dest, ring->ids, ring->times, rf, ring->eids, tpe_log2);
+      hipLaunchKernelGGL(append_commit<4>, grid4, dim3(kThreads), 0, stream, P);
       break;
     default:
-      hipLaunchKernelGGL(ring_write<2>, dim3(grid), dim3(256), 0, stream, src, dst, time, fb, b,
-                         eid_base, row_bytes, dest, ring->ids, ring->times, rf, ring->eids, tpe_log2);
+      hipLaunchKernelGGL(append_commit<2>, grid4, dim3(kThreads), 0, stream, P);
       break;
   }
-  return check_launch("ring_write");
+  return check_launch("append_commit");
 }

@@ -103,6 +103,8 @@ class DataPipeline:
             names.append("neg_src"); qgroups.append((raw_batch.neg_src, raw_batch.time, 1))
             sizes.append(b); per_event.append(1)
 
+        if spec.edge_ids and not self.graph.track_edge_ids:
+            raise ValueError("GatherSpec.edge_ids needs a TemporalGraph built with track_edge_ids=True")
         want_co = spec.co_occurrence and "src" in names and "dst" in names
         co_mode = _CO_MODES[spec.co_occurrence_mode] if want_co else _lib.TGX_CO_NONE
         d_t = int(spec.time_encoding)
