@@ -42,24 +42,28 @@ def bytes_per_batch(cfg, Q: int, V: int, pairs: int, d_t: int = 100) -> int:
 
 
 class EventTimer:
-    """HIP events around every tgx_recent launch, recorded on the launching stream."""
+    """Pairs of HIP events handed to tgx_recent, which has the kernel dispatch
+    itself record its start and end on them (hipExtLaunchKernelGGL)."""
 
-    def __init__(self, torch):
+    def __init__(self, torch, n):
         self.torch = torch
         self.pairs = []
+        self.free = []
+        for _ in range(n):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            e1.record()  # materialise the hipEvent_t handles
+            self.free.append((e0, e1))
+        torch.cuda.synchronize()
         self.active = False
 
-    def before(self):
-        if self.active:
-            e = self.torch.cuda.Event(enable_timing=True)
-            e.record()
-            self.pairs.append([e, None])
-
-    def after(self):
-        if self.active:
-            e = self.torch.cuda.Event(enable_timing=True)
-            e.record()
-            self.pairs[-1][1] = e
+    def events(self):
+        if not self.active or not self.free:
+            return 0, 0
+        e0, e1 = self.free.pop()
+        self.pairs.append((e0, e1))
+        return e0.cuda_event, e1.cuda_event
 
     def total_ms(self):
         return sum(a.elapsed_time(b) for a, b in self.pairs)
@@ -141,6 +145,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=1400)
     ap.add_argument("--config", default="c3")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--queries-per-workgroup", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quiet", action="store_true")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -172,6 +177,7 @@ def main():
 
     g = stream_check.make_graph(cfg)
     pipe = stream_check.make_pipeline(cfg, g)
+    pipe.queries_per_workgroup = a.queries_per_workgroup
     from tgengine_amd import RawBatch
     offs = np.concatenate([[0], np.cumsum(lens)])
     n_neg = cfg.n_neg
@@ -183,7 +189,7 @@ def main():
                         edge_feat=dev["feat"][s:e], neg=neg)
 
     raws = [raw(i) for i in range(total)]
-    timer = EventTimer(torch)
+    timer = EventTimer(torch, K)
     g.kernel_timer = timer
     for i in range(W):
         pipe.prepare(raws[i])
@@ -193,12 +199,17 @@ def main():
 
     masks = []
     timer.active = True
+    host_prep = host_adv = 0.0
     torch.cuda.synchronize()
     t_start = time.perf_counter()
     for i in range(W, total):
+        h0 = time.perf_counter()
         pb = pipe.prepare(raws[i])
+        h1 = time.perf_counter()
         masks.append((pb.src_neighbors.mask, pb.dst_neighbors.mask, pb.neg_neighbors.mask))
         g.advance(raws[i].src, raws[i].dst, raws[i].time, raws[i].edge_feat)
+        host_adv += time.perf_counter() - h1
+        host_prep += h1 - h0
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_start
     timer.active = False
@@ -249,6 +260,7 @@ def main():
                                f"{cfg.queries_per_event} queries/event, d_t=100"
                                + (", co-occurrence" if cfg.co_occurrence else ""),
                    "batches_timed": f"{W}..{total - 1}", "events_per_batch": cfg.batch},
+        "host_us_per_step": {"prepare": host_prep / K * 1e6, "advance": host_adv / K * 1e6},
         "prepare_kernel": {"queries_per_s": total_q / (kern_ms / 1e3), "us_per_launch":
                            avg_launch_s * 1e6, "mean_valid_per_query": sum(Vs) / total_q,
                            "bytes_per_launch": sum(byts) / n_launch},

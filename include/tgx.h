@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define TGX_ABI_VERSION 3
+#define TGX_ABI_VERSION 4
 
 /* status codes */
 #define TGX_OK 0
@@ -147,6 +147,10 @@ typedef struct tgx_recent_args {
   int32_t* status;         /* [TGX_STATUS_WORDS] or NULL */
   int32_t num_query_groups;                          /* 0 = use nodes/times */
   tgx_query_group query_groups[TGX_MAX_QUERY_GROUPS];
+  /* optional hipEvent_t pair recorded by the kernel dispatch itself (start and
+   * end of the kernel's execution); both NULL = plain launch */
+  void* timing_start;
+  void* timing_stop;
 } tgx_recent_args;
 
 #define TGX_MAX_SLOTS 64

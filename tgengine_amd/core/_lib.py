@@ -60,7 +60,8 @@ class TgxRecentArgs(ctypes.Structure):
                 ("d_t", c_i32), ("te_w", c_vp), ("te_b", c_vp), ("dt_mode", c_i32), ("out_te", c_vp),
                 ("co_mode", c_i32), ("co_a", c_vp), ("co_c", c_vp), ("co_pair", c_vp),
                 ("status", c_vp), ("num_query_groups", c_i32),
-                ("query_groups", TgxQueryGroup * TGX_MAX_QUERY_GROUPS)]
+                ("query_groups", TgxQueryGroup * TGX_MAX_QUERY_GROUPS),
+                ("timing_start", c_vp), ("timing_stop", c_vp)]
 
 
 # every symbol include/tgx.h declares, with its ctypes signature
@@ -101,7 +102,7 @@ def lib() -> ctypes.CDLL:
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
-        if handle.tgx_abi_version() != 3:
+        if handle.tgx_abi_version() != 4:
             raise RuntimeError("libtgx ABI version mismatch")
         _lib = handle
         return _lib

@@ -21,6 +21,7 @@ Extensions (keyword-only, defaults match the reference):
 from __future__ import annotations
 
 import ctypes
+import threading
 from dataclasses import dataclass
 from typing import Optional
 
@@ -46,8 +47,35 @@ class Snapshot:
     overflow_eids: Optional[Tensor] = None
 
 
+try:
+    _raw_stream = torch._C._cuda_getCurrentRawStream  # (device_index) -> hipStream_t as int
+except AttributeError:  # pragma: no cover - older torch
+    _raw_stream = None
+
+
 def _stream_handle(device: torch.device) -> int:
+    """hipStream_t of the caller's current stream on ``device``."""
+    if _raw_stream is not None:
+        return _raw_stream(device.index)
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def _as(t: Tensor, dtype: torch.dtype, device: torch.device) -> Tensor:
+    """``t`` as a contiguous ``dtype`` tensor on ``device`` (no copy when it already is)."""
+    if t.dtype == dtype and t.device == device and t.is_contiguous():
+        return t
+    return t.to(device, dtype).contiguous()
+
+
+_tls = threading.local()
+
+
+def _recent_args() -> "_lib.TgxRecentArgs":
+    """A per-thread argument block for tgx_recent, reused across calls."""
+    a = getattr(_tls, "recent_args", None)
+    if a is None:
+        a = _tls.recent_args = _lib.TgxRecentArgs()
+    return a
 
 
 class TemporalGraph:
@@ -100,8 +128,9 @@ class TemporalGraph:
         self._ws: Optional[Tensor] = None
         self._ring_struct: Optional[_lib.TgxRing] = None
         self._csr_struct: Optional[_lib.TgxCsr] = None
-        # optional object with before()/after(), called around each tgx_recent launch
-        # on the launching thread (used to bracket the kernel with HIP events)
+        # optional object whose events() returns a (start, stop) pair of raw
+        # hipEvent_t handles (or (0, 0)); each tgx_recent launch records the
+        # kernel's own start and end on them
         self.kernel_timer = None
 
     # ------------------------------------------------------------------ ring
@@ -156,7 +185,7 @@ class TemporalGraph:
             else:
                 raise RuntimeError("Index put requires the source and destination dtypes match, "
                                    f"got {self.feat_dtype} for the ring and {edge_feat.dtype} for edge_feat")
-        return edge_feat.to(self.device).contiguous()
+        return _as(edge_feat, self.feat_dtype, self.device)
 
     def _workspace(self, nbytes: int) -> Tensor:
         if self._ws is None or self._ws.numel() < nbytes:
@@ -182,9 +211,9 @@ class TemporalGraph:
 
     def _append_ring(self, src, dst, time, edge_feat, b: int) -> None:
         dev = self.device
-        src = src.to(dev, torch.int64).contiguous()
-        dst = dst.to(dev, torch.int64).contiguous()
-        time = time.to(dev, torch.float64).contiguous()
+        src = _as(src, torch.int64, dev)
+        dst = _as(dst, torch.int64, dev)
+        time = _as(time, torch.float64, dev)
         feat = self._feat_in(edge_feat, b)
         L = _lib.lib()
         need = int(L.tgx_ring_append_workspace_size(b))
@@ -265,8 +294,8 @@ class TemporalGraph:
                 raise ValueError(f"at most {_lib.TGX_MAX_QUERY_GROUPS} query groups")
             Q = 0
             for (gn, gt, per) in groups:
-                gn = gn.reshape(-1).to(dev, torch.int64).contiguous()
-                gt = gt.reshape(-1).to(dev, torch.float64).contiguous()
+                gn = _as(gn.reshape(-1), torch.int64, dev)
+                gt = _as(gt.reshape(-1), torch.float64, dev)
                 if gn.shape[0] != gt.shape[0] * per:
                     raise ValueError("query group node/time sizes do not match")
                 qgroups.append((gn, gt, per))
@@ -275,8 +304,8 @@ class TemporalGraph:
             Q = int(nodes.shape[0])
             if times.shape[0] != Q:
                 raise ValueError("nodes and times must have the same length")
-            nodes = nodes.to(dev, torch.int64).contiguous()
-            times = times.to(dev, torch.float64).contiguous()
+            nodes = _as(nodes, torch.int64, dev)
+            times = _as(times, torch.float64, dev)
         out = {
             "ids": torch.empty((Q, k), dtype=torch.int32, device=dev),
             "times": torch.empty((Q, k), dtype=torch.float64, device=dev),
@@ -294,32 +323,44 @@ class TemporalGraph:
             out["co_a"] = torch.empty((num_groups, L, 2), dtype=torch.int32, device=dev)
             out["co_c"] = torch.empty((num_groups, L, 2), dtype=torch.int32, device=dev)
             out["co_pair"] = torch.empty((num_groups,), dtype=torch.float32, device=dev)
-        args = _lib.TgxRecentArgs(
-            nodes=nodes.data_ptr() if (Q and not qgroups) else 0,
-            times=times.data_ptr() if (Q and not qgroups) else 0, num_queries=Q,
-            k=k, plan=_lib.ptr(plan), group=group, num_groups=num_groups,
-            out_ids=out["ids"].data_ptr(), out_times=out["times"].data_ptr(),
-            out_feats=out["feats"].data_ptr(), out_mask=out["mask"].data_ptr(),
-            out_eids=_lib.ptr(out.get("eids")),
-            d_t=d_t, te_w=_lib.ptr(te_w), te_b=_lib.ptr(te_b), dt_mode=dt_mode,
-            out_te=_lib.ptr(out.get("te")), co_mode=co_mode, co_a=_lib.ptr(out.get("co_a")),
-            co_c=_lib.ptr(out.get("co_c")), co_pair=_lib.ptr(out.get("co_pair")),
-            status=self._status.data_ptr(), num_query_groups=len(qgroups))
+        args = _recent_args()
+        args.nodes = nodes.data_ptr() if (Q and not qgroups) else 0
+        args.times = times.data_ptr() if (Q and not qgroups) else 0
+        args.num_queries = Q
+        args.k = k
+        args.plan = _lib.ptr(plan)
+        args.group = group
+        args.num_groups = num_groups
+        args.out_ids = out["ids"].data_ptr()
+        args.out_times = out["times"].data_ptr()
+        args.out_feats = out["feats"].data_ptr()
+        args.out_mask = out["mask"].data_ptr()
+        args.out_eids = _lib.ptr(out.get("eids"))
+        args.d_t = d_t
+        args.te_w = _lib.ptr(te_w)
+        args.te_b = _lib.ptr(te_b)
+        args.dt_mode = dt_mode
+        args.out_te = _lib.ptr(out.get("te"))
+        args.co_mode = co_mode
+        args.co_a = _lib.ptr(out.get("co_a"))
+        args.co_c = _lib.ptr(out.get("co_c"))
+        args.co_pair = _lib.ptr(out.get("co_pair"))
+        args.status = self._status.data_ptr()
+        args.num_query_groups = len(qgroups)
         for i, (gn, gt, per) in enumerate(qgroups):
             qg = args.query_groups[i]
             qg.nodes, qg.times, qg.count, qg.times_per = gn.data_ptr(), gt.data_ptr(), gn.shape[0], per
+        args.timing_start = args.timing_stop = 0
         if Q > 0:
             ring = self._ring()
             csr = self._csr()
             L_ = _lib.lib()
             timer = self.kernel_timer
             if timer is not None:
-                timer.before()
+                args.timing_start, args.timing_stop = timer.events()
             rc = L_.tgx_recent(ctypes.byref(ring) if ring is not None else None,
                                ctypes.byref(csr) if csr is not None else None,
                                ctypes.byref(args), _stream_handle(dev))
-            if timer is not None:
-                timer.after()
             _lib.check(rc, "tgx_recent")
         out["mask"] = out["mask"].view(torch.bool)
         return out

@@ -24,6 +24,7 @@
 // (float4 stores, cosine evaluated in float64 from the exact fp32 argument).
 // A workgroup holds `group` queries so a (src, dst) pair meets in one LDS.
 #include "tgx_internal.h"
+#include <hip/hip_ext.h>
 #include "tgx_cos.h"
 
 namespace tgx {
@@ -646,15 +647,19 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
     (void)hipGetLastError();
     attr_done = true;
   }
+  hipEvent_t ev0 = static_cast<hipEvent_t>(a->timing_start);
+  hipEvent_t ev1 = static_cast<hipEvent_t>(a->timing_stop);
+  if ((ev0 == nullptr) != (ev1 == nullptr))
+    return fail(TGX_ERR_ARG, "tgx_recent: timing_start and timing_stop must both be set or both NULL");
   switch (vec) {
     case 16:
-      hipLaunchKernelGGL(recent_fused<16>, grid, block, lds, stream, P);
+      hipExtLaunchKernelGGL(recent_fused<16>, grid, block, lds, stream, ev0, ev1, 0, P);
       break;
     case 4:
-      hipLaunchKernelGGL(recent_fused<4>, grid, block, lds, stream, P);
+      hipExtLaunchKernelGGL(recent_fused<4>, grid, block, lds, stream, ev0, ev1, 0, P);
       break;
     default:
-      hipLaunchKernelGGL(recent_fused<2>, grid, block, lds, stream, P);
+      hipExtLaunchKernelGGL(recent_fused<2>, grid, block, lds, stream, ev0, ev1, 0, P);
       break;
   }
   return check_launch("recent_fused");

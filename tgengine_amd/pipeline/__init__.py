@@ -44,10 +44,19 @@ def event_plan(b: int, groups: list) -> np.ndarray:
 
 
 class DataPipeline:
-    def __init__(self, spec: GatherSpec, graph: TemporalGraph, time_encoder=None):
+    """``time_encoder``: optional module with a ``linear`` Linear(1, d_t) whose
+    weight/bias replace the fixed cosine frequencies.  ``queries_per_workgroup``:
+    queries one workgroup (one wavefront each) gathers when no co-occurrence pair
+    has to share a workgroup."""
+
+    def __init__(self, spec: GatherSpec, graph: TemporalGraph, time_encoder=None,
+                 queries_per_workgroup: int = 4):
+        if not 1 <= queries_per_workgroup <= _lib.TGX_MAX_GROUP:
+            raise ValueError(f"queries_per_workgroup must be in [1, {_lib.TGX_MAX_GROUP}]")
         self.spec = spec
         self.graph = graph
         self.time_encoder = time_encoder
+        self.queries_per_workgroup = int(queries_per_workgroup)
         self._plans: dict = {}
         self._te: dict = {}
 
@@ -178,8 +187,9 @@ class DataPipeline:
             return g._query(None, None, k, groups=qgroups, plan=plan, group=G, num_groups=b,
                             d_t=d_t, te_w=te_w, te_b=te_b, dt_mode=dt_mode, co_mode=co_mode,
                             want_eids=self.spec.edge_ids)
-        return g._query(None, None, k, groups=qgroups, d_t=d_t, te_w=te_w, te_b=te_b,
-                        dt_mode=dt_mode, want_eids=self.spec.edge_ids)
+        return g._query(None, None, k, groups=qgroups, group=self.queries_per_workgroup,
+                        d_t=d_t, te_w=te_w, te_b=te_b, dt_mode=dt_mode,
+                        want_eids=self.spec.edge_ids)
 
     @staticmethod
     def _co_occur_from_neighbors(src_nbrs: NeighborData, dst_nbrs: NeighborData) -> Tensor:
