@@ -1,0 +1,176 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol
+include/tgx.h declares, its struct layouts match the ctypes mirror, and every
+argument check returns the documented error before anything is launched."""
+import ctypes
+import re
+import subprocess
+import threading
+from pathlib import Path
+
+import pytest
+
+from tgengine_amd.core import _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "tgx.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(tgx_\w+)\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    names = _declared()
+    assert len(names) >= 7
+    for n in names:
+        assert hasattr(L, n), n
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+    assert L.tgx_abi_version() == 4
+    nm = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
+                        text=True).stdout
+    exported = set(re.findall(r"\bT (tgx_\w+)", nm))
+    assert set(names) <= exported
+
+
+LAYOUT_PROBE = r"""
+#include <stdio.h>
+#include <stddef.h>
+#include "tgx.h"
+#define F(T, f) printf(#T "." #f " %zu\n", offsetof(T, f));
+#define S(T) printf(#T " %zu\n", sizeof(T));
+int main(void) {
+  S(tgx_ring) F(tgx_ring, num_nodes) F(tgx_ring, slots) F(tgx_ring, ids) F(tgx_ring, eids)
+  F(tgx_ring, scratch)
+  S(tgx_csr) F(tgx_csr, offsets) F(tgx_csr, eids)
+  S(tgx_query_group) F(tgx_query_group, count) F(tgx_query_group, times_per)
+  S(tgx_recent_args) F(tgx_recent_args, k) F(tgx_recent_args, plan) F(tgx_recent_args, group)
+  F(tgx_recent_args, num_groups) F(tgx_recent_args, out_eids) F(tgx_recent_args, d_t)
+  F(tgx_recent_args, te_w) F(tgx_recent_args, dt_mode) F(tgx_recent_args, out_te)
+  F(tgx_recent_args, co_mode) F(tgx_recent_args, co_a) F(tgx_recent_args, status)
+  F(tgx_recent_args, num_query_groups) F(tgx_recent_args, query_groups)
+  F(tgx_recent_args, timing_start) F(tgx_recent_args, timing_stop)
+  return 0;
+}
+"""
+
+
+def test_struct_layouts_match_ctypes(tmp_path):
+    src = tmp_path / "probe.c"
+    src.write_text(LAYOUT_PROBE)
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", "-std=c99", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout
+    mirror = {"tgx_ring": _lib.TgxRing, "tgx_csr": _lib.TgxCsr,
+              "tgx_query_group": _lib.TgxQueryGroup, "tgx_recent_args": _lib.TgxRecentArgs}
+    for line in out.splitlines():
+        key, val = line.split()
+        if "." in key:
+            t, f = key.split(".")
+            assert getattr(mirror[t], f).offset == int(val), key
+        else:
+            assert ctypes.sizeof(mirror[key]) == int(val), key
+
+
+def _err():
+    return _lib.lib().tgx_last_error().decode()
+
+
+def test_recent_argument_checks():
+    L = _lib.lib()
+    assert L.tgx_recent(None, None, None, None) == 1 and "args is NULL" in _err()
+    a = _lib.TgxRecentArgs(k=0, group=1, num_queries=1, num_groups=1)
+    assert L.tgx_recent(None, None, ctypes.byref(a), None) == 3 and "k=0" in _err()
+    a = _lib.TgxRecentArgs(k=4, group=9, num_queries=1, num_groups=1)
+    assert L.tgx_recent(None, None, ctypes.byref(a), None) == 3 and "group=9" in _err()
+    a = _lib.TgxRecentArgs(k=4, group=1, num_queries=0, num_groups=0)
+    assert L.tgx_recent(None, None, ctypes.byref(a), None) == 0  # nothing to do
+    a = _lib.TgxRecentArgs(k=4, group=1, num_queries=5, num_groups=5)
+    assert L.tgx_recent(None, None, ctypes.byref(a), None) == 1 and "must not be NULL" in _err()
+    a = _lib.TgxRecentArgs(k=4, group=1, num_queries=5, num_groups=5, num_query_groups=5)
+    assert L.tgx_recent(None, None, ctypes.byref(a), None) == 3 and "query groups" in _err()
+    ring = _lib.TgxRing(num_nodes=10, slots=65, feat_dim=2, feat_dtype=0, ids=8, times=8)
+    a = _lib.TgxRecentArgs(k=4, group=1, num_queries=5, num_groups=5, nodes=8, times=8,
+                           out_ids=8, out_times=8, out_mask=8)
+    assert L.tgx_recent(ctypes.byref(ring), None, ctypes.byref(a), None) == 3 and "slots=65" in _err()
+    ring.slots = 4
+    ring.feat_dtype = 7
+    assert L.tgx_recent(ctypes.byref(ring), None, ctypes.byref(a), None) == 2
+    ring.feat_dtype = 0
+    a.d_t = 600
+    assert L.tgx_recent(ctypes.byref(ring), None, ctypes.byref(a), None) == 3 and "d_t=600" in _err()
+    a.d_t = 10
+    assert L.tgx_recent(ctypes.byref(ring), None, ctypes.byref(a), None) == 1 and "te_w" in _err()
+    a.d_t = 0
+    a.co_mode = 1
+    assert L.tgx_recent(ctypes.byref(ring), None, ctypes.byref(a), None) == 1 and "group >= 2" in _err()
+    a.co_mode = 0
+    a.dt_mode = 5
+    assert L.tgx_recent(ctypes.byref(ring), None, ctypes.byref(a), None) == 1 and "dt_mode" in _err()
+    a.dt_mode = 0
+    a.timing_start = 8
+    assert L.tgx_recent(ctypes.byref(ring), None, ctypes.byref(a), None) == 1 and "timing" in _err()
+    a.timing_start = 0
+    a.plan = 0
+    a.num_groups = 1
+    assert L.tgx_recent(ctypes.byref(ring), None, ctypes.byref(a), None) == 1 and "without a plan" in _err()
+
+
+def test_ring_append_argument_checks():
+    L = _lib.lib()
+    ws = ctypes.create_string_buffer(1 << 16)
+    assert L.tgx_ring_append(None, 8, 8, 8, None, 4, 0, ws, 1 << 16, None, None) == 1
+    ring = _lib.TgxRing(num_nodes=10, slots=4, feat_dim=2, feat_dtype=0, ids=8, times=8, feats=8,
+                        write_pos=8, scratch=8)
+    assert L.tgx_ring_append(ctypes.byref(ring), 8, 8, 8, None, -1, 0, ws, 1 << 16, None, None) == 1
+    assert L.tgx_ring_append(ctypes.byref(ring), 8, 8, 8, None, 0, 0, None, 0, None, None) == 0
+    ring.scratch = 0
+    assert L.tgx_ring_append(ctypes.byref(ring), 8, 8, 8, None, 4, 0, ws, 1 << 16, None, None) == 1
+    assert "scratch" in _err()
+    ring.scratch = 8
+    ring.slots = 65
+    assert L.tgx_ring_append(ctypes.byref(ring), 8, 8, 8, None, 4, 0, ws, 1 << 16, None, None) == 3
+    ring.slots = 4
+    ring.feat_dtype = 3
+    assert L.tgx_ring_append(ctypes.byref(ring), 8, 8, 8, None, 4, 0, ws, 1 << 16, None, None) == 2
+    ring.feat_dtype = 0
+    need = L.tgx_ring_append_workspace_size(4)
+    assert L.tgx_ring_append(ctypes.byref(ring), 8, 8, 8, None, 4, 0, ws, need - 1, None, None) == 1
+    assert "workspace" in _err()
+    ring.num_nodes = 1 << 31
+    assert L.tgx_ring_append(ctypes.byref(ring), 8, 8, 8, None, 4, 0, ws, 1 << 16, None, None) == 3
+
+
+def test_size_queries():
+    L = _lib.lib()
+    assert L.tgx_ring_scratch_size(1000) == (2 * 1000 + 16) * 4
+    n = 2 * 4000
+    ws = L.tgx_ring_append_workspace_size(4000)
+    assert ws >= 4 * n * 2 + 4 * (n // 2 + 1) + 4 * (n // 65 + 1)
+    assert L.tgx_ring_append_workspace_size(0) > 0
+
+
+def test_co_occurrence_argument_checks():
+    L = _lib.lib()
+    assert L.tgx_co_occurrence(8, 8, -1, 4, 8, 8, None, None) == 1
+    assert L.tgx_co_occurrence(8, 8, 4, 5000, 8, 8, None, None) == 3
+    assert L.tgx_co_occurrence(None, None, 0, 4, None, None, None, None) == 0
+    assert L.tgx_co_occurrence(None, None, 4, 4, None, None, None, None) == 1
+
+
+def test_last_error_is_per_thread():
+    L = _lib.lib()
+    L.tgx_co_occurrence(8, 8, -1, 4, 8, 8, None, None)
+    main_msg = _err()
+    seen = []
+
+    def other():
+        L.tgx_co_occurrence(8, 8, 4, 5000, 8, 8, None, None)
+        seen.append(_lib.lib().tgx_last_error().decode())
+
+    th = threading.Thread(target=other)
+    th.start()
+    th.join()
+    assert "negative" in main_msg and "above 4096" in seen[0]
+    assert _err() == main_msg

@@ -634,6 +634,10 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
   else if (P.row_bytes % 4 == 0 && (!fe || (al(P.r_feats, 3) && al(P.c_feats, 3) && al(P.o_feats, 3))))
     vec = 4;
 
+  hipEvent_t ev0 = static_cast<hipEvent_t>(a->timing_start);
+  hipEvent_t ev1 = static_cast<hipEvent_t>(a->timing_stop);
+  if ((ev0 == nullptr) != (ev1 == nullptr))
+    return fail(TGX_ERR_ARG, "tgx_recent: timing_start and timing_stop must both be set or both NULL");
   const dim3 grid(static_cast<unsigned>(a->num_groups));
   const dim3 block(kWave * a->group);
   static bool attr_done = false;
@@ -647,10 +651,6 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
     (void)hipGetLastError();
     attr_done = true;
   }
-  hipEvent_t ev0 = static_cast<hipEvent_t>(a->timing_start);
-  hipEvent_t ev1 = static_cast<hipEvent_t>(a->timing_stop);
-  if ((ev0 == nullptr) != (ev1 == nullptr))
-    return fail(TGX_ERR_ARG, "tgx_recent: timing_start and timing_stop must both be set or both NULL");
   switch (vec) {
     case 16:
       hipExtLaunchKernelGGL(recent_fused<16>, grid, block, lds, stream, ev0, ev1, 0, P);
