@@ -38,6 +38,30 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build libtgx)")
 
 
+def build_host(verbose: bool = False) -> Path:
+    """The torch extension `tgengine_amd._tgx_host` (host glue, plain g++), linked
+    against libtgx.so through an $ORIGIN rpath."""
+    import sysconfig
+    import torch
+    from torch.utils import cpp_extension as ce
+    out = PKG / ("_tgx_host" + sysconfig.get_config_var("EXT_SUFFIX"))
+    tmp = out.with_suffix(".tmp")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = ["g++", "-O2", "-shared", "-fPIC", "-std=c++17", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           "-DTORCH_EXTENSION_NAME=_tgx_host", "-DTORCH_API_INCLUDE_EXTENSION_H",
+           *[f"-I{p}" for p in ce.include_paths()], f"-I{sysconfig.get_paths()['include']}",
+           f"-I{INCLUDE}", str(CSRC / "tgx_host.cpp"), "-o", str(tmp),
+           *[f"-L{p}" for p in ce.library_paths()], "-lc10", "-ltorch", "-ltorch_cpu",
+           "-ltorch_python", f"-L{OUT_DIR}", "-ltgx", "-Wl,-rpath,$ORIGIN/_lib"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"host glue build failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, out)
+    return out
+
+
 def build(verbose: bool = False) -> Path:
     hipcc = _hipcc()
     obj_dir = OUT_DIR / "obj"
@@ -66,6 +90,7 @@ def build(verbose: bool = False) -> Path:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    build_host(verbose)
     return LIB
 
 

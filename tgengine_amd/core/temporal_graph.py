@@ -21,7 +21,6 @@ Extensions (keyword-only, defaults match the reference):
 from __future__ import annotations
 
 import ctypes
-import threading
 from dataclasses import dataclass
 from typing import Optional
 
@@ -31,6 +30,12 @@ from torch import Tensor
 
 from . import _lib
 from .batch import NeighborData
+
+try:
+    from tgengine_amd import _tgx_host
+except ImportError as _exc:  # pragma: no cover - the product path has no fallback
+    _tgx_host = None
+    _HOST_ERR = _exc
 
 _DTYPES = {torch.float32: _lib.TGX_F32, torch.bfloat16: _lib.TGX_BF16}
 
@@ -67,15 +72,12 @@ def _as(t: Tensor, dtype: torch.dtype, device: torch.device) -> Tensor:
     return t.to(device, dtype).contiguous()
 
 
-_tls = threading.local()
-
-
-def _recent_args() -> "_lib.TgxRecentArgs":
-    """A per-thread argument block for tgx_recent, reused across calls."""
-    a = getattr(_tls, "recent_args", None)
-    if a is None:
-        a = _tls.recent_args = _lib.TgxRecentArgs()
-    return a
+def _host():
+    """The host-glue extension; raises when it was not built (no fallback)."""
+    if _tgx_host is None:
+        raise RuntimeError("tgengine_amd._tgx_host is not built: run `python -m tgengine_amd.build` "
+                           f"({_HOST_ERR})")
+    return _tgx_host
 
 
 class TemporalGraph:
@@ -210,19 +212,11 @@ class TemporalGraph:
         self._num_edges += b
 
     def _append_ring(self, src, dst, time, edge_feat, b: int) -> None:
-        dev = self.device
-        src = _as(src, torch.int64, dev)
-        dst = _as(dst, torch.int64, dev)
-        time = _as(time, torch.float64, dev)
         feat = self._feat_in(edge_feat, b)
-        L = _lib.lib()
-        need = int(L.tgx_ring_append_workspace_size(b))
+        need = int(_lib.lib().tgx_ring_append_workspace_size(b))
         ws = self._workspace(need)
-        rc = L.tgx_ring_append(ctypes.byref(self._ring()), src.data_ptr(), dst.data_ptr(),
-                               time.data_ptr(), _lib.ptr(feat), b, self._num_edges,
-                               ws.data_ptr(), ws.numel(), self._status.data_ptr(),
-                               _stream_handle(dev))
-        _lib.check(rc, "tgx_ring_append")
+        _host().ring_append(ctypes.addressof(self._ring()), src, dst, time, feat, self._num_edges,
+                            ws, self._status, _stream_handle(self.device))
 
     # ------------------------------------------------------------------ CSR
     def freeze_csr(self) -> None:
@@ -277,99 +271,51 @@ class TemporalGraph:
                te_w: Optional[Tensor] = None, te_b: Optional[Tensor] = None,
                dt_mode: int = _lib.TGX_DT_DYGFORMER, co_mode: int = _lib.TGX_CO_NONE,
                want_eids: bool = False) -> dict:
-        """One tgx_recent launch; returns the output tensors by name.
+        """One tgx_recent launch.
 
         Queries come either as ``nodes``/``times`` or as ``groups``: a list of
-        (nodes, times, times_per) read in place and concatenated in order.
+        (nodes, times, times_per) read in place and concatenated in order.  Returns
+        lists of per-group views under "ids", "times", "feats", "mask" (bool), and
+        "eids" / "te" when asked for, plus "co_a", "co_c", "co_pair" with co-occurrence.
         """
         if not self._frozen:
             self.freeze_csr()
-        dev = self.device
         k = int(k)
         if not 1 <= k <= _lib.TGX_MAX_K:
             raise ValueError(f"k must be in [1, {_lib.TGX_MAX_K}], got {k}")
-        qgroups = []
-        if groups is not None:
-            if len(groups) > _lib.TGX_MAX_QUERY_GROUPS:
-                raise ValueError(f"at most {_lib.TGX_MAX_QUERY_GROUPS} query groups")
-            Q = 0
-            for (gn, gt, per) in groups:
-                gn = _as(gn.reshape(-1), torch.int64, dev)
-                gt = _as(gt.reshape(-1), torch.float64, dev)
-                if gn.shape[0] != gt.shape[0] * per:
-                    raise ValueError("query group node/time sizes do not match")
-                qgroups.append((gn, gt, per))
-                Q += int(gn.shape[0])
-        else:
-            Q = int(nodes.shape[0])
-            if times.shape[0] != Q:
+        if groups is None:
+            if times.shape[0] != nodes.shape[0]:
                 raise ValueError("nodes and times must have the same length")
-            nodes = _as(nodes, torch.int64, dev)
-            times = _as(times, torch.float64, dev)
-        out = {
-            "ids": torch.empty((Q, k), dtype=torch.int32, device=dev),
-            "times": torch.empty((Q, k), dtype=torch.float64, device=dev),
-            "feats": torch.empty((Q, k, self.edge_feat_dim), dtype=self.feat_dtype, device=dev),
-            "mask": torch.empty((Q, k), dtype=torch.uint8, device=dev),
-        }
+            groups = [(nodes, times, 1)]
+        if len(groups) > _lib.TGX_MAX_QUERY_GROUPS:
+            raise ValueError(f"at most {_lib.TGX_MAX_QUERY_GROUPS} query groups")
+        ring = self._ring()
+        csr = self._csr()
+        ev0 = ev1 = 0
+        if self.kernel_timer is not None:
+            ev0, ev1 = self.kernel_timer.events()
+        res = _host().recent(
+            ctypes.addressof(ring) if ring is not None else 0,
+            ctypes.addressof(csr) if csr is not None else 0,
+            [g[0] for g in groups], [g[1] for g in groups], [int(g[2]) for g in groups],
+            k, self.edge_feat_dim, self.feat_dtype, plan, group,
+            -1 if num_groups is None else int(num_groups), int(d_t), te_w, te_b, int(dt_mode),
+            int(co_mode), bool(want_eids), self._status, _stream_handle(self.device), ev0, ev1)
+        out = {"ids": res[0], "times": res[1], "feats": res[2], "mask": res[3]}
         if want_eids:
-            out["eids"] = torch.empty((Q, k), dtype=torch.int64, device=dev)
+            out["eids"] = res[4]
         if d_t > 0:
-            out["te"] = torch.empty((Q, k, d_t), dtype=torch.float32, device=dev)
-        if num_groups is None:
-            num_groups = (Q + group - 1) // group
+            out["te"] = res[5]
         if co_mode != _lib.TGX_CO_NONE:
-            L = k if co_mode == _lib.TGX_CO_FREQ else k + 1
-            out["co_a"] = torch.empty((num_groups, L, 2), dtype=torch.int32, device=dev)
-            out["co_c"] = torch.empty((num_groups, L, 2), dtype=torch.int32, device=dev)
-            out["co_pair"] = torch.empty((num_groups,), dtype=torch.float32, device=dev)
-        args = _recent_args()
-        args.nodes = nodes.data_ptr() if (Q and not qgroups) else 0
-        args.times = times.data_ptr() if (Q and not qgroups) else 0
-        args.num_queries = Q
-        args.k = k
-        args.plan = _lib.ptr(plan)
-        args.group = group
-        args.num_groups = num_groups
-        args.out_ids = out["ids"].data_ptr()
-        args.out_times = out["times"].data_ptr()
-        args.out_feats = out["feats"].data_ptr()
-        args.out_mask = out["mask"].data_ptr()
-        args.out_eids = _lib.ptr(out.get("eids"))
-        args.d_t = d_t
-        args.te_w = _lib.ptr(te_w)
-        args.te_b = _lib.ptr(te_b)
-        args.dt_mode = dt_mode
-        args.out_te = _lib.ptr(out.get("te"))
-        args.co_mode = co_mode
-        args.co_a = _lib.ptr(out.get("co_a"))
-        args.co_c = _lib.ptr(out.get("co_c"))
-        args.co_pair = _lib.ptr(out.get("co_pair"))
-        args.status = self._status.data_ptr()
-        args.num_query_groups = len(qgroups)
-        for i, (gn, gt, per) in enumerate(qgroups):
-            qg = args.query_groups[i]
-            qg.nodes, qg.times, qg.count, qg.times_per = gn.data_ptr(), gt.data_ptr(), gn.shape[0], per
-        args.timing_start = args.timing_stop = 0
-        if Q > 0:
-            ring = self._ring()
-            csr = self._csr()
-            L_ = _lib.lib()
-            timer = self.kernel_timer
-            if timer is not None:
-                args.timing_start, args.timing_stop = timer.events()
-            rc = L_.tgx_recent(ctypes.byref(ring) if ring is not None else None,
-                               ctypes.byref(csr) if csr is not None else None,
-                               ctypes.byref(args), _stream_handle(dev))
-            _lib.check(rc, "tgx_recent")
-        out["mask"] = out["mask"].view(torch.bool)
+            out["co_a"], out["co_c"], out["co_pair"] = res[6]
         return out
 
     def recent(self, nodes: Tensor, times: Tensor, k: int) -> NeighborData:
         """Most recent k neighbours before each query time (reference :183-280)."""
         o = self._query(nodes, times, k, want_eids=self.track_edge_ids)
-        return NeighborData(neighbor_ids=o["ids"], timestamps=o["times"], edge_feats=o["feats"],
-                            mask=o["mask"], edge_ids=o.get("eids"))
+        return NeighborData(neighbor_ids=o["ids"][0], timestamps=o["times"][0],
+                            edge_feats=o["feats"][0], mask=o["mask"][0],
+                            edge_ids=o["eids"][0] if "eids" in o else None)
 
     def recent_2hop(self, nodes: Tensor, times: Tensor, k1: int, k2: int) -> NeighborData:
         """1-hop and 2-hop neighbours (reference :397-473): the 2-hop query of slot

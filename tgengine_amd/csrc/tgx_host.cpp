@@ -1,0 +1,145 @@
+// Host glue of the Python API (torch extension module `tgengine_amd._tgx_host`).
+//
+// One call per TemporalGraph.recent / DataPipeline.prepare / advance: it checks
+// the inputs, allocates the outputs from the caching allocator, fills the C-ABI
+// argument block, launches through libtgx and returns the per-group views.  This
+// keeps the per-batch host cost to a few microseconds; all device work is in
+// libtgx (include/tgx.h), which never sees a torch type.
+#include <torch/extension.h>
+
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "tgx.h"
+
+namespace {
+
+void check(int rc, const char* what) {
+  if (rc != TGX_OK) throw std::runtime_error(std::string(what) + " failed: " + tgx_last_error());
+}
+
+at::Tensor as_dev(const at::Tensor& t, at::ScalarType dt, const at::Device& dev) {
+  if (t.scalar_type() == dt && t.device() == dev && t.is_contiguous()) return t;
+  return t.to(dev, dt).contiguous();
+}
+
+int64_t ptr(const c10::optional<at::Tensor>& t) {
+  return t.has_value() ? reinterpret_cast<int64_t>(t->data_ptr()) : 0;
+}
+
+// Queries arrive as groups (nodes, times, times_per) read in place by the kernel.
+// Returns [ids, times, feats, mask(bool), eids|None-placeholder, te|placeholder,
+//          co_a, co_c, co_pair] as lists of per-group views (co_* unsplit).
+std::vector<std::vector<at::Tensor>> recent(
+    int64_t ring_addr, int64_t csr_addr, const std::vector<at::Tensor>& gnodes,
+    const std::vector<at::Tensor>& gtimes, const std::vector<int64_t>& gper, int64_t k,
+    int64_t feat_dim, at::ScalarType feat_dtype, const c10::optional<at::Tensor>& plan,
+    int64_t group, int64_t num_groups, int64_t d_t, const c10::optional<at::Tensor>& te_w,
+    const c10::optional<at::Tensor>& te_b, int64_t dt_mode, int64_t co_mode, bool want_eids,
+    const at::Tensor& status, int64_t stream, int64_t ev0, int64_t ev1) {
+  const size_t ng = gnodes.size();
+  if (ng == 0 || ng > TGX_MAX_QUERY_GROUPS || gtimes.size() != ng || gper.size() != ng)
+    throw std::invalid_argument("recent: 1..4 query groups with matching times");
+  const at::Device dev = status.device();
+  std::vector<at::Tensor> n(ng), t(ng);
+  std::vector<int64_t> sizes(ng);
+  int64_t Q = 0;
+  for (size_t g = 0; g < ng; ++g) {
+    n[g] = as_dev(gnodes[g].reshape({-1}), at::kLong, dev);
+    t[g] = as_dev(gtimes[g].reshape({-1}), at::kDouble, dev);
+    if (n[g].numel() != t[g].numel() * gper[g])
+      throw std::invalid_argument("recent: query group node/time sizes do not match");
+    sizes[g] = n[g].numel();
+    Q += sizes[g];
+  }
+  if (num_groups < 0) num_groups = (Q + group - 1) / group;
+  auto o32 = at::TensorOptions().device(dev).dtype(at::kInt);
+  at::Tensor ids = at::empty({Q, k}, o32);
+  at::Tensor tms = at::empty({Q, k}, at::TensorOptions().device(dev).dtype(at::kDouble));
+  at::Tensor fts = at::empty({Q, k, feat_dim}, at::TensorOptions().device(dev).dtype(feat_dtype));
+  at::Tensor msk = at::empty({Q, k}, at::TensorOptions().device(dev).dtype(at::kBool));
+  c10::optional<at::Tensor> eids, te, co_a, co_c, co_pair;
+  if (want_eids) eids = at::empty({Q, k}, at::TensorOptions().device(dev).dtype(at::kLong));
+  if (d_t > 0) te = at::empty({Q, k, d_t}, at::TensorOptions().device(dev).dtype(at::kFloat));
+  if (co_mode != TGX_CO_NONE) {
+    const int64_t L = co_mode == TGX_CO_FREQ ? k : k + 1;
+    co_a = at::empty({num_groups, L, 2}, o32);
+    co_c = at::empty({num_groups, L, 2}, o32);
+    co_pair = at::empty({num_groups}, at::TensorOptions().device(dev).dtype(at::kFloat));
+  }
+  tgx_recent_args a{};
+  a.num_queries = Q;
+  a.k = static_cast<int32_t>(k);
+  a.plan = plan.has_value() ? plan->data_ptr<int32_t>() : nullptr;
+  a.group = static_cast<int32_t>(group);
+  a.num_groups = num_groups;
+  a.out_ids = ids.data_ptr<int32_t>();
+  a.out_times = tms.data_ptr<double>();
+  a.out_feats = fts.data_ptr();
+  a.out_mask = reinterpret_cast<uint8_t*>(msk.data_ptr<bool>());
+  a.out_eids = eids.has_value() ? eids->data_ptr<int64_t>() : nullptr;
+  a.d_t = static_cast<int32_t>(d_t);
+  a.te_w = te_w.has_value() ? te_w->data_ptr<float>() : nullptr;
+  a.te_b = te_b.has_value() ? te_b->data_ptr<float>() : nullptr;
+  a.dt_mode = static_cast<int32_t>(dt_mode);
+  a.out_te = te.has_value() ? te->data_ptr<float>() : nullptr;
+  a.co_mode = static_cast<int32_t>(co_mode);
+  a.co_a = co_a.has_value() ? co_a->data_ptr<int32_t>() : nullptr;
+  a.co_c = co_c.has_value() ? co_c->data_ptr<int32_t>() : nullptr;
+  a.co_pair = co_pair.has_value() ? co_pair->data_ptr<float>() : nullptr;
+  a.status = status.data_ptr<int32_t>();
+  a.num_query_groups = static_cast<int32_t>(ng);
+  for (size_t g = 0; g < ng; ++g) {
+    a.query_groups[g].nodes = n[g].data_ptr<int64_t>();
+    a.query_groups[g].times = t[g].data_ptr<double>();
+    a.query_groups[g].count = sizes[g];
+    a.query_groups[g].times_per = static_cast<int32_t>(gper[g]);
+  }
+  a.timing_start = reinterpret_cast<void*>(ev0);
+  a.timing_stop = reinterpret_cast<void*>(ev1);
+  if (Q > 0)
+    check(tgx_recent(reinterpret_cast<const tgx_ring*>(ring_addr),
+                     reinterpret_cast<const tgx_csr*>(csr_addr), &a,
+                     reinterpret_cast<void*>(stream)),
+          "tgx_recent");
+  std::vector<std::vector<at::Tensor>> out;
+  auto split = [&](const at::Tensor& x) {
+    return ng == 1 ? std::vector<at::Tensor>{x} : at::split_with_sizes(x, sizes, 0);
+  };
+  out.push_back(split(ids));
+  out.push_back(split(tms));
+  out.push_back(split(fts));
+  out.push_back(split(msk));
+  out.push_back(eids.has_value() ? split(*eids) : std::vector<at::Tensor>{});
+  out.push_back(te.has_value() ? split(*te) : std::vector<at::Tensor>{});
+  if (co_mode != TGX_CO_NONE) out.push_back({*co_a, *co_c, *co_pair});
+  else out.push_back({});
+  return out;
+}
+
+void ring_append(int64_t ring_addr, const at::Tensor& src, const at::Tensor& dst,
+                 const at::Tensor& time, const c10::optional<at::Tensor>& feat,
+                 int64_t eid_base, const at::Tensor& workspace, const at::Tensor& status,
+                 int64_t stream) {
+  const at::Device dev = status.device();
+  const int64_t b = src.numel();
+  at::Tensor s = as_dev(src, at::kLong, dev);
+  at::Tensor d = as_dev(dst, at::kLong, dev);
+  at::Tensor t = as_dev(time, at::kDouble, dev);
+  if (d.numel() != b || t.numel() != b)
+    throw std::invalid_argument("advance: src, dst and time must have the same length");
+  check(tgx_ring_append(reinterpret_cast<const tgx_ring*>(ring_addr), s.data_ptr<int64_t>(),
+                        d.data_ptr<int64_t>(), t.data_ptr<double>(),
+                        feat.has_value() ? feat->data_ptr() : nullptr, b, eid_base,
+                        workspace.data_ptr(), static_cast<size_t>(workspace.numel()),
+                        status.data_ptr<int32_t>(), reinterpret_cast<void*>(stream)),
+        "tgx_ring_append");
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("recent", &recent, "allocate outputs, launch tgx_recent, return per-group views");
+  m.def("ring_append", &ring_append, "launch tgx_ring_append on one batch");
+}

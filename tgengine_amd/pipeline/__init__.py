@@ -127,8 +127,13 @@ class DataPipeline:
             all_times = torch.cat([g[1].repeat_interleave(g[2]) if g[2] > 1 else g[1]
                                    for g in qgroups])
             hop = self.graph.recent_2hop(all_nodes, all_times, k, k2)
-            out = {"ids": hop.neighbor_ids, "times": hop.timestamps, "feats": hop.edge_feats,
-                   "mask": hop.mask, "eids": hop.edge_ids}
+
+            def split(t):
+                return None if t is None else torch.split_with_sizes(t, sizes, dim=0)
+
+            out = {"ids": split(hop.neighbor_ids), "times": split(hop.timestamps),
+                   "feats": split(hop.edge_feats), "mask": split(hop.mask),
+                   "eids": split(hop.edge_ids)}
             extra = {"hop2_ids": hop.hop2_ids, "hop2_times": hop.hop2_times,
                      "hop2_feats": hop.hop2_feats, "hop2_mask": hop.hop2_mask}
             if d_t > 0 or want_co:
@@ -138,11 +143,8 @@ class DataPipeline:
             out = self._fused(qgroups, k, b, per_event, d_t, te_w, te_b, dt_mode, co_mode)
             extra = {}
 
-        def split(t):
-            return None if t is None else torch.split_with_sizes(t, sizes, dim=0)
-
-        parts = {kk: split(out.get(kk)) for kk in ("ids", "times", "feats", "mask", "te", "eids")}
-        hparts = {kk: split(v) for kk, v in extra.items()}
+        parts = {kk: out.get(kk) for kk in ("ids", "times", "feats", "mask", "te", "eids")}
+        hparts = {kk: torch.split_with_sizes(v, sizes, dim=0) for kk, v in extra.items()}
         nbrs = {}
         for i, name in enumerate(names):
             nd = NeighborData(parts["ids"][i], parts["times"][i], parts["feats"][i], parts["mask"][i])
