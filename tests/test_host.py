@@ -143,22 +143,62 @@ def test_cpu_baseline_restatement_matches_oracle(name, nb):
 
 
 # ------------------------------------------------------------- device cosine on the host
-def test_device_cosine_host_build(tmp_path):
+def _rev_frac_host(tmp_path, args):
     exe = tmp_path / "cos_check"
     r = subprocess.run(["/opt/rocm/bin/hipcc", "-O2", "-std=c++17", "-ffp-contract=off",
                         f"-I{ROOT / 'tgengine_amd' / 'csrc'}", str(ROOT / "tests" / "cos_check.cpp"),
                         "-o", str(exe)], capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
+    out = subprocess.run([str(exe)], input=np.asarray(args, np.float32).tobytes(),
+                         capture_output=True, check=True).stdout
+    return np.frombuffer(out, np.float64)
+
+
+def test_time_encoding_reduction_host_build(tmp_path):
+    """rev_frac (the float64 half of the device cosine) against libm: cos(2 pi f) must
+    equal cos(x) to 2e-7 below 2^29 (single rounding of x/(2 pi)) and to 1e-12 above,
+    where the double-double table of frac(2^E/(2 pi)) does an exact reduction."""
     rng = np.random.default_rng(1)
     w = O.time_weights(100)
     dts = np.concatenate([10 ** rng.uniform(-3, 9, 4000), rng.uniform(-1e9, 1e9, 2000)]).astype(np.float32)
-    args = O.time_args(dts, w).ravel()
-    extra = np.float32([0.0, -0.0, np.pi / 2, 1e12, 3e38, -3e38, 1.0995116e12, 7.5e15])
-    args = np.concatenate([args, extra, (np.arange(-5000, 5000) * np.float32(np.pi / 2)).astype(np.float32)])
-    y = np.frombuffer(subprocess.run([str(exe)], input=args.tobytes(), capture_output=True,
-                                     check=True).stdout, np.float32)
-    err = np.abs(y.astype(np.float64) - np.cos(args.astype(np.float64)))
-    assert err.max() < 1e-7, (err.max(), args[err.argmax()])
+    small = O.time_args(dts, w).ravel()
+    small = small[np.abs(small) < 2.0 ** 29]
+    big = np.concatenate([
+        (10 ** rng.uniform(np.log10(2.0 ** 29), 38.5, 20000)).astype(np.float32),
+        -(10 ** rng.uniform(np.log10(2.0 ** 29), 38.5, 2000)).astype(np.float32),
+        np.float32([2.0 ** 29, -(2.0 ** 29), 1e12, 3e38, -3e38, 1.0995116e12, 7.5e15,
+                    np.finfo(np.float32).max]),
+        (np.arange(1, 5000) * np.float32(2.0 ** 29 + 64)).astype(np.float32)])
+    for args, tol in ((small, 2e-7), (big, 1e-12)):
+        f = _rev_frac_host(tmp_path, args)
+        assert np.all(np.abs(f) <= 0.5)
+        err = np.abs(np.cos(2 * np.pi * f) - np.cos(args.astype(np.float64)))
+        assert err.max() < tol, (tol, err.max(), args[err.argmax()])
+    # closed forms: cos(0) = 1 (f = 0), and non-finite arguments give NaN
+    f = _rev_frac_host(tmp_path, np.float32([0.0, -0.0, np.inf, -np.inf, np.nan]))
+    assert f[0] == 0.0 and f[1] == 0.0 and np.all(np.isnan(f[2:]))
+
+
+def test_time_encoding_reduction_table_is_generated():
+    """tgx_rev_table.h is what gen_rev_table.py writes (pi from mpmath at 400 bits),
+    and hi + lo equals frac(2^E / (2 pi)) in exact rational arithmetic for a few E."""
+    from fractions import Fraction
+    import importlib.util
+    import mpmath
+    src = ROOT / "tgengine_amd" / "csrc" / "gen_rev_table.py"
+    spec = importlib.util.spec_from_file_location("gen_rev_table", src)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    rows = mod.table()
+    text = (ROOT / "tgengine_amd" / "csrc" / "tgx_rev_table.h").read_text()
+    for e, hi, lo in rows:
+        assert f"{{{hi!r}, {lo!r}}}" in text and f"E = {e} " in text
+    mpmath.mp.prec = 500
+    pi = Fraction(int(mpmath.floor(mpmath.pi * mpmath.mpf(2) ** 480)), 2 ** 480)
+    for e, hi, lo in rows[::17] + rows[-1:]:
+        exact = Fraction(2 ** e) / (2 * pi)
+        exact -= exact.numerator // exact.denominator
+        assert abs(Fraction(hi) + Fraction(lo) - exact) < Fraction(1, 2 ** 100)
 
 
 # ------------------------------------------------------------- bench contract

@@ -1,13 +1,23 @@
-// cos of an fp32 argument, evaluated in float64 (time-encoding hot loop).
+// Cosine of an fp32 argument for the fused time encoding.
 //
-// Reduction x = k*pi + r with k = rint(x/pi) obtained by adding 1.5*2^52 (the
-// low mantissa bit of the sum is k's parity), r by Cody-Waite with a two-term
-// pi (error ~1e-16 for |x| < 2^40), then cos(r) on |r| <= pi/2 by a degree-5
-// polynomial in r^2 and cos(x) = (-1)^k cos(r).  The coefficients are a
-// near-minimax fit computed for this library (iterated reweighted least
-// squares on Chebyshev nodes, max error 2.2e-10 on |r| <= pi/2 * 1.0001).
-// Callers route |x| >= 2^40 to cos_slow.  The same source compiles for the
-// host, which is how the CPU tests check it against float64 cos.
+// cos(x) = cos(2 pi f) with f the signed fractional part of x / (2 pi), f in
+// [-1/2, 1/2], computed in float64 by rev_frac.  The device then evaluates
+// cos(2 pi f) with v_cos_f32, whose argument is in revolutions (max abs error
+// 1.3e-7 measured on gfx950 over every fp32 |f| <= 1/2).
+//
+//  * |x| < 2^29 (rev_frac_small): u = x * (1/(2 pi)) rounded once in float64, so
+//    |u - x/(2 pi)| <= 2 |u| 2^-53 < 2e-8 revolutions; f = u - rint(u) exactly.
+//  * |x| >= 2^29: x = M 2^E with an integer |M| < 2^24 and E in [6, 104], so
+//    frac(x / (2 pi)) = frac(M F_E) with F_E = frac(2^E / (2 pi)) held as a
+//    double-double hi + lo (tgx_rev_table.h, generated from a 400-bit pi).
+//    p = M hi and its rounding error e = fma(M, hi, -p) are exact, so
+//    f = (p - rint(p)) + (e + M lo) is within ~2^-80 of the true fraction.
+//  * non-finite x gives NaN.
+//
+// Worst case on the device: 2e-8 rev (reduction) + 2^-27 rev (f rounded to fp32)
+// + 1.3e-7 (v_cos_f32), i.e. below 3.5e-7 absolute.  rev_frac is plain float64
+// arithmetic and also builds for the host, where the CPU tests compare
+// cos(2 pi f) with libm's cos(x).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -15,42 +25,33 @@
 #include <cmath>
 #include <cstdint>
 
+#include "tgx_rev_table.h"
+
 namespace tgx {
 
-constexpr double kInvPi = 0.3183098861837907;
-constexpr double kPiHi = 3.141592653589793;
-constexpr double kPiLo = 1.2246467991473532e-16;
-constexpr double kRoundMagic = 6755399441055744.0;  // 1.5 * 2^52
-constexpr double kA0 = 0.999999999780424;
-constexpr double kA1 = -0.49999999357852726;
-constexpr double kA2 = 0.0416666362342501;
-constexpr double kA3 = -0.0013888361089159438;
-constexpr double kA4 = 2.4760145078500364e-05;
-constexpr double kA5 = -2.605120135781943e-07;
-constexpr float kBigArg = 1099511627776.0f;  // 2^40
+constexpr double kInv2Pi = 0.15915494309189535;
+constexpr float kRevArg = 536870912.0f;  // 2^29
 
-__host__ __device__ inline float cos_fast(float x) {
-  const double xd = static_cast<double>(x);
-  const double t = fma(xd, kInvPi, kRoundMagic);
-  const double k = t - kRoundMagic;
-  const uint32_t parity = static_cast<uint32_t>(__builtin_bit_cast(uint64_t, t)) << 31;
-  double r = fma(-k, kPiHi, xd);
-  r = fma(-k, kPiLo, r);
-  const double z = r * r;
-  double p = fma(z, kA5, kA4);
-  p = fma(p, z, kA3);
-  p = fma(p, z, kA2);
-  p = fma(p, z, kA1);
-  p = fma(p, z, kA0);
-  return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, static_cast<float>(p)) ^ parity);
+__host__ __device__ inline double rev_frac_small(float x) {
+  const double u = static_cast<double>(x) * kInv2Pi;
+  return u - rint(u);
 }
 
-__host__ __device__ inline float cos_slow(float x) {
-  return static_cast<float>(cos(static_cast<double>(x)));
-}
-
-__host__ __device__ inline float cos_any(float x) {
-  return fabsf(x) < kBigArg ? cos_fast(x) : cos_slow(x);
+// tab: an array initialised with TGX_REV_TABLE_ROWS
+__host__ __device__ inline double rev_frac(float x, const double (*tab)[2]) {
+  if (fabsf(x) < kRevArg) return rev_frac_small(x);
+  const uint32_t bits = __builtin_bit_cast(uint32_t, x);
+  const int ex = static_cast<int>((bits >> 23) & 0xffu);
+  if (ex == 0xff) return static_cast<double>(x - x);  // inf or NaN -> NaN
+  const int E = ex - 150;                             // x = M * 2^E
+  double M = static_cast<double>(static_cast<int32_t>((bits & 0x7fffffu) | 0x800000u));
+  if (bits >> 31) M = -M;
+  const double hi = tab[E - TGX_REV_TABLE_MIN_EXP][0];
+  const double lo = tab[E - TGX_REV_TABLE_MIN_EXP][1];
+  const double p = M * hi;
+  const double e = fma(M, hi, -p);
+  const double f = (p - rint(p)) + fma(M, lo, e);
+  return f - rint(f);
 }
 
 }  // namespace tgx

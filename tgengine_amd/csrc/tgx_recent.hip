@@ -17,14 +17,34 @@
 //     tgengine/pipeline/__init__.py:206-219; TGX_CO_DYGFORMER as
 //     tgengine/models/dygformer.py:71-87 on the 1+K sequences with the node first.
 //
-// Mapping.  One wavefront per query: lanes hold the B <= 64 ring slots, a
-// counting rank over the wave's LDS candidate list orders them, and the same
-// wave then streams the K feature rows (16-byte loads/stores, lanes spread
-// over rows*chunks so every access is coalesced) and the K x d_t encodings
-// (float4 stores, cosine evaluated in float64 from the exact fp32 argument).
-// A workgroup holds `group` queries so a (src, dst) pair meets in one LDS.
+// Mapping.  One wavefront per query, `group` queries per workgroup (a plan group
+// puts a (src, dst) pair in one workgroup for the co-occurrence counts).  Lane s
+// loads ring slot s (with its feature row when the row is at most 64 bytes, in
+// the same memory round trip) and the node's write position.  Ranking:
+//   * fast path (no CSR candidates): a ring is written oldest-to-newest from slot
+//     write_pos % B on, so when the filled slots are exactly the last ones in that
+//     write order and their times strictly increase along it, a candidate's rank
+//     is its write-order distance from the oldest filled slot (one shuffle and
+//     two ballots verify the premise);
+//   * otherwise the candidates go to an LDS list (CSR window first, then ring
+//     slots) and each is ranked by counting earlier (time, index) entries.
+// The lane holding a selected candidate writes its id / time / mask at output
+// position K - V + rank - drop; feature rows then move to their positions by
+// lane shuffles (small rows) or 16-byte loads/stores spread over the wave, and
+// the K x d_t encodings stream out as float4 nontemporal stores with the pad
+// rows (DyGFormer dt mode) written as zeros without evaluating a cosine.  The
+// cosine of the exact fp32 argument x is v_cos_f32 of the revolution fraction of
+// x (tgx_cos.h): 6 VALU per element while every argument of the wave is below
+// 2^29, a table-driven exact reduction otherwise.
 #include "tgx_internal.h"
 #include <hip/hip_ext.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <map>
+#include <mutex>
+#include <tuple>
+
 #include "tgx_cos.h"
 
 namespace tgx {
@@ -37,10 +57,12 @@ struct Params {
   // ring
   int64_t N;
   int B;  // 0 when there is no ring
+  int b_pow2;
   const int32_t* r_ids;
   const double* r_times;
   const uint8_t* r_feats;
   const int64_t* r_eids;
+  const int64_t* r_wp;
   // csr
   int has_csr;
   const int64_t* c_off;
@@ -62,6 +84,7 @@ struct Params {
   int G;
   // outputs
   int64_t row_bytes;
+  int nch;  // row_bytes / VEC
   int32_t* o_ids;
   double* o_times;
   uint8_t* o_feats;
@@ -78,10 +101,14 @@ struct Params {
   int32_t* co_c;
   float* co_pair;
   int32_t* status;
-  // LDS layout
+  // LDS layout: weights (te_bytes), then one wave_bytes region per wavefront
   int te_bytes;
   int wave_bytes;
   int cand_cap;
+  int off_cid, off_code, off_pcode, off_pdt, off_pid, off_pt, off_pe, off_tab;
+  // work decomposition: m queries per wavefront in sub-groups of 2^lg_bp lanes
+  int m, lg_bp;
+  int split;  // wavefronts per query (m == 1): each writes every split-th output chunk
 };
 
 template <int VEC>
@@ -97,6 +124,66 @@ struct Vec<4> {
 template <>
 struct Vec<2> {
   using T = uint16_t;
+};
+
+__constant__ double kRevTableDev[][2] = {TGX_REV_TABLE_ROWS};
+
+// cos(x) as v_cos_f32 of the fp32-rounded revolution fraction (tgx_cos.h):
+// cos_small for |x| < kRevArg, cos_full for every fp32 x
+__device__ __forceinline__ float cos_small(float x) {
+  return __builtin_amdgcn_cosf(static_cast<float>(rev_frac_small(x)));
+}
+__device__ __forceinline__ float cos_full(float x) {
+  return __builtin_amdgcn_cosf(static_cast<float>(rev_frac(x, kRevTableDev)));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 1; m < kWave; m <<= 1) v = fmaxf(v, __shfl_xor(v, m));
+  return v;
+}
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ u32x4 shfl_v(u32x4 x, int src) {
+  u32x4 r;
+  r[0] = __shfl(x[0], src);
+  r[1] = __shfl(x[1], src);
+  r[2] = __shfl(x[2], src);
+  r[3] = __shfl(x[3], src);
+  return r;
+}
+
+// x / n for x * n < 2^32 (n >= 1): one multiply-high by ceil(2^32 / n)
+// Output stores.  Small-row launches write with ordinary stores (the encodings
+// then stream out of L2 at a higher rate); large-row launches, whose row copy
+// already streams, use nontemporal stores (measured faster for both shapes).
+template <bool NT, typename T>
+__device__ __forceinline__ void put(T* p, const T& v) {
+  if constexpr (NT)
+    __builtin_nontemporal_store(v, p);
+  else
+    *p = v;
+}
+
+// wavefronts per workgroup, the kernel's launch bound (512 threads)
+constexpr int kMaxWaves = 8;
+
+// queries of a launch above which small-row queries are packed several per wave
+// (about the wave slots of one MI355X: 256 CUs x 4 SIMDs x 8)
+constexpr int64_t kPackMinQueries = 8192;
+
+// row chunks each lane loads before storing them (large-row copy)
+constexpr int kCopyDepth = 4;
+
+struct FastDiv {
+  uint32_t n, m;
+  __device__ explicit FastDiv(uint32_t n_) : n(n_), m(n_ > 1 ? 0xffffffffu / n_ + 1u : 0u) {}
+  __device__ __forceinline__ uint32_t div(uint32_t x) const { return n > 1 ? __umulhi(x, m) : x; }
 };
 
 // smallest i in [lo, hi] with i == hi or t[i] >= q (t ascending); wave-uniform result
@@ -119,25 +206,34 @@ __device__ __forceinline__ int64_t wave_lower_bound(const double* __restrict__ t
 __device__ __forceinline__ int64_t query_of(const Params& P, int64_t g, int j) {
   if (j >= P.G) return -1;
   const int64_t slot = g * P.G + j;
-  int64_t q;
-  if (P.plan != nullptr)
-    q = P.plan[slot];
-  else
-    q = slot;
+  const int64_t q = P.plan != nullptr ? static_cast<int64_t>(P.plan[slot]) : slot;
   return (q >= 0 && q < P.Q) ? q : -1;
 }
 
+// node and time of query q; the query group is chosen with compares against the
+// group offsets (constant indices only, so the arguments stay in registers)
 __device__ __forceinline__ void query_load(const Params& P, int64_t q, int64_t& node, double& qt) {
   if (P.ngroups == 0) {
     node = P.nodes[q];
     qt = P.qtimes[q];
     return;
   }
-  int g = 0;
-  while (g + 1 < P.ngroups && q >= P.goff[g + 1]) ++g;
-  const int64_t l = q - P.goff[g];
-  node = P.gn[g][l];
-  qt = P.gt[g][P.gdiv[g] == 1 ? l : static_cast<int64_t>(static_cast<uint32_t>(l) / static_cast<uint32_t>(P.gdiv[g]))];
+  const int64_t* np = P.gn[0];
+  const double* tp = P.gt[0];
+  int64_t off = 0;
+  int div = P.gdiv[0];
+#pragma unroll
+  for (int g = 1; g < TGX_MAX_QUERY_GROUPS; ++g) {
+    if (g < P.ngroups && q >= P.goff[g]) {
+      np = P.gn[g];
+      tp = P.gt[g];
+      off = P.goff[g];
+      div = P.gdiv[g];
+    }
+  }
+  const int64_t l = q - off;
+  node = np[l];
+  qt = tp[div == 1 ? l : static_cast<int64_t>(static_cast<uint32_t>(l) / static_cast<uint32_t>(div))];
 }
 
 __device__ __forceinline__ int64_t query_node(const Params& P, int64_t q) {
@@ -147,15 +243,156 @@ __device__ __forceinline__ int64_t query_node(const Params& P, int64_t q) {
   return node;
 }
 
-template <int VEC>
-__global__ __launch_bounds__(512) void recent_fused(Params P) {
+// Time encodings of np consecutive output rows starting at row r0 (the wave's
+// queries are consecutive): out_te[r0 + gp, :] from pdt[gp]; a DyGFormer pad
+// (pcode < 0) encodes to zeros without evaluating a cosine.
+template <bool BIG, bool NT>
+__device__ __forceinline__ void encode_rows(const Params& P, int64_t r0, int np, const int32_t* pcode,
+                                            const float* pdt, const float* s_w, const float* s_b,
+                                            int start, int stride) {
+  const int d_t = P.d_t;
+  const bool dyg = P.dt_mode == TGX_DT_DYGFORMER;
+  const bool has_b = P.te_b != nullptr;
+  if (P.te_vec4) {
+    const int nq = d_t / 4;
+    const int total = np * nq;
+    const FastDiv dq(nq);
+    const f32x4* w4 = reinterpret_cast<const f32x4*>(s_w);
+    const f32x4* b4 = reinterpret_cast<const f32x4*>(s_b);
+    f32x4* o4 = reinterpret_cast<f32x4*>(P.o_te) + r0 * nq;
+    for (int idx = start; idx < total; idx += stride) {
+      const int gp = static_cast<int>(dq.div(idx));
+      const int c = idx - gp * nq;
+      f32x4 o = {0.f, 0.f, 0.f, 0.f};
+      if (!dyg || pcode[gp] >= 0) {
+        f32x4 a = pdt[gp] * w4[c];
+        if (has_b) a = a + b4[c];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = BIG ? cos_full(a[j]) : cos_small(a[j]);
+      }
+      put<NT>(o4 + idx, o);
+    }
+  } else {
+    const int total = np * d_t;
+    const FastDiv dd(d_t);
+    float* out = P.o_te + r0 * d_t;
+    for (int idx = start; idx < total; idx += stride) {
+      const int gp = static_cast<int>(dd.div(idx));
+      const int j = idx - gp * d_t;
+      float o = 0.f;
+      if (!dyg || pcode[gp] >= 0) {
+        float a = pdt[gp] * s_w[j];
+        if (has_b) a = a + s_b[j];
+        o = BIG ? cos_full(a) : cos_small(a);
+      }
+      out[idx] = o;
+    }
+  }
+}
+
+// Co-occurrence counts of one (query a, query c) pair by one wavefront; A and Cc
+// are the K neighbour ids of the two queries (LDS).  Output row g.
+__device__ __forceinline__ void co_occurrence_pair(const Params& P, int64_t g, int64_t qa, int64_t qc,
+                                                   const int32_t* A, const int32_t* Cc, int lane) {
+  const int K = P.K;
+  if (P.co_mode == TGX_CO_FREQ) {
+    for (int side = 0; side < 2; ++side) {
+      const int32_t* X = side == 0 ? A : Cc;
+      int32_t* out = side == 0 ? P.co_a : P.co_c;
+      int pc = 0;
+      for (int i0 = 0; i0 < K; i0 += kWave) {
+        const int i = i0 + lane;
+        int32_t x = -1;
+        int na = 0, nc = 0;
+        if (i < K) {
+          x = X[i];
+          if (x != -1) {
+            for (int j = 0; j < K; ++j) {
+              na += A[j] == x;
+              nc += Cc[j] == x;
+            }
+          }
+          out[(g * K + i) * 2 + 0] = na;
+          out[(g * K + i) * 2 + 1] = nc;
+        }
+        pc += __popcll(__ballot(i < K && x != -1 && nc > 0));
+      }
+      if (side == 0 && lane == 0 && P.co_pair != nullptr) P.co_pair[g] = static_cast<float>(pc);
+    }
+    return;
+  }
+  // DyGFormer counts on A' = [node_a] ++ A, C' = [node_c] ++ C (length K+1)
+  const int32_t na0 = static_cast<int32_t>(query_node(P, qa));
+  const int32_t nc0 = static_cast<int32_t>(query_node(P, qc));
+  const int L = K + 1;
+  if (P.co_pair != nullptr) {
+    // (B,) count over the K sequences, as in FREQ mode
+    int pc = 0;
+    for (int i0 = 0; i0 < K; i0 += kWave) {
+      const int i = i0 + lane;
+      bool hit = false;
+      if (i < K && A[i] != -1)
+        for (int j = 0; j < K && !hit; ++j) hit = Cc[j] == A[i];
+      pc += __popcll(__ballot(hit));
+    }
+    if (lane == 0) P.co_pair[g] = static_cast<float>(pc);
+  }
+  for (int side = 0; side < 2; ++side) {
+    int32_t* out = side == 0 ? P.co_a : P.co_c;
+    for (int i = lane; i < L; i += kWave) {
+      const int32_t ai = i == 0 ? na0 : A[i - 1];
+      const int32_t ci = i == 0 ? nc0 : Cc[i - 1];
+      int f0 = 0, f1 = 0;
+      if (side == 0) {
+        if (ai != -1) {
+          for (int j = 0; j < L; ++j) {
+            const int32_t aj = j == 0 ? na0 : A[j - 1];
+            const int32_t cj = j == 0 ? nc0 : Cc[j - 1];
+            f0 += aj == ai;
+            f1 += (aj == ci) && (cj != -1);
+          }
+        }
+      } else {
+        if (ci != -1) {
+          for (int j = 0; j < L; ++j) {
+            const int32_t aj = j == 0 ? na0 : A[j - 1];
+            const int32_t cj = j == 0 ? nc0 : Cc[j - 1];
+            f0 += (cj == ai) && (aj != -1);
+            f1 += cj == ci;
+          }
+        }
+      }
+      out[(g * L + i) * 2 + 0] = f0;
+      out[(g * L + i) * 2 + 1] = f1;
+    }
+  }
+}
+
+// One wavefront per tile of queries.  No plan: a tile is m = 64/Bp consecutive
+// queries (sub-group h = lanes h*Bp .. h*Bp+Bp-1 takes query h, Bp >= B); with
+// a plan: m = 1 and the workgroup is the plan group, wave j taking query j.
+// Every load of the wave (queries, ring slots and small feature rows, CSR
+// windows, edge ids) is issued and consumed before its first global store:
+// gfx9 counts vector loads and stores in one in-order vmcnt, so a load behind
+// stores would wait for their completion.  With at most one wave per SIMD slot
+// for the whole grid the gathers all run up front and the stores then stream.
+template <int VEC, int NREG>
+__global__ __launch_bounds__(kMaxWaves * kWave) __attribute__((amdgpu_waves_per_eu(8))) void recent_fused(Params P) {
   using VT = typename Vec<VEC>::T;
   extern __shared__ __align__(16) uint8_t smem[];
   const int lane = threadIdx.x & (kWave - 1);
-  const int wv = threadIdx.x / kWave;
+  const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
   const int64_t g = blockIdx.x;
   const int K = P.K;
   const int B = P.B;
+  const int C = P.cand_cap;
+  const int m = P.m;
+  const int lg = P.lg_bp;
+  const int Bp = 1 << lg;
+  const int h = lane >> lg;
+  const int sl = lane & (Bp - 1);
+  const uint64_t submask = Bp == kWave ? ~uint64_t(0) : ((uint64_t(1) << Bp) - 1);
+  const bool dyg = P.dt_mode == TGX_DT_DYGFORMER;
 
   float* s_w = reinterpret_cast<float*>(smem);
   float* s_b = s_w + (P.te_bytes / 8);
@@ -163,288 +400,301 @@ __global__ __launch_bounds__(512) void recent_fused(Params P) {
     s_w[i] = P.te_w[i];
     s_b[i] = P.te_b != nullptr ? P.te_b[i] : 0.0f;
   }
-  uint8_t* wbase = smem + P.te_bytes + static_cast<size_t>(wv) * P.wave_bytes;
-  const int C = P.cand_cap;
-  double* ct = reinterpret_cast<double*>(wbase);
-  int32_t* cid = reinterpret_cast<int32_t*>(wbase + C * 8);
-  int32_t* ccode = reinterpret_cast<int32_t*>(wbase + C * 12);
-  int32_t* pcode = reinterpret_cast<int32_t*>(wbase + C * 16);
-  float* pdt = reinterpret_cast<float*>(wbase + C * 16 + K * 4);
-  int32_t* pid = reinterpret_cast<int32_t*>(wbase + C * 16 + K * 8);
+  __syncthreads();
+  uint8_t* wb = smem + P.te_bytes + static_cast<size_t>(wv) * P.wave_bytes;
+  double* ct = reinterpret_cast<double*>(wb);                       // [m][C] candidates
+  int32_t* cid = reinterpret_cast<int32_t*>(wb + P.off_cid);
+  int32_t* ccode = reinterpret_cast<int32_t*>(wb + P.off_code);
+  int32_t* pcode = reinterpret_cast<int32_t*>(wb + P.off_pcode);  // [m][K] slot, B + CSR index, -1
+  float* pdt = reinterpret_cast<float*>(wb + P.off_pdt);           // [m][K] dt
+  int32_t* pid = reinterpret_cast<int32_t*>(wb + P.off_pid);       // [m][K] id
+  double* pt = reinterpret_cast<double*>(wb + P.off_pt);           // [m][K] time
+  int64_t* tq = reinterpret_cast<int64_t*>(wb + P.off_tab);        // [m] query (-1 = none)
+  int64_t* tur = tq + m;                                            // [m] ring row
+  int64_t* tcb = tur + m;                                           // [m] CSR window start
+  int64_t* pe = reinterpret_cast<int64_t*>(wb + P.off_pe);         // [m][K] edge id
 
-  const int64_t q = query_of(P, g, wv);
-  const bool active = q >= 0;
+  // ---- the wave's queries: query slot wv / split of the workgroup; the split
+  // waves of one query repeat its (cheap) gather and share its outputs ----
+  const int split = P.split;
+  const int qs = wv / split;
+  const int part = wv - qs * split;
+  int64_t q;
+  if (P.plan != nullptr) {
+    q = query_of(P, g, qs);
+  } else {
+    const int64_t t = g * (blockDim.x / kWave / split) + qs;
+    q = t * m + h;
+    if (q >= P.Q) q = -1;
+  }
   int64_t node = -1;
   double qt = 0.0;
-  if (active) query_load(P, q, node, qt);
-  const bool bad = active && node >= P.N;
-  if (bad && lane == 0 && P.status != nullptr) atomicAdd(&P.status[TGX_ST_BAD_QUERY_NODE], 1);
+  if (q >= 0) query_load(P, q, node, qt);
+  const bool bad = q >= 0 && node >= P.N;
+  if (bad && sl == 0 && part == 0 && P.status != nullptr) atomicAdd(&P.status[TGX_ST_BAD_QUERY_NODE], 1);
   const int64_t ur = node < 0 ? 0 : node;
+  const bool live = q >= 0 && !bad;
 
-  // ---- candidates: CSR window, then valid ring slots (compacted) ----
-  int ncand = 0;
+  // ---- ring slot sl of query h, its feature row (NREG > 0) and write position ----
+  int32_t rid = -1;
+  double rt = 0.0;
+  int64_t wp = 0;
+  VT rows[NREG > 0 ? NREG : 1];
+#pragma unroll
+  for (int k = 0; k < (NREG > 0 ? NREG : 1); ++k) rows[k] = VT{};
+  if (live && B > 0) {
+    if (sl < B) {
+      rid = P.r_ids[ur * B + sl];
+      rt = P.r_times[ur * B + sl];
+      if constexpr (NREG > 0) {
+        const VT* src = reinterpret_cast<const VT*>(P.r_feats + (ur * B + sl) * P.row_bytes);
+#pragma unroll
+        for (int k = 0; k < NREG; ++k)
+          if (k < P.nch) rows[k] = src[k];
+      }
+    }
+    if (P.r_wp != nullptr) wp = P.r_wp[ur];
+  }
+
+  // |w| and |b| bounds of the cosine domain check, computed while the loads fly
+  float te_wmax = 0.f, te_bmax = 0.f;
+  if (P.d_t > 0) {
+    for (int i = lane; i < P.d_t; i += kWave) {
+      te_wmax = fmaxf(te_wmax, fabsf(s_w[i]));
+      te_bmax = fmaxf(te_bmax, fabsf(s_b[i]));
+    }
+    te_wmax = wave_max(te_wmax);
+    te_bmax = wave_max(te_bmax);
+  }
+
+  // ---- CSR windows: a 64-ary search per query of the wave, all lanes ----
+  int ncsr = 0;
   int64_t cbase = 0;
-  if (active && !bad && P.has_csr && node >= 0) {
-    const int64_t s0 = P.c_off[node];
-    const int64_t s1 = P.c_off[node + 1];
-    const int64_t cnt = wave_lower_bound(P.c_times, s0, s1, qt, lane) - s0;
-    const int take = static_cast<int>(cnt < K ? cnt : K);
-    cbase = s0 + cnt - take;
-    for (int j = lane; j < take; j += kWave) {
-      ct[j] = P.c_times[cbase + j];
-      cid[j] = P.c_ids[cbase + j];
-      ccode[j] = B + j;
+  if (P.has_csr) {
+    for (int hh = 0; hh < m; ++hh) {
+      const int64_t nh = __shfl(node, hh << lg);
+      const double th = __shfl(qt, hh << lg);
+      const int lh = __shfl(static_cast<int>(live), hh << lg);
+      if (lh && nh >= 0) {
+        const int64_t s0 = P.c_off[nh];
+        const int64_t s1 = P.c_off[nh + 1];
+        const int64_t cnt = wave_lower_bound(P.c_times, s0, s1, th, lane) - s0;
+        const int take = static_cast<int>(cnt < K ? cnt : K);
+        if (h == hh) {
+          ncsr = take;
+          cbase = s0 + cnt - take;
+        }
+      }
     }
-    ncand = take;
+    for (int j = sl; j < ncsr; j += Bp) {
+      ct[h * C + j] = P.c_times[cbase + j];
+      cid[h * C + j] = P.c_ids[cbase + j];
+      ccode[h * C + j] = B + j;
+    }
   }
-  if (active && !bad && B > 0) {
-    int32_t rid = -1;
-    double rt = 0.0;
-    bool v = false;
-    if (lane < B) {
-      rid = P.r_ids[ur * B + lane];
-      rt = P.r_times[ur * B + lane];
-      v = (rid != -1) && (rt < qt);
-    }
-    const uint64_t m = __ballot(v);
-    if (v) {
-      const int at = ncand + __popcll(m & ((uint64_t(1) << lane) - 1));
-      ct[at] = rt;
-      cid[at] = rid;
-      ccode[at] = lane;
-    }
-    ncand += __popcll(m);
-  }
-  __syncthreads();
-
-  // ---- rank: position of each candidate among the V most recent ----
+  const bool v = live && sl < B && rid != -1 && rt < qt;
+  const uint64_t mine = (__ballot(v) >> (h << lg)) & submask;
+  const int ncand = ncsr + __popcll(mine);
   const int V = ncand < K ? ncand : K;
   const int drop = ncand - V;
-  for (int p = lane; p < K - V; p += kWave) pcode[p] = -1;
-  for (int c = lane; c < ncand; c += kWave) {
-    const double tc = ct[c];
-    int r = 0;
-    for (int c2 = 0; c2 < ncand; ++c2) {
-      const double t2 = ct[c2];
-      r += (t2 < tc) || (t2 == tc && c2 < c);
-    }
-    if (r >= drop) pcode[K - V + (r - drop)] = c;
+  if (sl == 0) {
+    tq[h] = q;
+    tur[h] = ur;
+    tcb[h] = cbase;
   }
-  __syncthreads();
 
-  // ---- ids / times / mask / edge ids; per-position dt and source code ----
-  if (active) {
-    for (int p = lane; p < K; p += kWave) {
-      const int c = pcode[p];
-      int32_t id = -1;
-      double t = 0.0;
-      uint8_t mk = 0;
-      int64_t e = -1;
-      int code = -1;
-      if (c >= 0) {
-        id = cid[c];
-        t = ct[c];
-        mk = 1;
-        code = ccode[c];
-        if (P.o_eids != nullptr) {
-          if (code < B)
-            e = P.r_eids != nullptr ? P.r_eids[ur * B + code] : -1;
-          else
-            e = P.c_eids != nullptr ? P.c_eids[cbase + (code - B)] : -1;
-        }
-      }
-      const int64_t o = q * K + p;
-      P.o_ids[o] = id;
-      P.o_times[o] = t;
-      P.o_mask[o] = mk;
-      if (P.o_eids != nullptr) P.o_eids[o] = e;
-      float dt;
-      if (P.dt_mode == TGX_DT_DYGFORMER)
-        dt = static_cast<float>(qt) - static_cast<float>(t);
-      else
-        dt = static_cast<float>(qt - t);
-      pdt[p] = dt;
-      pid[p] = id;
-      pcode[p] = code;
+  // ---- rank into LDS positions ----
+  bool lane_big = false;
+  auto emit = [&](int p, int32_t id, double t, int code) {
+    const int pp = h * K + p;
+    const float dt = dyg ? static_cast<float>(qt) - static_cast<float>(t) : static_cast<float>(qt - t);
+    pdt[pp] = dt;
+    pt[pp] = t;
+    pcode[pp] = code;
+    pid[pp] = id;
+    lane_big |= (!dyg || code >= 0) && !(fabsf(dt) * te_wmax + te_bmax < kRevArg);
+  };
+  // fast path: no CSR candidates, and the filled slots are the newest ones in
+  // write order (oldest = slot write_pos % B) with strictly increasing times;
+  // then a candidate's rank is its write-order distance from the oldest filled slot
+  bool broken = true;
+  int order = 0;
+  const bool try_fast = live && ncsr == 0 && B > 0 && P.r_wp != nullptr;
+  if (try_fast) {
+    const int w = P.b_pow2 ? static_cast<int>(wp & (B - 1)) : static_cast<int>(wp % B);
+    order = sl - w < 0 ? sl - w + B : sl - w;
+    const uint64_t filled = (__ballot(sl < B && rid != -1) >> (h << lg)) & submask;
+    const int empty = B - __popcll(filled);
+    const int nxt = sl + 1 == B ? 0 : sl + 1;
+    const double tn = __shfl(rt, (h << lg) + nxt);
+    broken = sl < B && (((rid != -1) != (order >= empty)) || (rid != -1 && order < B - 1 && !(rt < tn)));
+    order -= empty;
+  }
+  const bool fast = try_fast && ((__ballot(broken) >> (h << lg)) & submask) == 0;
+  if (q >= 0) {
+    if (fast) {
+      if (v && order >= drop) emit(K - V + (order - drop), rid, rt, sl);
+    } else if (v) {
+      const int at = h * C + ncsr + __popcll(mine & ((uint64_t(1) << sl) - 1));
+      ct[at] = rt;
+      cid[at] = rid;
+      ccode[at] = sl;
     }
+  }
+  wave_sync();
+  if (q >= 0) {
+    if (!fast) {
+      for (int c = sl; c < ncand; c += Bp) {
+        const double tc = ct[h * C + c];
+        int r = 0;
+        for (int c2 = 0; c2 < ncand; ++c2) {
+          const double t2 = ct[h * C + c2];
+          r += (t2 < tc) || (t2 == tc && c2 < c);
+        }
+        if (r >= drop) emit(K - V + (r - drop), cid[h * C + c], tc, ccode[h * C + c]);
+      }
+    }
+    for (int p = sl; p < K - V; p += Bp) emit(p, -1, 0.0, -1);
   } else {
-    for (int p = lane; p < K; p += kWave) {
-      pid[p] = -1;
-      pcode[p] = -1;
+    for (int p = sl; p < K; p += Bp) {
+      pcode[h * K + p] = -1;
+      pid[h * K + p] = -1;
     }
   }
-  __syncthreads();
+  const bool te_big = __ballot(lane_big) != 0;
+  wave_sync();
 
-  if (active) {
-    // ---- feature rows: K rows x nch chunks of VEC bytes, lane-flattened ----
-    if (P.o_feats != nullptr && P.row_bytes > 0) {
-      const int nch = static_cast<int>(P.row_bytes / VEC);
-      const int64_t total = static_cast<int64_t>(K) * nch;
-      const int sp = kWave / nch, sc = kWave % nch;
-      int p = lane / nch, c = lane % nch;
-      uint8_t* obase = P.o_feats + q * K * P.row_bytes;
-      const uint8_t* rbase = B > 0 ? P.r_feats + ur * B * P.row_bytes : nullptr;
-      const uint8_t* cbase_f = P.has_csr ? P.c_feats + cbase * P.row_bytes : nullptr;
-      for (int64_t idx = lane; idx < total; idx += 4 * kWave) {
-        VT v[4];
-        VT* dptr[4];
+  // the wave's valid queries are consecutive from q0: output row q0*K + gp for
+  // wave position gp = h*K + p < np
+  const int64_t q0 = tq[0];
+  int nvalid = 0;
+  for (int hh = 0; hh < m; ++hh) nvalid += tq[hh] >= 0 ? 1 : 0;
+  if (q0 < 0) nvalid = 0;
+  const int np = nvalid * K;
+  const int64_t r0 = q0 * K;
+  const FastDiv dk(K);
+  const int ostart = part * kWave + lane;  // this wave's share of the output chunks
+  const int ostride = split * kWave;
+
+  // ---- edge ids into LDS (loads, before any store) ----
+  if (P.o_eids != nullptr) {
+    for (int gp = lane; gp < np; gp += kWave) {
+      const int hh = static_cast<int>(dk.div(gp));
+      const int code = pcode[gp];
+      int64_t e = -1;
+      if (code >= 0 && code < B)
+        e = P.r_eids != nullptr ? P.r_eids[tur[hh] * B + code] : -1;
+      else if (code >= B)
+        e = P.c_eids != nullptr ? P.c_eids[tcb[hh] + (code - B)] : -1;
+      pe[gp] = e;
+    }
+  }
+
+  auto store_te = [&]() {
+  // ---- time encoding ----
+  if (P.d_t > 0 && np > 0) {
+    if (te_big)
+      encode_rows<true, (NREG == 0)>(P, r0, np, pcode, pdt, s_w, s_b, ostart, ostride);
+    else
+      encode_rows<false, (NREG == 0)>(P, r0, np, pcode, pdt, s_w, s_b, ostart, ostride);
+  }
+
+  };
+  auto store_feats = [&]() {
+  // ---- feature rows: np rows x nch chunks of VEC bytes, one flat run ----
+  if (P.o_feats != nullptr && P.row_bytes > 0) {
+    const int nch = P.nch;
+    const int total = np * nch;
+    const FastDiv dv(nch);
+    VT* of = reinterpret_cast<VT*>(P.o_feats) + r0 * nch;
+    if constexpr (NREG > 0) {
+      // ring rows come from the lanes that loaded them, CSR rows from memory;
+      // every lane takes part in every shuffle
+      for (int b0 = part * kWave; b0 < total; b0 += ostride) {
+        const int idx = b0 + lane;
+        int gp = 0, c = 0, code = -1, hh = 0;
+        if (idx < total) {
+          gp = static_cast<int>(dv.div(idx));
+          c = idx - gp * nch;
+          hh = static_cast<int>(dk.div(gp));
+          code = pcode[gp];
+        }
+        const int srcl = (code >= 0 && code < B) ? (hh << lg) + code : lane;
+        VT val = VT{};
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          dptr[u] = nullptr;
-          v[u] = VT{};
-          if (idx + u * kWave < total) {
-            const int code = pcode[p];
+        for (int k = 0; k < NREG; ++k) {
+          const VT x = shfl_v(rows[k], srcl);
+          if (k == c) val = x;
+        }
+        if (idx < total) {
+          if (code < 0)
+            val = VT{};
+          else if (code >= B)
+            val = reinterpret_cast<const VT*>(P.c_feats + (tcb[hh] + (code - B)) * P.row_bytes)[c];
+          put<false>(of + idx, val);
+        }
+      }
+    } else {
+      for (int idx0 = part * kWave; idx0 < total; idx0 += kCopyDepth * ostride) {
+        VT v4[kCopyDepth];
+#pragma unroll
+        for (int u = 0; u < kCopyDepth; ++u) {
+          const int idx = idx0 + u * ostride + lane;
+          v4[u] = VT{};
+          if (idx < total) {
+            const int gp = static_cast<int>(dv.div(idx));
+            const int c = idx - gp * nch;
+            const int hh = static_cast<int>(dk.div(gp));
+            const int code = pcode[gp];
             if (code >= 0) {
-              const uint8_t* s = code < B ? rbase + static_cast<int64_t>(code) * P.row_bytes
-                                          : cbase_f + static_cast<int64_t>(code - B) * P.row_bytes;
-              v[u] = reinterpret_cast<const VT*>(s)[c];
+              const uint8_t* src = code < B ? P.r_feats + (tur[hh] * B + code) * P.row_bytes
+                                            : P.c_feats + (tcb[hh] + (code - B)) * P.row_bytes;
+              v4[u] = reinterpret_cast<const VT*>(src)[c];
             }
-            dptr[u] = reinterpret_cast<VT*>(obase + static_cast<int64_t>(p) * P.row_bytes) + c;
-          }
-          c += sc;
-          p += sp;
-          if (c >= nch) {
-            c -= nch;
-            ++p;
           }
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-          if (dptr[u] != nullptr) __builtin_nontemporal_store(v[u], dptr[u]);
-      }
-    }
-
-    // ---- time encoding: K rows x d_t ----
-    if (P.d_t > 0) {
-      const bool dyg = P.dt_mode == TGX_DT_DYGFORMER;
-      const bool has_b = P.te_b != nullptr;
-      float* tbase = P.o_te + q * K * static_cast<int64_t>(P.d_t);
-      if (P.te_vec4) {
-        const int nq = P.d_t / 4;
-        const int total = K * nq;
-        const int sp = kWave / nq, sc = kWave % nq;
-        int p = lane / nq, c = lane % nq;
-        const f32x4* w4 = reinterpret_cast<const f32x4*>(s_w);
-        const f32x4* b4 = reinterpret_cast<const f32x4*>(s_b);
-        f32x4* out4 = reinterpret_cast<f32x4*>(tbase);
-        for (int idx = lane; idx < total; idx += kWave) {
-          f32x4 o = {0.f, 0.f, 0.f, 0.f};
-          if (!dyg || pcode[p] >= 0) {
-            const float dt = pdt[p];
-            f32x4 a = dt * w4[c];
-            if (has_b) a = a + b4[c];
-            const float amax = fmaxf(fmaxf(fabsf(a[0]), fabsf(a[1])), fmaxf(fabsf(a[2]), fabsf(a[3])));
-            if (__builtin_expect(amax < kBigArg, 1)) {
-              o[0] = cos_fast(a[0]);
-              o[1] = cos_fast(a[1]);
-              o[2] = cos_fast(a[2]);
-              o[3] = cos_fast(a[3]);
-            } else {
-              o[0] = cos_slow(a[0]);
-              o[1] = cos_slow(a[1]);
-              o[2] = cos_slow(a[2]);
-              o[3] = cos_slow(a[3]);
-            }
-          }
-          __builtin_nontemporal_store(o, out4 + idx);
-          c += sc;
-          p += sp;
-          if (c >= nq) {
-            c -= nq;
-            ++p;
-          }
-        }
-      } else {
-        const int total = K * P.d_t;
-        for (int idx = lane; idx < total; idx += kWave) {
-          const int p = idx / P.d_t, j = idx - p * P.d_t;
-          float o = 0.f;
-          if (!dyg || pcode[p] >= 0) {
-            float a = pdt[p] * s_w[j];
-            if (has_b) a = a + s_b[j];
-            o = fabsf(a) < kBigArg ? cos_fast(a) : cos_slow(a);
-          }
-          tbase[static_cast<int64_t>(p) * P.d_t + j] = o;
+        for (int u = 0; u < kCopyDepth; ++u) {
+          const int idx = idx0 + u * ostride + lane;
+          if (idx < total) put<true>(of + idx, v4[u]);
         }
       }
     }
   }
 
-  // ---- co-occurrence of the group's (query 0, query 1) pair ----
+  };
+  auto store_ids = [&]() {
+  // ---- ids / times / mask / edge ids ----
+  for (int gp = ostart; gp < np; gp += ostride) {
+    const int64_t o = r0 + gp;
+    P.o_ids[o] = pid[gp];
+    P.o_times[o] = pt[gp];
+    P.o_mask[o] = pcode[gp] >= 0 ? 1 : 0;
+    if (P.o_eids != nullptr) P.o_eids[o] = pe[gp];
+  }
+
+  };
+  // Store order: with register-held rows there is nothing left to load, so the
+  // bulk (the encodings) goes first; with large rows the row copy loads first,
+  // before any encoding store can hold its loads back in vmcnt.
+  if constexpr (NREG > 0) {
+    store_te();
+    store_feats();
+  } else {
+    store_feats();
+    store_te();
+  }
+  store_ids();
+
+  // ---- co-occurrence of the plan group's (query 0, query 1) pair ----
   if (P.co_mode != TGX_CO_NONE) {
     __syncthreads();
     const int64_t qa = query_of(P, g, 0), qc = query_of(P, g, 1);
-    if (qa >= 0 && qc >= 0 && wv < 2) {
-      const int32_t* A = reinterpret_cast<const int32_t*>(smem + P.te_bytes + C * 16 + K * 8);
-      const int32_t* Cc =
-          reinterpret_cast<const int32_t*>(smem + P.te_bytes + P.wave_bytes + C * 16 + K * 8);
-      if (P.co_mode == TGX_CO_FREQ) {
-        const int32_t* X = wv == 0 ? A : Cc;
-        int32_t* out = wv == 0 ? P.co_a : P.co_c;
-        int pc = 0;
-        for (int i0 = 0; i0 < K; i0 += kWave) {
-          const int i = i0 + lane;
-          int32_t x = -1;
-          int na = 0, nc = 0;
-          if (i < K) {
-            x = X[i];
-            if (x != -1) {
-              for (int j = 0; j < K; ++j) {
-                na += A[j] == x;
-                nc += Cc[j] == x;
-              }
-            }
-            out[(g * K + i) * 2 + 0] = na;
-            out[(g * K + i) * 2 + 1] = nc;
-          }
-          pc += __popcll(__ballot(i < K && x != -1 && nc > 0));
-        }
-        if (wv == 0 && lane == 0 && P.co_pair != nullptr) P.co_pair[g] = static_cast<float>(pc);
-      } else {
-        // DyGFormer counts on A' = [node_a] ++ A, C' = [node_c] ++ C (length K+1)
-        const int32_t na0 = static_cast<int32_t>(query_node(P, qa));
-        const int32_t nc0 = static_cast<int32_t>(query_node(P, qc));
-        const int L = K + 1;
-        int32_t* out = wv == 0 ? P.co_a : P.co_c;
-        if (wv == 0 && P.co_pair != nullptr) {
-          // (B,) count over the K sequences, as in FREQ mode
-          int pc = 0;
-          for (int i0 = 0; i0 < K; i0 += kWave) {
-            const int i = i0 + lane;
-            bool hit = false;
-            if (i < K && A[i] != -1)
-              for (int j = 0; j < K && !hit; ++j) hit = Cc[j] == A[i];
-            pc += __popcll(__ballot(hit));
-          }
-          if (lane == 0) P.co_pair[g] = static_cast<float>(pc);
-        }
-        for (int i = lane; i < L; i += kWave) {
-          const int32_t ai = i == 0 ? na0 : A[i - 1];
-          const int32_t ci = i == 0 ? nc0 : Cc[i - 1];
-          int f0 = 0, f1 = 0;
-          if (wv == 0) {
-            if (ai != -1) {
-              for (int j = 0; j < L; ++j) {
-                const int32_t aj = j == 0 ? na0 : A[j - 1];
-                const int32_t cj = j == 0 ? nc0 : Cc[j - 1];
-                f0 += aj == ai;
-                f1 += (aj == ci) && (cj != -1);
-              }
-            }
-          } else {
-            if (ci != -1) {
-              for (int j = 0; j < L; ++j) {
-                const int32_t aj = j == 0 ? na0 : A[j - 1];
-                const int32_t cj = j == 0 ? nc0 : Cc[j - 1];
-                f0 += (cj == ai) && (aj != -1);
-                f1 += cj == ci;
-              }
-            }
-          }
-          out[(g * L + i) * 2 + 0] = f0;
-          out[(g * L + i) * 2 + 1] = f1;
-        }
-      }
+    if (qa >= 0 && qc >= 0 && wv == 0) {
+      const int32_t* A = reinterpret_cast<const int32_t*>(smem + P.te_bytes + P.off_pid);
+      const int32_t* Cc = reinterpret_cast<const int32_t*>(smem + P.te_bytes +
+                                                          static_cast<size_t>(split) * P.wave_bytes + P.off_pid);
+      co_occurrence_pair(P, g, qa, qc, A, Cc, lane);
     }
   }
 }
@@ -495,6 +745,31 @@ __global__ __launch_bounds__(64) void co_occurrence_rows(const int32_t* __restri
 
 int round16(int x) { return (x + 15) & ~15; }
 
+// Workgroups of `kern` (threads, lds bytes) resident on the current device at
+// once: CUs x occupancy, cached per (device, kernel, threads, lds).
+int resident_groups(const void* kern, int threads, size_t lds, int* out) {
+  static std::mutex mu;
+  static std::map<std::tuple<int, const void*, int, size_t>, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(TGX_ERR_HIP, "tgx_recent: hipGetDevice failed");
+  const auto key = std::make_tuple(dev, kern, threads, lds);
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(key);
+  if (it != cache.end()) {
+    *out = it->second;
+    return TGX_OK;
+  }
+  (void)hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  int cus = 0, per_cu = 0;
+  hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, lds);
+  if (e != hipSuccess) return fail(TGX_ERR_HIP, "tgx_recent: occupancy query: %s", hipGetErrorString(e));
+  const int n = (cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1);
+  cache.emplace(key, n);
+  *out = n;
+  return TGX_OK;
+}
+
 }  // namespace
 }  // namespace tgx
 
@@ -536,6 +811,8 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
     P.r_times = ring->times;
     P.r_feats = static_cast<const uint8_t*>(ring->feats);
     P.r_eids = ring->eids;
+    P.r_wp = ring->write_pos;
+    P.b_pow2 = (P.B & (P.B - 1)) == 0 ? 1 : 0;
     feat_dim = ring->feat_dim;
     dtype = ring->feat_dtype;
   }
@@ -620,10 +897,55 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
   P.status = a->status;
 
   const int K = a->k;
-  P.cand_cap = K + P.B;
+  P.cand_cap = (P.has_csr ? K : 0) + P.B;
+  auto wave_lds = [&](int m) {
+    return round16(m * P.cand_cap * 16) + round16(m * K * 4) * 3 + round16(m * K * 8) * 2 + round16(m * 24);
+  };
+  // Queries per wave.  Packing m = 64 / Bp queries into sub-groups of Bp >= B
+  // lanes (Bp at least 16, the wave's LDS within 12 KB) pays off only when the
+  // rows ride in registers and the batch has more queries than the device has
+  // wave slots (one round of waves instead of two); otherwise, and with a plan,
+  // one query per wave keeps the most waves in flight.
+  const bool small_rows = P.B > 0 && a->out_feats != nullptr && P.row_bytes > 0 &&
+                          P.row_bytes <= 64 && P.row_bytes % 16 == 0;
+  int lg = 6;
+  if (a->plan == nullptr && small_rows && a->num_queries > kPackMinQueries) {
+    lg = 4;
+    while ((1 << lg) < P.B) ++lg;
+    while (lg < 6 && wave_lds(kWave >> lg) > 12 * 1024) ++lg;
+  }
+  P.m = kWave >> lg;
+  P.lg_bp = lg;
   P.te_bytes = 2 * round16(a->d_t * 4);
-  P.wave_bytes = round16(P.cand_cap * 16 + K * 12);
-  const size_t lds = static_cast<size_t>(P.te_bytes) + static_cast<size_t>(a->group) * P.wave_bytes;
+  P.off_cid = round16(P.m * P.cand_cap * 8);
+  P.off_code = P.off_cid + round16(P.m * P.cand_cap * 4);
+  P.off_pcode = P.off_code + round16(P.m * P.cand_cap * 4);
+  P.off_pdt = P.off_pcode + round16(P.m * K * 4);
+  P.off_pid = P.off_pdt + round16(P.m * K * 4);
+  P.off_pt = P.off_pid + round16(P.m * K * 4);
+  P.off_pe = P.off_pt + round16(P.m * K * 8);
+  P.off_tab = P.off_pe + round16(P.m * K * 8);
+  P.wave_bytes = P.off_tab + round16(P.m * 24);
+  // split: with one query per wave and fewer queries than wave slots, up to 8
+  // waves share each query's outputs.  A workgroup holds at most kMaxWaves waves
+  // (the kernel's launch bound): the plan group times split, else 8 / split
+  // query slots.
+  int split = 1;
+  const int gmin = a->plan != nullptr ? a->group : 1;
+  if (P.m == 1)
+    while (split < 8 && a->num_queries * (split * 2) <= kPackMinQueries && gmin * split * 2 <= kMaxWaves)
+      split *= 2;
+  P.split = split;
+  const int qslots = a->plan != nullptr ? a->group : (split > 1 ? kMaxWaves / split : 4);
+  const int waves = qslots * split;
+  if (waves < 1 || waves > kMaxWaves)
+    return fail(TGX_ERR_LIMIT, "tgx_recent: %d wavefronts per workgroup outside [1, %d]", waves, kMaxWaves);
+  int64_t nblocks = a->num_groups;
+  if (a->plan == nullptr) {
+    const int64_t ntiles = (a->num_queries + P.m - 1) / P.m;
+    nblocks = (ntiles + qslots - 1) / qslots;
+  }
+  const size_t lds = static_cast<size_t>(P.te_bytes) + static_cast<size_t>(waves) * P.wave_bytes;
   if (lds > 160 * 1024) return fail(TGX_ERR_LIMIT, "tgx_recent: %zu bytes of LDS needed", lds);
 
   int vec = 2;
@@ -633,34 +955,46 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
     vec = 16;
   else if (P.row_bytes % 4 == 0 && (!fe || (al(P.r_feats, 3) && al(P.c_feats, 3) && al(P.o_feats, 3))))
     vec = 4;
+  P.nch = static_cast<int>(P.row_bytes / vec);
+  // rows of at most 4 16-byte chunks ride in registers with the ring slot
+  int nreg = 0;
+  if (vec == 16 && fe && P.B > 0) nreg = P.nch <= 2 ? 2 : (P.nch <= 4 ? 4 : 0);
 
   hipEvent_t ev0 = static_cast<hipEvent_t>(a->timing_start);
   hipEvent_t ev1 = static_cast<hipEvent_t>(a->timing_stop);
   if ((ev0 == nullptr) != (ev1 == nullptr))
     return fail(TGX_ERR_ARG, "tgx_recent: timing_start and timing_stop must both be set or both NULL");
-  const dim3 grid(static_cast<unsigned>(a->num_groups));
-  const dim3 block(kWave * a->group);
-  static bool attr_done = false;
-  if (!attr_done) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(recent_fused<16>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(recent_fused<4>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(recent_fused<2>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+
+  const dim3 grid(static_cast<unsigned>(nblocks));
+  const dim3 block(kWave * waves);
+  static std::once_flag attr_once;
+  std::call_once(attr_once, [] {
+    const void* fns[] = {reinterpret_cast<const void*>(recent_fused<16, 0>),
+                         reinterpret_cast<const void*>(recent_fused<16, 2>),
+                         reinterpret_cast<const void*>(recent_fused<16, 4>),
+                         reinterpret_cast<const void*>(recent_fused<4, 0>),
+                         reinterpret_cast<const void*>(recent_fused<2, 0>)};
+    for (const void* f : fns)
+      (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     (void)hipGetLastError();
-    attr_done = true;
-  }
-  switch (vec) {
-    case 16:
-      hipExtLaunchKernelGGL(recent_fused<16>, grid, block, lds, stream, ev0, ev1, 0, P);
-      break;
-    case 4:
-      hipExtLaunchKernelGGL(recent_fused<4>, grid, block, lds, stream, ev0, ev1, 0, P);
-      break;
-    default:
-      hipExtLaunchKernelGGL(recent_fused<2>, grid, block, lds, stream, ev0, ev1, 0, P);
-      break;
+  });
+  auto launch = [&](auto kernel) {
+    if (ev0 != nullptr)
+      hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, ev0, ev1, 0, P);
+    else
+      hipLaunchKernelGGL(kernel, grid, block, lds, stream, P);
+  };
+  if (vec == 16) {
+    if (nreg == 2)
+      launch(recent_fused<16, 2>);
+    else if (nreg == 4)
+      launch(recent_fused<16, 4>);
+    else
+      launch(recent_fused<16, 0>);
+  } else if (vec == 4) {
+    launch(recent_fused<4, 0>);
+  } else {
+    launch(recent_fused<2, 0>);
   }
   return check_launch("recent_fused");
 }
