@@ -4,14 +4,16 @@ A step is one pass of the hot path over one batch of the synthetic stream:
 ``DataPipeline.prepare(batch i)`` (fused gather + feature rows + 100-d cosine
 time encoding [+ co-occurrence]) followed by ``TemporalGraph.advance(batch i)``
 (ring update), on a graph created empty -- the BASELINE streaming regime.  The
-whole stream window (W warm-up + K timed batches) is staged in HBM before the
-timed region.
+whole stream window is staged in HBM before timing.
 
-Reported (one JSON line): whole-job prepared queries/s over the timed steps,
-plus the prepare kernel's roofline (algorithmic bytes per launch over the mean
-launch time, from HIP events on the launch stream) and the CPU baseline: the
-torch-CPU restatement of the reference path run on the same ring state for a
-bounded window of following batches (its outputs must equal the GPU's).
+Batches: W warm-up, then the timed region of K steps (``value`` = prepared
+queries/s over its wall clock between two device synchronisations, nothing but
+the hot path inside), then a roofline window: the fused prepare kernels of the
+next R batches on the ring state the timed region left, captured in a HIP graph
+and replayed between two HIP events on the launch stream; ``roofline.achieved``
+= algorithmic bytes per launch over the mean launch time.  Then the CPU baseline: the torch-CPU restatement of the reference
+path run on the same ring state for a bounded window of following batches (its
+outputs must equal the GPU's).
 """
 from __future__ import annotations
 
@@ -39,34 +41,6 @@ def bytes_per_batch(cfg, Q: int, V: int, pairs: int, d_t: int = 100) -> int:
     r = Q * (16 + B * 12) + V * d * s_f
     w = Q * (K * 13 + K * d * s_f + K * d_t * 4)
     return int(r + w + pairs * 16 * K)
-
-
-class EventTimer:
-    """Pairs of HIP events handed to tgx_recent, which has the kernel dispatch
-    itself record its start and end on them (hipExtLaunchKernelGGL)."""
-
-    def __init__(self, torch, n):
-        self.torch = torch
-        self.pairs = []
-        self.free = []
-        for _ in range(n):
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
-            e0.record()
-            e1.record()  # materialise the hipEvent_t handles
-            self.free.append((e0, e1))
-        torch.cuda.synchronize()
-        self.active = False
-
-    def events(self):
-        if not self.active or not self.free:
-            return 0, 0
-        e0, e1 = self.free.pop()
-        self.pairs.append((e0, e1))
-        return e0.cuda_event, e1.cuda_event
-
-    def total_ms(self):
-        return sum(a.elapsed_time(b) for a, b in self.pairs)
 
 
 def stage_stream(cfg, first: int, count: int, torch, device):
@@ -148,6 +122,8 @@ def main():
     ap.add_argument("--queries-per-workgroup", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quiet", action="store_true")
+    ap.add_argument("--roofline-steps", type=int, default=200,
+                    help="batches after the timed region whose prepare kernels are timed back to back")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after timing, run a plain device copy of this size (PMC byte calibration)")
     a = ap.parse_args()
@@ -164,9 +140,12 @@ def main():
     cfg = CONFIGS[a.config]
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
-    total = min(a.warmup + a.steps, num_batches(cfg))
-    W = min(a.warmup, total - a.steps) if total > a.steps else 0
-    K = total - W
+    # batches: W warm-up, K timed (value), R roofline window (kernel-dispatch events)
+    avail = num_batches(cfg)
+    K = min(a.steps, avail)
+    R = min(a.roofline_steps, max(0, avail - K))
+    W = min(a.warmup, max(0, avail - K - R))
+    total = W + K + R
     t0 = time.time()
     dev, lens, bts = stage_stream(cfg, 0, total, torch, device)
     log(f"{cfg.name}: staged {total} batches ({sum(lens)} events) in {time.time() - t0:.1f}s")
@@ -189,20 +168,18 @@ def main():
                         edge_feat=dev["feat"][s:e], neg=neg)
 
     raws = [raw(i) for i in range(total)]
-    timer = EventTimer(torch, K)
-    g.kernel_timer = timer
     for i in range(W):
         pipe.prepare(raws[i])
         g.advance(raws[i].src, raws[i].dst, raws[i].time, raws[i].edge_feat)
     torch.cuda.synchronize()
     log(f"warm-up {W} batches done")
 
+    # timed region: K steps, nothing but the hot path between the synchronisations
     masks = []
-    timer.active = True
     host_prep = host_adv = 0.0
     torch.cuda.synchronize()
     t_start = time.perf_counter()
-    for i in range(W, total):
+    for i in range(W, W + K):
         h0 = time.perf_counter()
         pb = pipe.prepare(raws[i])
         h1 = time.perf_counter()
@@ -212,24 +189,56 @@ def main():
         host_prep += h1 - h0
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_start
-    timer.active = False
-    kern_ms = timer.total_ms()
-    n_launch = len(timer.pairs)
+
+    # roofline window: the prepare kernels of the next R batches of the stream on the
+    # ring state the timed region left, captured once in a HIP graph and replayed
+    # between two HIP events on the launch stream, so the kernels run back to back
+    # with no host in the loop (a dispatch that records its own timing events runs
+    # measurably slower, and a Python launch loop cannot keep up with the kernel)
+    rmasks = []
+    kern_ms = 0.0
+    if R:
+        args = pipe.launch_args(raws[W + K])
+        eager = [int(sum(int(m.sum()) for m in pipe.launch(raws[i], args)["mask"]))
+                 for i in range(W + K, min(W + K + 3, total))]
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(W + K, total):
+                rmasks.append(tuple(pipe.launch(raws[i], args)["mask"]))
+        graph.replay()  # first replay uploads the graph
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        kern_ms = e0.elapsed_time(e1)
+        replayed = [int(sum(int(m.sum()) for m in ms)) for ms in rmasks[:len(eager)]]
+        if replayed != eager:
+            raise RuntimeError(f"graph replay disagrees with eager launches: {replayed} vs {eager}")
+        del graph
+    n_launch = max(R, 1)
     st = g.status()
     if any(st.values()):
         raise RuntimeError(f"device diagnostics: {st}")
 
-    Qs = [int(sum(m.shape[0] for m in ms)) for ms in masks]
-    Vs = [int(sum(int(m.sum()) for m in ms)) for ms in masks]
-    pairs = [lens[W + j] if cfg.co_occurrence else 0 for j in range(K)]
-    byts = [bytes_per_batch(cfg, Qs[j], Vs[j], pairs[j]) for j in range(K)]
+    def algo_bytes(mask_list, first):
+        qs = [int(sum(m.shape[0] for m in ms)) for ms in mask_list]
+        vs = [int(sum(int(m.sum()) for m in ms)) for ms in mask_list]
+        prs = [lens[first + j] if cfg.co_occurrence else 0 for j in range(len(mask_list))]
+        return qs, vs, [bytes_per_batch(cfg, qs[j], vs[j], prs[j]) for j in range(len(mask_list))]
+
+    Qs, Vs, _ = algo_bytes(masks, W)
+    rQs, rVs, rbyts = algo_bytes(rmasks, W + K)
     total_q = sum(Qs)
     value = total_q / wall
     avg_launch_s = kern_ms / 1e3 / n_launch
-    achieved = sum(byts) / n_launch / avg_launch_s / 1e9
-    log(f"timed {K} steps: wall {wall * 1e3:.1f} ms, prepare kernel {kern_ms:.2f} ms "
-        f"({avg_launch_s * 1e6:.1f} us/launch), {achieved:.0f} GB/s, mean V/query "
-        f"{sum(Vs) / total_q:.2f}")
+    achieved = sum(rbyts) / n_launch / avg_launch_s / 1e9 if rbyts else 0.0
+    log(f"timed {K} steps: wall {wall * 1e3:.1f} ms ({wall / K * 1e6:.1f} us/step); roofline window "
+        f"{R} launches: {avg_launch_s * 1e6:.2f} us/launch, {achieved:.0f} GB/s, mean V/query "
+        f"{sum(rVs) / max(sum(rQs), 1):.2f}")
 
     if a.copy_calibration_mib > 0:
         n = a.copy_calibration_mib << 20
@@ -246,7 +255,7 @@ def main():
         traffic = json.loads(pmc.read_text()).get("traffic_bytes_per_launch")
 
     cpu = None
-    if not a.no_cpu and total < num_batches(cfg):
+    if not a.no_cpu and total < avail:
         cpu = cpu_baseline(cfg, g, pipe, total, a.cpu_seconds, torch, log, num_batches(cfg))
 
     line = {
@@ -259,13 +268,18 @@ def main():
                                f"K={cfg.k}, B={cfg.buffer_size}, d={cfg.feat_dim} {cfg.feat_dtype}, "
                                f"{cfg.queries_per_event} queries/event, d_t=100"
                                + (", co-occurrence" if cfg.co_occurrence else ""),
-                   "batches_timed": f"{W}..{total - 1}", "events_per_batch": cfg.batch},
+                   "batches_timed": f"{W}..{W + K - 1}", "events_per_batch": cfg.batch},
         "host_us_per_step": {"prepare": host_prep / K * 1e6, "advance": host_adv / K * 1e6},
-        "prepare_kernel": {"queries_per_s": total_q / (kern_ms / 1e3), "us_per_launch":
-                           avg_launch_s * 1e6, "mean_valid_per_query": sum(Vs) / total_q,
-                           "bytes_per_launch": sum(byts) / n_launch},
+        "prepare_kernel": {"us_per_launch": avg_launch_s * 1e6, "launches": n_launch,
+                           "batches": f"{W + K}..{total - 1}",
+                           "queries_per_s": sum(rQs) / (kern_ms / 1e3) if kern_ms else None,
+                           "mean_valid_per_query": sum(rVs) / max(sum(rQs), 1),
+                           "bytes_per_launch": sum(rbyts) / n_launch},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": achieved / PEAK_HBM_GBS, "traffic": traffic},
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
+                     "kernel": "recent_fused",
+                     "timing": f"HIP event pair around a graph replay of the {R} launches of "
+                               f"batches {W + K}..{total - 1}"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -87,15 +87,12 @@ class DataPipeline:
         return t
 
     # -- prepare -------------------------------------------------------------
-    def prepare(self, raw_batch: RawBatch) -> PreparedBatch:
-        spec = self.spec
-        k, k2 = spec.neighbors.k, spec.neighbors.k2
-        fn = spec.neighbors.for_nodes
-        device = raw_batch.device
+    def _query_groups(self, raw_batch: RawBatch):
+        """Query groups in the reference order [src, dst, neg (row-major), neg_src],
+        read in place by the kernel: names, (nodes, times, negatives per event),
+        sizes and negatives per event (pipeline/__init__.py:40-70)."""
+        fn = self.spec.neighbors.for_nodes
         b = raw_batch.src.shape[0]
-
-        # query groups in the reference order [src, dst, neg (row-major), neg_src],
-        # read in place by the kernel: (nodes, times, negatives per event)
         names, qgroups, sizes, per_event = [], [], [], []
         if "src" in fn:
             names.append("src"); qgroups.append((raw_batch.src, raw_batch.time, 1))
@@ -111,6 +108,37 @@ class DataPipeline:
         if "neg" in fn and raw_batch.neg_src is not None:
             names.append("neg_src"); qgroups.append((raw_batch.neg_src, raw_batch.time, 1))
             sizes.append(b); per_event.append(1)
+        return names, qgroups, sizes, per_event
+
+    def launch_args(self, raw_batch: RawBatch) -> tuple:
+        """(d_t, te_w, te_b, dt_mode, co_mode) of the fused launch for this spec."""
+        spec = self.spec
+        fn = spec.neighbors.for_nodes
+        want_co = spec.co_occurrence and "src" in fn and "dst" in fn
+        co_mode = _CO_MODES[spec.co_occurrence_mode] if want_co else _lib.TGX_CO_NONE
+        d_t = int(spec.time_encoding)
+        te_w = te_b = None
+        if d_t > 0:
+            te_w, te_b = self._te_params(d_t)
+        return d_t, te_w, te_b, _DT_MODES[spec.dt_mode], co_mode
+
+    def launch(self, raw_batch: RawBatch, args: Optional[tuple] = None) -> dict:
+        """The one fused tgx_recent launch of ``prepare`` (1-hop), returning its raw
+        output views (lists per query group) without building a PreparedBatch;
+        for timing loops that must not be host-bound."""
+        names, qgroups, _, per_event = self._query_groups(raw_batch)
+        d_t, te_w, te_b, dt_mode, co_mode = args if args is not None else self.launch_args(raw_batch)
+        if "src" not in names or "dst" not in names:
+            co_mode = _lib.TGX_CO_NONE
+        return self._fused(qgroups, self.spec.neighbors.k, raw_batch.src.shape[0], per_event, d_t,
+                           te_w, te_b, dt_mode, co_mode)
+
+    def prepare(self, raw_batch: RawBatch) -> PreparedBatch:
+        spec = self.spec
+        k, k2 = spec.neighbors.k, spec.neighbors.k2
+        device = raw_batch.device
+        b = raw_batch.src.shape[0]
+        names, qgroups, sizes, per_event = self._query_groups(raw_batch)
 
         if spec.edge_ids and not self.graph.track_edge_ids:
             raise ValueError("GatherSpec.edge_ids needs a TemporalGraph built with track_edge_ids=True")
