@@ -547,9 +547,15 @@ __global__ __launch_bounds__(kMaxWaves * kWave) __attribute__((amdgpu_waves_per_
       for (int c = sl; c < ncand; c += Bp) {
         const double tc = ct[h * C + c];
         int r = 0;
-        for (int c2 = 0; c2 < ncand; ++c2) {
-          const double t2 = ct[h * C + c2];
-          r += (t2 < tc) || (t2 == tc && c2 < c);
+        for (int c0 = 0; c0 < ncand; c0 += 4) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int c2 = c0 + u;
+            if (c2 < ncand) {
+              const double t2 = ct[h * C + c2];
+              r += (t2 < tc) || (t2 == tc && c2 < c);
+            }
+          }
         }
         if (r >= drop) emit(K - V + (r - drop), cid[h * C + c], tc, ccode[h * C + c]);
       }
