@@ -14,7 +14,8 @@
  * Reference interfaces replaced (paths relative to the tgengine checkout):
  *   tgx_ring_append   <- TemporalGraph.advance post-freeze branch
  *                        tgengine/core/temporal_graph.py:123-129 and
- *                        _append_overflow :351-387 (pure torch there; no native op)
+ *                        _append_overflow :351-387 (pure torch there; no native op);
+ *                        tgx_ring_plan / tgx_ring_commit / tgx_ring_discard split it
  *   tgx_recent        <- TemporalGraph.recent :183-349 (ring merge _merge_overflow
  *                        :307-349, CSR window :241-305) and the pybind op
  *                        temporal_recent_k (tgengine/core/csrc/temporal_sample.cu:291-329,
@@ -37,7 +38,7 @@
 extern "C" {
 #endif
 
-#define TGX_ABI_VERSION 4
+#define TGX_ABI_VERSION 5
 
 /* status codes */
 #define TGX_OK 0
@@ -171,6 +172,27 @@ int tgx_ring_append(const tgx_ring* ring, const int64_t* src, const int64_t* dst
                     void* workspace, size_t workspace_bytes, int32_t* status, void* stream);
 size_t tgx_ring_append_workspace_size(int64_t b);
 size_t tgx_ring_scratch_size(int64_t num_nodes);
+
+/* tgx_ring_append in two halves, so the first can run while other work still
+ * reads the ring (the same split of _append_overflow, temporal_graph.py:351-387):
+ *   tgx_ring_plan   : per-node counts and the entry lists of the batch, in the
+ *                     workspace and the ring's scratch; reads src/dst/time, never
+ *                     the ring arrays.  Needs the scratch counters at zero (as
+ *                     every commit or discard leaves them).
+ *   tgx_ring_commit : the ring writes of a planned batch (same arguments and
+ *                     workspace as its plan); restores the counters; reports the
+ *                     plan's diagnostics into `status`.
+ *   tgx_ring_discard: drops a planned batch without touching the ring arrays and
+ *                     restores the counters.
+ * Plan, then exactly one of commit / discard, ordered on streams by the caller. */
+int tgx_ring_plan(const tgx_ring* ring, const int64_t* src, const int64_t* dst,
+                  const double* time, int64_t b, void* workspace, size_t workspace_bytes,
+                  void* stream);
+int tgx_ring_commit(const tgx_ring* ring, const int64_t* src, const int64_t* dst,
+                    const double* time, const void* feat, int64_t b, int64_t eid_base,
+                    void* workspace, size_t workspace_bytes, int32_t* status, void* stream);
+int tgx_ring_discard(const tgx_ring* ring, const int64_t* src, const int64_t* dst, int64_t b,
+                     void* workspace, size_t workspace_bytes, void* stream);
 
 /* Fused most-recent-K gather (+ time encoding, + co-occurrence) (kernels b, c).
  * ring and/or csr may be NULL (no candidates from that store). */

@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(L, n), n
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
-    assert L.tgx_abi_version() == 4
+    assert L.tgx_abi_version() == 5
     nm = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
                         text=True).stdout
     exported = set(re.findall(r"\bT (tgx_\w+)", nm))
@@ -142,12 +142,37 @@ def test_ring_append_argument_checks():
     assert L.tgx_ring_append(ctypes.byref(ring), 8, 8, 8, None, 4, 0, ws, 1 << 16, None, None) == 3
 
 
+def test_ring_plan_commit_discard_argument_checks():
+    L = _lib.lib()
+    ws = ctypes.create_string_buffer(1 << 16)
+    ring = _lib.TgxRing(num_nodes=10, slots=4, feat_dim=2, feat_dtype=0, ids=8, times=8, feats=8,
+                        write_pos=8, scratch=8)
+    r = ctypes.byref(ring)
+    assert L.tgx_ring_plan(None, 8, 8, 8, 4, ws, 1 << 16, None) == 1
+    assert L.tgx_ring_commit(None, 8, 8, 8, None, 4, 0, ws, 1 << 16, None, None) == 1
+    assert L.tgx_ring_discard(None, 8, 8, 4, ws, 1 << 16, None) == 1
+    # empty batches are no-ops for every half
+    assert L.tgx_ring_plan(r, 8, 8, 8, 0, None, 0, None) == 0
+    assert L.tgx_ring_commit(r, 8, 8, 8, None, 0, 0, None, 0, None, None) == 0
+    assert L.tgx_ring_discard(r, 8, 8, 0, None, 0, None) == 0
+    # the plan needs times, the discard does not
+    assert L.tgx_ring_plan(r, 8, 8, None, 4, ws, 1 << 16, None) == 1
+    assert "tgx_ring_plan" in _err()
+    need = L.tgx_ring_append_workspace_size(4)
+    assert L.tgx_ring_discard(r, 8, 8, 4, ws, need - 1, None) == 1
+    assert "workspace" in _err()
+    ring.slots = 65
+    assert L.tgx_ring_commit(r, 8, 8, 8, None, 4, 0, ws, 1 << 16, None, None) == 3
+
+
 def test_size_queries():
     L = _lib.lib()
-    assert L.tgx_ring_scratch_size(1000) == (2 * 1000 + 16) * 4
+    # per-node counter + 8-entry node list, and 16 control words
+    assert L.tgx_ring_scratch_size(1000) == (9 * 1000 + 16) * 4
     n = 2 * 4000
     ws = L.tgx_ring_append_workspace_size(4000)
-    assert ws >= 4 * n * 2 + 4 * (n // 2 + 1) + 4 * (n // 65 + 1)
+    # tickets, 8-byte overflow pairs (or lists), groups, large groups
+    assert ws >= 4 * n + 8 * n + 4 * (n // 2 + 1) + 4 * (n // 65 + 1)
     assert L.tgx_ring_append_workspace_size(0) > 0
 
 

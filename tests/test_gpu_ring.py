@@ -1,10 +1,14 @@
 """Ring update (tgx_ring_append through TemporalGraph.advance) against the oracle.
 
 Bit-exact comparison of ids, times, feature rows, write positions and edge ids
-after every batch, over shapes that reach every code path of the kernel:
-singleton nodes, small groups (2..64 entries), large groups (> 64 entries, one
-or several 8192-index bitmap windows), B not a power of two, bf16 rows of odd
-width, zero-width rows, invalid node ids, and batches larger than 16384 entries.
+after every batch, over shapes that reach every code path of both update
+designs: the two-launch path (batches of up to 32768 entries: singletons,
+groups of up to 8 entries ranked from the node lists, larger groups from the
+lists plus the overflow array over one or several 8192-index bitmap windows)
+and the four-launch path (larger batches: small groups of 2..64 entries, large
+groups over one or several windows), plus B not a power of two, bf16 rows of
+odd width, zero-width rows, invalid node ids and the size boundary between the
+two paths.
 """
 import numpy as np
 import pytest
@@ -131,6 +135,45 @@ def test_ring_batch_larger_than_16384_entries():
     _run(6, 300_000, 32, 8, True, _hot(300_000, 12000, 2, 0.05))
 
 
+def _windows_gen(b, nb):
+    """Nodes 3 and 4 with > 64 entries spread over several 8192-index windows,
+    the rest groups of a few entries each."""
+    def gen(rng):
+        for _ in range(nb):
+            src = rng.integers(100, 5000, b)
+            dst = rng.integers(100, 5000, b)
+            src[:: b // 60] = 3
+            dst[-5::-97] = 4
+            yield src, dst
+    return gen
+
+
+def test_ring_two_launch_large_group_many_windows():
+    # 16000 events = 32000 entries: the two-launch path, four bitmap windows
+    _run(8, 5000, 64, 4, False, _windows_gen(16000, 2))
+
+
+@pytest.mark.parametrize("b", [16384, 16385])
+def test_ring_two_and_four_launch_size_boundary(b):
+    # 32768 entries (last two-launch size) and 32770 (first four-launch size)
+    _run(9, 20_000, 32, 8, True, _windows_gen(b, 2))
+
+
+def test_ring_list_capacity_edges():
+    """Groups of exactly 7, 8, 9 and 10 entries (a full node list, and the first
+    overflow entries) next to singletons, for B below and above the group size."""
+    def gen(rng):
+        for _ in range(4):
+            nodes = np.concatenate([np.repeat(np.arange(4), [7, 8, 9, 10]),
+                                    rng.integers(10, 1000, 266)])
+            rng.shuffle(nodes)
+            src = nodes[:150]
+            dst = nodes[150:]
+            yield src, dst
+    for B in (4, 8, 9, 16):
+        _run(10, 1000, B, 8, False, gen)
+
+
 def test_ring_invalid_ids_are_skipped_and_flagged():
     rng = np.random.default_rng(7)
     N, B, d = 20, 4, 2
@@ -180,3 +223,117 @@ def test_ring_zero_features_when_edge_feat_is_none():
     g.advance(torch.from_numpy(src).cuda(), torch.from_numpy(dst).cuda(), torch.from_numpy(time).cuda())
     O.ring_advance(ring, src, dst, time, np.zeros((64, 6), np.float32))
     _compare(g, ring, "no feats")
+
+
+# ------------------------------------------------------------- planned updates
+# DataPipeline.prepare starts the ring update of its batch on a side stream
+# (TemporalGraph.plan_append); advance() commits the plan when it receives the
+# same src/dst/time tensors, otherwise discards it.  Every path must leave the
+# ring exactly as the oracle's update, with the node counters back at zero.
+
+def _stream_batches(rng, N, n_batches, b, hot=3):
+    out = []
+    for bi in range(n_batches):
+        src = rng.integers(0, N, b)
+        dst = rng.integers(0, N, b)
+        src[: b // 4] = rng.integers(0, hot, b // 4)  # repeated nodes -> small/large groups
+        t0 = 10.0 * (2 * b + 10) * (bi + 1)
+        time = t0 + np.cumsum(rng.exponential(1.0, b) + 1e-3)
+        out.append((src.astype(np.int64), dst.astype(np.int64), time))
+    return out
+
+
+def _dev(src, dst, time, feat, bf16):
+    return (torch.from_numpy(src).cuda(), torch.from_numpy(dst).cuda(), torch.from_numpy(time).cuda(),
+            _to_dev(feat, bf16))
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_planned_updates_match_the_oracle(bf16):
+    rng = np.random.default_rng(41)
+    N, B, d = 300, 8, 8 if bf16 else 6
+    g, ring = _graph_and_ring(N, B, d, bf16)
+    for bi, (src, dst, time) in enumerate(_stream_batches(rng, N, 6, 700)):
+        feat = _feat(rng, len(src), d, bf16)
+        s, t_dst, t, f = _dev(src, dst, time, feat, bf16)
+        assert g.plan_append(s, t_dst, t) == (bi > 0)  # the ring exists from the first advance on
+        g.advance(s, t_dst, t, f)
+        O.ring_advance(ring, src, dst, time, feat)
+        _compare(g, ring, f"planned batch {bi}")
+    assert all(v == 0 for v in g.status().values())
+
+
+@pytest.mark.parametrize("b,nb", [(300, 5), (17000, 2)])  # two- and four-launch paths
+def test_plan_discarded_when_advance_gets_other_tensors(b, nb):
+    rng = np.random.default_rng(42)
+    N, B, d = 200, 4, 4
+    g, ring = _graph_and_ring(N, B, d, False)
+    batches = _stream_batches(rng, N, nb, b)
+    for bi, (src, dst, time) in enumerate(batches):
+        feat = _feat(rng, len(src), d, False)
+        s, t_dst, t, f = _dev(src, dst, time, feat, False)
+        g.plan_append(s, t_dst, t)
+        if bi % 2:
+            # equal values in other tensors: the plan is dropped, the batch still applies
+            g.advance(s.clone(), t_dst.clone(), t.clone(), f)
+        else:
+            # a plan for a batch that never comes, then the real one
+            other = _stream_batches(rng, N, 1, b)[0]
+            o = _dev(*other, _feat(rng, b, d, False), False)
+            g.plan_append(o[0], o[1], o[2])
+            g.advance(s, t_dst, t, f)
+        O.ring_advance(ring, src, dst, time, feat)
+        _compare(g, ring, f"batch {bi}")
+    assert all(v == 0 for v in g.status().values())
+
+
+def test_plan_sees_in_place_changes_and_reports_status_once():
+    rng = np.random.default_rng(43)
+    N, B, d = 100, 4, 2
+    g, ring = _graph_and_ring(N, B, d, False)
+    (src, dst, time), (src2, dst2, time2) = _stream_batches(rng, N, 2, 200)
+    feat = _feat(rng, 200, d, False)
+    s, t_dst, t, f = _dev(src, dst, time, feat, False)
+    g.advance(s, t_dst, t, f)  # allocates the ring
+    O.ring_advance(ring, src, dst, time, feat)
+    # plan a batch, then change it in place: the version counter forces a re-plan
+    feat2 = _feat(rng, 200, d, False)
+    s2, d2, t2, f2 = _dev(src2, dst2, time2, feat2, False)
+    g.plan_append(s2, d2, t2)
+    src2 = src2.copy()
+    src2[:10] = np.arange(10)
+    s2[:10] = torch.arange(10, device="cuda")
+    g.advance(s2, d2, t2, f2)
+    O.ring_advance(ring, src2, dst2, time2, feat2)
+    _compare(g, ring, "after in-place change")
+    # out-of-range node ids in a planned batch are reported once, at the commit
+    (src3, dst3, time3), = _stream_batches(rng, N, 1, 200)
+    src3 = src3.copy()
+    src3[:3] = N + 5
+    feat3 = _feat(rng, 200, d, False)
+    s3, d3, t3, f3 = _dev(src3, dst3, time3, feat3, False)
+    g.plan_append(s3, d3, t3)
+    g.advance(s3, d3, t3, f3)
+    assert g.status()["bad_event_nodes"] == 3
+    N_ = g.num_nodes
+    assert int(g._ov_scratch[:N_].abs().sum()) == 0
+
+
+def test_restore_and_reset_drop_a_pending_plan():
+    rng = np.random.default_rng(44)
+    N, B, d = 80, 4, 2
+    g, ring = _graph_and_ring(N, B, d, False)
+    (a, b_, c), (a2, b2, c2) = _stream_batches(rng, N, 2, 100)
+    feat = _feat(rng, 100, d, False)
+    s, t_dst, t, f = _dev(a, b_, c, feat, False)
+    g.advance(s, t_dst, t, f)
+    O.ring_advance(ring, a, b_, c, feat)
+    snap = g.snapshot()
+    s2, d2, t2, f2 = _dev(a2, b2, c2, _feat(rng, 100, d, False), False)
+    g.plan_append(s2, d2, t2)
+    g.restore(snap)
+    assert g._plan is None
+    _compare(g, ring, "restored with a plan pending")
+    g.plan_append(s2, d2, t2)
+    g.reset()
+    assert g._plan is None

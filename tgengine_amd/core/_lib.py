@@ -68,6 +68,12 @@ class TgxRecentArgs(ctypes.Structure):
 SIGNATURES = {
     "tgx_ring_append": (c_i32, [ctypes.POINTER(TgxRing), c_vp, c_vp, c_vp, c_vp, c_i64, c_i64,
                                 c_vp, ctypes.c_size_t, c_vp, c_vp]),
+    "tgx_ring_plan": (c_i32, [ctypes.POINTER(TgxRing), c_vp, c_vp, c_vp, c_i64, c_vp, ctypes.c_size_t,
+                              c_vp]),
+    "tgx_ring_commit": (c_i32, [ctypes.POINTER(TgxRing), c_vp, c_vp, c_vp, c_vp, c_i64, c_i64,
+                                c_vp, ctypes.c_size_t, c_vp, c_vp]),
+    "tgx_ring_discard": (c_i32, [ctypes.POINTER(TgxRing), c_vp, c_vp, c_i64, c_vp, ctypes.c_size_t,
+                                 c_vp]),
     "tgx_ring_append_workspace_size": (ctypes.c_size_t, [c_i64]),
     "tgx_ring_scratch_size": (ctypes.c_size_t, [c_i64]),
     "tgx_recent": (c_i32, [ctypes.POINTER(TgxRing), ctypes.POINTER(TgxCsr),
@@ -102,7 +108,7 @@ def lib() -> ctypes.CDLL:
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
-        if handle.tgx_abi_version() != 4:
+        if handle.tgx_abi_version() != 5:
             raise RuntimeError("libtgx ABI version mismatch")
         _lib = handle
         return _lib

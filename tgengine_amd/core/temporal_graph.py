@@ -21,6 +21,7 @@ Extensions (keyword-only, defaults match the reference):
 from __future__ import annotations
 
 import ctypes
+import threading
 from dataclasses import dataclass
 from typing import Optional
 
@@ -50,6 +51,21 @@ class Snapshot:
     overflow_write_pos: Tensor
     num_edges: int
     overflow_eids: Optional[Tensor] = None
+
+
+@dataclass
+class _Plan:
+    """A ring update planned by plan_append, waiting for its advance()."""
+
+    key: tuple
+    src: Tensor
+    dst: Tensor
+    time: Tensor
+    done: "torch.cuda.Event"
+
+
+def _plan_key(*ts: Tensor) -> tuple:
+    return tuple((t.data_ptr(), tuple(t.shape), t.dtype, t._version) for t in ts)
 
 
 try:
@@ -128,6 +144,11 @@ class TemporalGraph:
 
         self._status = torch.zeros(_lib.TGX_STATUS_WORDS, dtype=torch.int32, device=self.device)
         self._ws: Optional[Tensor] = None
+        # a ring update planned ahead of its advance() (see plan_append)
+        self._plan: Optional[_Plan] = None
+        self._plan_ws: Optional[Tensor] = None
+        self._plan_stream = None
+        self._plan_lock = threading.Lock()
         self._ring_struct: Optional[_lib.TgxRing] = None
         self._csr_struct: Optional[_lib.TgxCsr] = None
         # optional object whose events() returns a (start, stop) pair of raw
@@ -194,12 +215,87 @@ class TemporalGraph:
             self._ws = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=self.device)
         return self._ws
 
+    # ------------------------------------------------------------------ planned updates
+    def plan_append(self, src: Tensor, dst: Tensor, time: Tensor) -> bool:
+        """Start the first half of the ring update of a batch that advance() will
+        receive next, on a side stream, so it overlaps the caller's current-stream
+        work (DataPipeline.prepare calls it before its gather launch).
+
+        The plan (tgx_ring_plan: per-node counts and entry lists) reads only
+        src/dst/time and the ring's scratch, never the ring arrays.  advance()
+        commits it when it receives the very same src/dst/time tensors unchanged
+        (same storage, shape, dtype and version counter), otherwise it discards
+        it and runs the whole update.  Returns whether a plan was started."""
+        if not self._frozen or self._ov_ids is None or self.device.type != "cuda":
+            return False
+        b = int(src.shape[0])
+        ok = (b > 0 and dst.shape[0] == b and time.shape[0] == b and src.dim() == 1 and dst.dim() == 1
+              and time.dim() == 1 and src.dtype == torch.int64 and dst.dtype == torch.int64
+              and time.dtype == torch.float64
+              and all(t.device == self.device and t.is_contiguous() for t in (src, dst, time)))
+        if not ok:
+            return False
+        with self._plan_lock:
+            main = torch.cuda.current_stream(self.device)
+            side = self._side_stream()
+            ready = torch.cuda.Event()
+            ready.record(main)          # the batch's inputs and the last commit are enqueued
+            side.wait_event(ready)
+            if self._plan is not None:  # an earlier plan nobody advanced: drop it first
+                self._discard_plan(side)
+            need = int(_lib.lib().tgx_ring_append_workspace_size(b))
+            if self._plan_ws is None or self._plan_ws.numel() < need:
+                self._plan_ws = torch.empty(max(need, 1 << 16), dtype=torch.uint8, device=self.device)
+                self._plan_ws.record_stream(side)
+            for t in (src, dst, time):
+                t.record_stream(side)
+            _host().ring_plan(ctypes.addressof(self._ring()), src, dst, time, self._plan_ws,
+                              side.cuda_stream)
+            done = torch.cuda.Event()
+            done.record(side)
+            self._plan = _Plan(_plan_key(src, dst, time), src, dst, time, done)
+        return True
+
+    def _side_stream(self):
+        if self._plan_stream is None:
+            self._plan_stream = torch.cuda.Stream(device=self.device)
+        return self._plan_stream
+
+    def _discard_plan(self, stream) -> None:
+        """Discard the pending plan on ``stream`` (ordered after the plan)."""
+        plan, self._plan = self._plan, None
+        stream.wait_event(plan.done)
+        _host().ring_discard(ctypes.addressof(self._ring()), plan.src, plan.dst, self._plan_ws,
+                             stream.cuda_stream)
+
+    def _drop_plan(self) -> None:
+        """Discard a pending plan on the current stream (before the ring or its
+        scratch is replaced)."""
+        with self._plan_lock:
+            if self._plan is not None:
+                self._discard_plan(torch.cuda.current_stream(self.device))
+
     def advance(self, src: Tensor, dst: Tensor, time: Tensor,
                 edge_feat: Optional[Tensor] = None) -> None:
         """Append a batch of undirected events (reference temporal_graph.py:104-131)."""
         b = int(src.shape[0])
         if dst.shape[0] != b or time.shape[0] != b:
             raise ValueError("src, dst and time must have the same length")
+        if self._plan is not None:
+            with self._plan_lock:
+                plan = self._plan
+                if plan is not None and self._frozen and plan.key == _plan_key(src, dst, time):
+                    self._plan = None
+                    feat = self._feat_in(edge_feat, b)
+                    main = torch.cuda.current_stream(self.device)
+                    main.wait_event(plan.done)
+                    _host().ring_commit(ctypes.addressof(self._ring()), src, dst, time, feat,
+                                        self._num_edges, self._plan_ws, self._status,
+                                        main.cuda_stream)
+                    self._num_edges += b
+                    return
+                if plan is not None:
+                    self._discard_plan(torch.cuda.current_stream(self.device))
         if not self._frozen:
             feat = (torch.zeros((b, self.edge_feat_dim), dtype=self.feat_dtype)
                     if edge_feat is None else self._feat_in(edge_feat, b).cpu())
@@ -347,6 +443,8 @@ class TemporalGraph:
 
     # ------------------------------------------------------------------ state
     def reset(self) -> None:
+        if self._ov_ids is not None:
+            self._drop_plan()
         self._frozen = False
         self._build = []
         self._offsets = self._nbr_ids = self._nbr_times = self._nbr_feats = self._nbr_eids = None
@@ -364,6 +462,7 @@ class TemporalGraph:
                         None if self._ov_eids is None else self._ov_eids.clone())
 
     def restore(self, snap: Snapshot) -> None:
+        self._drop_plan()
         self._ov_ids.copy_(snap.overflow_ids)
         self._ov_times.copy_(snap.overflow_times)
         self._ov_feats.copy_(snap.overflow_feats)

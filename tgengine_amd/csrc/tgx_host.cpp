@@ -137,9 +137,42 @@ void ring_append(int64_t ring_addr, const at::Tensor& src, const at::Tensor& dst
         "tgx_ring_append");
 }
 
+// the two halves of ring_append (tensors already int64 / float64 / contiguous on
+// the device: the caller keeps them alive across both calls)
+void ring_plan(int64_t ring_addr, const at::Tensor& src, const at::Tensor& dst,
+               const at::Tensor& time, const at::Tensor& workspace, int64_t stream) {
+  check(tgx_ring_plan(reinterpret_cast<const tgx_ring*>(ring_addr), src.data_ptr<int64_t>(),
+                      dst.data_ptr<int64_t>(), time.data_ptr<double>(), src.numel(),
+                      workspace.data_ptr(), static_cast<size_t>(workspace.numel()),
+                      reinterpret_cast<void*>(stream)),
+        "tgx_ring_plan");
+}
+
+void ring_commit(int64_t ring_addr, const at::Tensor& src, const at::Tensor& dst,
+                 const at::Tensor& time, const c10::optional<at::Tensor>& feat, int64_t eid_base,
+                 const at::Tensor& workspace, const at::Tensor& status, int64_t stream) {
+  check(tgx_ring_commit(reinterpret_cast<const tgx_ring*>(ring_addr), src.data_ptr<int64_t>(),
+                        dst.data_ptr<int64_t>(), time.data_ptr<double>(),
+                        feat.has_value() ? feat->data_ptr() : nullptr, src.numel(), eid_base,
+                        workspace.data_ptr(), static_cast<size_t>(workspace.numel()),
+                        status.data_ptr<int32_t>(), reinterpret_cast<void*>(stream)),
+        "tgx_ring_commit");
+}
+
+void ring_discard(int64_t ring_addr, const at::Tensor& src, const at::Tensor& dst,
+                  const at::Tensor& workspace, int64_t stream) {
+  check(tgx_ring_discard(reinterpret_cast<const tgx_ring*>(ring_addr), src.data_ptr<int64_t>(),
+                         dst.data_ptr<int64_t>(), src.numel(), workspace.data_ptr(),
+                         static_cast<size_t>(workspace.numel()), reinterpret_cast<void*>(stream)),
+        "tgx_ring_discard");
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("recent", &recent, "allocate outputs, launch tgx_recent, return per-group views");
   m.def("ring_append", &ring_append, "launch tgx_ring_append on one batch");
+  m.def("ring_plan", &ring_plan, "launch tgx_ring_plan (first half of an append)");
+  m.def("ring_commit", &ring_commit, "launch tgx_ring_commit (second half of an append)");
+  m.def("ring_discard", &ring_discard, "launch tgx_ring_discard (drop a planned append)");
 }

@@ -9,21 +9,38 @@
 // entry with e later same-node entries is kept iff e < kept = min(c, B) and
 // lands in slot (write_pos + kept - 1 - e) % B.
 //
-// Design: four launches on the caller's stream, all spread over the device.
-//   1. count  : per-node tickets from node-indexed counters owned by the ring
-//               (zero between calls); equal nodes inside a wavefront are
-//               matched first so a hot node costs one atomic per wavefront.
-//   2. groups : the ticket-0 entry of every node seen more than once reserves
-//               a contiguous list of c slots and a group id, small (c <= 64)
-//               or large (one atomic per wave, offsets by a wave scan).
-//   3. fill   : list[base[u] + ticket] = entry index.
-//   4. commit : singletons (c == 1) are written directly; a small group is
-//               ranked by one wavefront in registers, a large group by a whole
-//               workgroup over LDS bitmaps of 8192-index windows walked down
-//               from the top of the batch; kept entries are written, count[u]
-//               is restored to zero and write_pos advances.
-// Feature rows move as 16-byte vectors when the row allows it.
+// Both designs below take per-node tickets from node-indexed counters owned by
+// the ring (zero between calls); equal nodes of a workgroup are first
+// aggregated in an LDS hash table, so a node costs one global atomic per
+// workgroup however hot it is.  Tickets number a node's entries in no
+// particular order; ranking by entry index happens when the node is written.
+//
+// Batches of up to kFastMaxEntries entries: two launches.
+//   plan   : tickets; ticket t < kListCap stores the entry in the node's list
+//            lst[u][t] (ring scratch), later tickets append (u, i) to an
+//            overflow array; the ticket-1 entry appends the node to the group
+//            list, the ticket-kListCap entry to the large-group list.  The
+//            three cursors share one 64-bit word: one atomic per workgroup.
+//   commit : singletons (c == 1) are written directly; a group of
+//            c <= kListCap is ranked by one wavefront from its node list; a
+//            larger group by a workgroup that marks its list and overflow
+//            entries in an LDS bitmap of the whole batch and takes the kept
+//            entries from the top.  The last workgroup to finish reports
+//            diagnostics and clears the cursors.
+// Larger batches: four launches, whose lists are sized after counting.
+//   count  : tickets.
+//   groups : the ticket-0 entry of every node seen more than once reserves
+//            a contiguous list of c slots and a group id, small (c <= 64)
+//            or large (one atomic per wave, offsets by a wave scan).
+//   fill   : list[base[u] + ticket] = entry index.
+//   commit : singletons as above; a small group is ranked by one wavefront in
+//            registers, a large group by a whole workgroup over bitmap
+//            windows walked down from the top of the batch.
+// Every path writes the kept entries, restores count[u] to zero and advances
+// write_pos.  Feature rows move as 16-byte vectors when the row allows it.
 #include "tgx_internal.h"
+
+#include <algorithm>
 
 namespace tgx {
 namespace {
@@ -33,7 +50,32 @@ constexpr int kCommitWaves = kThreads / kWave;
 constexpr int kWinBits = 8192;                 // bitmap window (indices)
 constexpr int kWinWords = kWinBits / 32;       // 256 words = 1 KB
 static_assert(kWinWords == kThreads, "one bitmap word per thread");
-enum { kCtlCursor = 0, kCtlGroups = 1, kCtlTimeOk = 2, kCtlLarge = 3 };
+// ctl words (ring scratch): four-launch cursors, shared diagnostics, two-launch cursors
+enum {
+  kCtlCursor = 0, kCtlGroups = 1, kCtlTimeOk = 2, kCtlLarge = 3, kCtlBad = 4,
+  kCtlFCursor = 8,  // uint64 over words 8, 9: two-launch overflow | groups | large counts
+  kCtlFDone = 10
+};
+// fields of the two-launch cursor word (every count is at most n <= 2^15)
+constexpr int kFieldBits = 21;
+constexpr uint64_t kFieldMask = (uint64_t(1) << kFieldBits) - 1;
+__host__ __device__ constexpr int field(uint64_t x, int f) {
+  return static_cast<int>((x >> (f * kFieldBits)) & kFieldMask);
+}
+enum { kFOvf = 0, kFGroups = 1, kFLarge = 2 };
+constexpr int kCtlWords = 16;
+constexpr int kHashBits = 9;                 // tickets: LDS hash of 2*kThreads slots
+constexpr int kHash = 1 << kHashBits;
+static_assert(kHash >= 2 * kThreads, "hash table at most half full");
+constexpr int64_t kSmallGroupBlocks = 256;  // commit blocks for small groups (4 waves each)
+constexpr int64_t kLargeGroupBlocks = 64;   // four-launch commit blocks for large groups
+constexpr int kListCap = 8;                 // node-indexed list entries per node
+constexpr int64_t kFastMaxEntries = 32768;  // two-launch path up to this many entries
+constexpr int kFastWords = kFastMaxEntries / 32;  // two-launch bitmap of the whole batch
+constexpr int kWordsPerThread = kFastWords / kThreads;
+static_assert(kWordsPerThread * kThreads == kFastWords, "bitmap words split evenly");
+constexpr int kScanUnroll = 32;             // overflow pairs in flight per thread
+constexpr int64_t kFastLargeBlocks = 128;   // two-launch commit blocks for large groups
 
 // (write_pos + off) % B for write_pos >= 0, 0 <= off < B
 __device__ __forceinline__ int64_t ring_slot(int64_t w, int off, int B) {
@@ -87,78 +129,153 @@ struct AppendParams {
   int64_t* wp;
   int64_t* eids;
   int32_t* cnt;     // [N] per-node counters (zero between calls)
-  int32_t* nbase;   // [N] list base of multi-entry nodes
-  int32_t* ctl;     // [16] cursor, group count, time flag
-  int32_t* ticket;  // [n]
-  int32_t* list;    // [n]
-  int32_t* groups;  // [n/2 + 1] small groups
-  int32_t* large;   // [n/65 + 1] large groups
+  int32_t* lst;     // [N, kListCap] two-launch lists
+  int32_t* nbase;   // [N] four-launch list base of multi-entry nodes (aliases lst)
+  int32_t* ctl;     // [kCtlWords] cursors and diagnostics
+  int32_t* ticket;  // [n] four-launch tickets
+  int32_t* list;    // [n] four-launch lists
+  int2* ovf;        // [n] two-launch overflow (node, entry) pairs (over list)
+  int32_t* groups;  // [n/2 + 1] groups
+  int32_t* large;   // [n/(kListCap+1) + 1] large groups
   int32_t* status;
   int tpe_log2;     // lanes per entry (singleton copy)
   int ga;           // blocks of the singleton role in commit
   int gb;           // blocks of the small-group role
 };
 
-// ---- 1. count -------------------------------------------------------------
+// node of entry i (-1 when outside [0, N): counted as a bad entry) and whether
+// its event time keeps the reference key from*(int(max t)+2)+i lexicographic
+// (int(max t)+2 > n-1)
+__device__ __forceinline__ int32_t entry_prologue(const AppendParams& P, int64_t i, int& bad,
+                                                  bool& time_ok) {
+  bad = 0;
+  time_ok = false;
+  if (i >= P.n) return -1;
+  const int64_t uu = entry_node(P.src, P.dst, i, P.b);
+  if (i < P.b) time_ok = trunc(P.time[i]) > static_cast<double>(P.n - 3);
+  if (uu < 0 || uu >= P.N) {
+    bad = 1;
+    return -1;
+  }
+  return static_cast<int32_t>(uu);
+}
+
+// Ticket of the entry of node u (>= 0), or -1 for u < 0.  Equal nodes of the
+// workgroup are aggregated in an LDS hash table (open addressing, at most half
+// full): each lane takes a local rank from its node's slot, then one global
+// atomic per distinct node reserves the workgroup's tickets.
+__device__ __forceinline__ int32_t node_ticket(const AppendParams& P, int32_t u, int32_t* hkey,
+                                               int32_t* hcnt, int32_t* hbase) {
+  for (int s = threadIdx.x; s < kHash; s += kThreads) {
+    hkey[s] = -1;
+    hcnt[s] = 0;
+  }
+  __syncthreads();
+  int hs = -1, rank = 0;
+  if (u >= 0) {
+    hs = static_cast<int>((static_cast<uint32_t>(u) * 2654435761u) >> (32 - kHashBits));
+    while (true) {  // terminates: fewer keys than slots
+      const int32_t old = atomicCAS(&hkey[hs], -1, u);
+      if (old == -1 || old == u) break;
+      hs = (hs + 1) & (kHash - 1);
+    }
+    rank = atomicAdd(&hcnt[hs], 1);
+  }
+  __syncthreads();
+  for (int s = threadIdx.x; s < kHash; s += kThreads)
+    if (hkey[s] >= 0) hbase[s] = atomicAdd(&P.cnt[hkey[s]], hcnt[s]);
+  __syncthreads();
+  return u >= 0 ? hbase[hs] + rank : -1;
+}
+
+__device__ __forceinline__ void report_diagnostics(const AppendParams& P, int bad, bool time_ok) {
+  const uint64_t bm = __ballot(bad);
+  const uint64_t tm = __ballot(time_ok);
+  if ((threadIdx.x & (kWave - 1)) == 0) {
+    if (bm) atomicAdd(&P.ctl[kCtlBad], __popcll(bm));
+    if (tm) atomicOr(&P.ctl[kCtlTimeOk], 1);
+  }
+}
+
+// the plan's diagnostics reach the status words only when the batch commits
+__device__ __forceinline__ void commit_diagnostics(const AppendParams& P) {
+  if (P.status != nullptr) {
+    if (P.ctl[kCtlBad] != 0) atomicAdd(&P.status[TGX_ST_BAD_EVENT_NODE], P.ctl[kCtlBad]);
+    if (P.ctl[kCtlTimeOk] == 0) atomicAdd(&P.status[TGX_ST_KEY_COLLISION], 1);
+  }
+  P.ctl[kCtlTimeOk] = 0;
+  P.ctl[kCtlBad] = 0;
+}
+
+// ---- four-launch 1. count ----------------------------------------------------
 __global__ __launch_bounds__(kThreads) void append_count(AppendParams P) {
+  __shared__ int32_t hkey[kHash];
+  __shared__ int32_t hcnt[kHash];
+  __shared__ int32_t hbase[kHash];
   const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  const int lane = threadIdx.x & (kWave - 1);
   if (i == 0) {
     P.ctl[kCtlCursor] = 0;
     P.ctl[kCtlGroups] = 0;
     P.ctl[kCtlLarge] = 0;
   }
-  int bad = 0;
-  bool time_ok = false;
-  int32_t u = -1;
-  if (i < P.n) {
-    const int64_t uu = entry_node(P.src, P.dst, i, P.b);
-    if (uu < 0 || uu >= P.N)
-      bad = 1;
-    else
-      u = static_cast<int32_t>(uu);
-    // reference key from*(int(max t)+2)+i is lexicographic iff int(max t)+2 > n-1
-    if (i < P.b) time_ok = trunc(P.time[i]) > static_cast<double>(P.n - 3);
-  }
-  // match equal nodes inside the wavefront: one atomic per distinct node
-  const uint64_t active = __ballot(u >= 0);
-  uint64_t todo = active;
-  uint64_t peers = 0;
-  while (todo) {
-    const int j = __ffsll(static_cast<unsigned long long>(todo)) - 1;
-    const int32_t uj = __shfl(u, j, kWave);
-    const uint64_t m = __ballot(u == uj) & active;
-    if ((m >> lane) & 1) peers = m;
-    todo &= ~m;
-  }
-  if (u >= 0) {
-    const int leader = __ffsll(static_cast<unsigned long long>(peers)) - 1;
-    const int rank = __popcll(peers & ((uint64_t(1) << lane) - 1));
-    int base = 0;
-    if (lane == leader) base = atomicAdd(&P.cnt[u], __popcll(peers));
-    // leader lanes publish their base; every lane reads its leader's
-    base = __shfl(base, leader, kWave);
-    P.ticket[i] = base + rank;
-  } else if (i < P.n) {
-    P.ticket[i] = -1;
-  }
-  const uint64_t bm = __ballot(bad);
-  const uint64_t tm = __ballot(time_ok);
-  if (lane == 0) {
-    if (bm && P.status != nullptr) atomicAdd(&P.status[TGX_ST_BAD_EVENT_NODE], __popcll(bm));
-    if (tm) atomicOr(&P.ctl[kCtlTimeOk], 1);
-  }
+  int bad;
+  bool time_ok;
+  const int32_t u = entry_prologue(P, i, bad, time_ok);
+  const int32_t t = node_ticket(P, u, hkey, hcnt, hbase);
+  if (i < P.n) P.ticket[i] = t;
+  report_diagnostics(P, bad, time_ok);
 }
 
-// ---- 2. groups --------------------------------------------------------------
+// ---- two-launch 1. plan -------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void fast_plan(AppendParams P) {
+  __shared__ int32_t hkey[kHash];
+  __shared__ int32_t hcnt[kHash];
+  __shared__ int32_t hbase[kHash];
+  __shared__ uint64_t wofs[kCommitWaves + 1];
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  const int wv = threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  int bad;
+  bool time_ok;
+  const int32_t u = entry_prologue(P, i, bad, time_ok);
+  const int32_t t = node_ticket(P, u, hkey, hcnt, hbase);
+  if (t >= 0 && t < kListCap) P.lst[static_cast<int64_t>(u) * kListCap + t] = static_cast<int32_t>(i);
+  // appends to the overflow, group and large-group lists: wave counts packed in
+  // one word, a workgroup prefix in LDS, one cursor atomic per workgroup
+  const uint64_t om = __ballot(t >= kListCap);
+  const uint64_t gm = __ballot(t == 1);
+  const uint64_t lm = __ballot(t == kListCap);
+  if (lane == 0)
+    wofs[wv] = static_cast<uint64_t>(__popcll(om)) |
+               (static_cast<uint64_t>(__popcll(gm)) << (kFGroups * kFieldBits)) |
+               (static_cast<uint64_t>(__popcll(lm)) << (kFLarge * kFieldBits));
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint64_t tot = 0;
+    for (int w = 0; w < kCommitWaves; ++w) {
+      const uint64_t c = wofs[w];
+      wofs[w] = tot;
+      tot += c;
+    }
+    wofs[kCommitWaves] =
+        tot != 0 ? atomicAdd(reinterpret_cast<unsigned long long*>(P.ctl + kCtlFCursor),
+                             static_cast<unsigned long long>(tot))
+                 : 0;
+  }
+  __syncthreads();
+  const uint64_t below = (uint64_t(1) << lane) - 1;
+  const uint64_t at = wofs[kCommitWaves] + wofs[wv];
+  if (t >= kListCap)
+    P.ovf[field(at, kFOvf) + __popcll(om & below)] = make_int2(u, static_cast<int32_t>(i));
+  if (t == 1) P.groups[field(at, kFGroups) + __popcll(gm & below)] = u;
+  if (t == kListCap) P.large[field(at, kFLarge) + __popcll(lm & below)] = u;
+  report_diagnostics(P, bad, time_ok);
+}
+
+// ---- four-launch 2. groups --------------------------------------------------------------
 __global__ __launch_bounds__(kThreads) void append_groups(AppendParams P) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   const int lane = threadIdx.x & (kWave - 1);
-  if (i == 0) {
-    if (P.ctl[kCtlTimeOk] == 0 && P.status != nullptr)
-      atomicAdd(&P.status[TGX_ST_KEY_COLLISION], 1);
-    P.ctl[kCtlTimeOk] = 0;
-  }
   int64_t u = -1;
   int c = 0;
   if (i < P.n && P.ticket[i] == 0) {
@@ -195,7 +312,7 @@ __global__ __launch_bounds__(kThreads) void append_groups(AppendParams P) {
   if (grp) P.nbase[u] = lbase + incl - sum;
 }
 
-// ---- 3. fill ----------------------------------------------------------------
+// ---- four-launch 3. fill ----------------------------------------------------------------
 __global__ __launch_bounds__(kThreads) void append_fill(AppendParams P) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   if (i >= P.n) return;
@@ -234,83 +351,17 @@ __device__ __forceinline__ void write_kept(const AppendParams& P, const int32_t*
   }
 }
 
-// ---- 4. commit --------------------------------------------------------------
-// blocks [0, ga): singletons; [ga, ga+gb): small groups, one per wavefront;
-// [ga+gb, ...): large groups, one per workgroup
+// one large group (c > 64) by the whole workgroup
 template <int VEC>
-__global__ __launch_bounds__(kThreads) void append_commit(AppendParams P) {
-  using V = typename VecT<VEC>::T;
-  __shared__ uint32_t bitmap[kWinWords];
-  __shared__ int32_t sfx[kWinWords];                     // set bits in later words
-  __shared__ int32_t rows[kCommitWaves][TGX_MAX_SLOTS];  // kept entry index by e
-  __shared__ int32_t wsum[kCommitWaves];
-  const int nv = static_cast<int>(P.row_bytes / VEC);
-  const int blk = static_cast<int>(blockIdx.x);
-
-  if (blk < P.ga) {
-    // singletons: tpe lanes per entry
-    const int tpe = 1 << P.tpe_log2;
-    const int epb = kThreads >> P.tpe_log2;
-    const int64_t i = static_cast<int64_t>(blk) * epb + (threadIdx.x >> P.tpe_log2);
-    const int l = threadIdx.x & (tpe - 1);
-    if (i >= P.n) return;
-    if (P.ticket[i] != 0) return;
-    const int64_t u = entry_node(P.src, P.dst, i, P.b);
-    if (P.cnt[u] != 1) return;
-    const int64_t w = P.wp[u];
-    const int64_t slot = u * P.B + ring_slot(w, 0, P.B);
-    const int64_t e = i < P.b ? i : i - P.b;
-    V* drow = reinterpret_cast<V*>(P.feats + slot * P.row_bytes);
-    if (P.feat != nullptr) {
-      const V* srow = reinterpret_cast<const V*>(P.feat + e * P.row_bytes);
-      for (int c = l; c < nv; c += tpe) drow[c] = srow[c];
-    } else {
-      for (int c = l; c < nv; c += tpe) drow[c] = V{};
-    }
-    if (l == 0) {
-      write_entry_meta(P, i, slot);
-      P.wp[u] = w + 1;
-      P.cnt[u] = 0;
-    }
-    return;
-  }
-
+__device__ __forceinline__ void commit_large(const AppendParams& P, int64_t gid, uint32_t* bitmap,
+                                             int32_t* sfx, int32_t* R, int32_t* wsum) {
   const int wv = threadIdx.x / kWave;
   const int lane = threadIdx.x & (kWave - 1);
-  if (blk < P.ga + P.gb) {
-    // small group (2 <= c <= 64): ranks by comparing list entries in registers
-    const int64_t gid = static_cast<int64_t>(blk - P.ga) * kCommitWaves + wv;
-    if (gid >= P.ctl[kCtlGroups]) return;  // wave-uniform
-    const int64_t u = P.groups[gid];
-    const int c = P.cnt[u];
-    const int base = P.nbase[u];
-    const int kept = c < P.B ? c : P.B;
-    int32_t* R = rows[wv];
-    const int32_t idx = lane < c ? P.list[base + lane] : -1;
-    int e = 0;
-    for (int j = 0; j < c; ++j) e += __shfl(idx, j, kWave) > idx;
-    if (lane < c && e < kept) R[e] = idx;
-    wave_sync_lds();
-    const int64_t w = P.wp[u];
-    write_kept<VEC>(P, R, u, kept, w, lane, kWave);
-    if (lane == 0) {
-      P.wp[u] = w + kept;
-      P.cnt[u] = 0;
-    }
-    return;
-  }
-
-  // large group (c > 64): the workgroup ranks the list over bitmap windows of
-  // kWinBits entry indices, from the top of the batch down, until `kept`
-  // entries are found
-  const int64_t gid = blk - P.ga - P.gb;
-  if (gid >= P.ctl[kCtlLarge]) return;  // workgroup-uniform
   const int t = threadIdx.x;
   const int64_t u = P.large[gid];
   const int c = P.cnt[u];
   const int base = P.nbase[u];
   const int kept = c < P.B ? c : P.B;
-  int32_t* R = rows[0];
   int64_t hi = P.n;
   int carry = 0;
   while (carry < kept && hi > 0) {  // uniform across the workgroup
@@ -359,9 +410,231 @@ __global__ __launch_bounds__(kThreads) void append_commit(AppendParams P) {
     P.wp[u] = w + kept;
     P.cnt[u] = 0;
   }
+  __syncthreads();  // the next group rewrites R and the bitmap
+}
+
+// singletons (c == 1), written directly: tpe lanes per entry, blocks [0, ga).
+// A group's counter reads c >= 2 or 0 (once its role restored it), never 1.
+template <int VEC>
+__device__ __forceinline__ void commit_singletons(const AppendParams& P, int blk) {
+  using V = typename VecT<VEC>::T;
+  const int nv = static_cast<int>(P.row_bytes / VEC);
+  const int tpe = 1 << P.tpe_log2;
+  const int epb = kThreads >> P.tpe_log2;
+  const int64_t i = static_cast<int64_t>(blk) * epb + (threadIdx.x >> P.tpe_log2);
+  const int l = threadIdx.x & (tpe - 1);
+  if (i >= P.n) return;
+  const int64_t u = entry_node(P.src, P.dst, i, P.b);
+  if (u < 0 || u >= P.N || P.cnt[u] != 1) return;
+  const int64_t w = P.wp[u];
+  const int64_t slot = u * P.B + ring_slot(w, 0, P.B);
+  const int64_t e = i < P.b ? i : i - P.b;
+  V* drow = reinterpret_cast<V*>(P.feats + slot * P.row_bytes);
+  if (P.feat != nullptr) {
+    const V* srow = reinterpret_cast<const V*>(P.feat + e * P.row_bytes);
+    for (int c = l; c < nv; c += tpe) drow[c] = srow[c];
+  } else {
+    for (int c = l; c < nv; c += tpe) drow[c] = V{};
+  }
+  if (l == 0) {
+    write_entry_meta(P, i, slot);
+    P.wp[u] = w + 1;
+    P.cnt[u] = 0;
+  }
+}
+
+// one group of c <= kWave entries listed in idx (lane j < c holds one entry
+// index), ranked in registers by one wavefront, then written
+template <int VEC>
+__device__ __forceinline__ void commit_small(const AppendParams& P, int64_t u, int c, int32_t idx,
+                                             int64_t w, int32_t* R) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int kept = c < P.B ? c : P.B;
+  int e = 0;
+  for (int j = 0; j < c; ++j) e += __shfl(idx, j, kWave) > idx;
+  if (lane < c && e < kept) R[e] = idx;
+  wave_sync_lds();
+  write_kept<VEC>(P, R, u, kept, w, lane, kWave);
+  if (lane == 0) {
+    P.wp[u] = w + kept;
+    P.cnt[u] = 0;
+  }
+  wave_sync_lds();  // R is rewritten by the next group
+}
+
+// ---- four-launch 4. commit ----------------------------------------------------
+// blocks [0, ga): singletons; [ga, ga+gb): small groups, one per wavefront;
+// [ga+gb, ...): large groups, one per workgroup
+template <int VEC>
+__global__ __launch_bounds__(kThreads) void append_commit(AppendParams P) {
+  __shared__ uint32_t bitmap[kWinWords];
+  __shared__ int32_t sfx[kWinWords];                     // set bits in later words
+  __shared__ int32_t rows[kCommitWaves][TGX_MAX_SLOTS];  // kept entry index by e
+  __shared__ int32_t wsum[kCommitWaves];
+  const int blk = static_cast<int>(blockIdx.x);
+  if (blk == 0 && threadIdx.x == 0) commit_diagnostics(P);
+  if (blk < P.ga) {
+    commit_singletons<VEC>(P, blk);
+    return;
+  }
+  const int wv = threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  if (blk < P.ga + P.gb) {
+    // small groups (2 <= c <= 64), one per wavefront, strided over the gb blocks
+    const int64_t ngroups = P.ctl[kCtlGroups];
+    for (int64_t gid = static_cast<int64_t>(blk - P.ga) * kCommitWaves + wv; gid < ngroups;
+         gid += static_cast<int64_t>(P.gb) * kCommitWaves) {  // wave-uniform
+      const int64_t u = P.groups[gid];
+      const int c = P.cnt[u];
+      const int32_t idx = lane < c ? P.list[P.nbase[u] + lane] : -1;
+      commit_small<VEC>(P, u, c, idx, P.wp[u], rows[wv]);
+    }
+    return;
+  }
+  // large groups (c > 64), one per workgroup, strided over the remaining blocks:
+  // the workgroup ranks the list over bitmap windows of kWinBits entry indices,
+  // from the top of the batch down, until `kept` entries are found
+  const int64_t nlarge = P.ctl[kCtlLarge];
+  const int64_t gstride = static_cast<int64_t>(gridDim.x) - P.ga - P.gb;
+  for (int64_t gid = blk - P.ga - P.gb; gid < nlarge; gid += gstride)  // workgroup-uniform
+    commit_large<VEC>(P, gid, bitmap, sfx, rows[0], wsum);
+}
+
+// ---- two-launch 2. commit -------------------------------------------------------
+__device__ __forceinline__ void load_pairs(const AppendParams& P, int j0, int novf,
+                                           int2 (&pr)[kScanUnroll]) {
+#pragma unroll
+  for (int r = 0; r < kScanUnroll; ++r) {
+    const int j = j0 + r * kThreads + static_cast<int>(threadIdx.x);
+    pr[r] = j < novf ? P.ovf[j] : make_int2(-1, 0);
+  }
+}
+
+// One large group (c > kListCap) by the whole workgroup.  Its entries (the node
+// list and its overflow pairs) are marked in an LDS bitmap of the whole batch
+// (bit i for entry i); thread t owns words [kWordsPerThread t, +kWordsPerThread)
+// and takes the set bits of its words from the highest, so R[e] is the entry
+// with e later entries of the node.  The first overflow chunk is loaded before
+// the node's own values, so both round trips overlap.
+template <int VEC>
+__device__ __forceinline__ void fast_large(const AppendParams& P, const int32_t* u_at, int novf,
+                                           uint32_t* bitmap, int32_t* R, int32_t* wsum) {
+  const int wv = threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int t = threadIdx.x;
+  int2 pr[kScanUnroll];
+  load_pairs(P, 0, novf, pr);
+  const int64_t u = *u_at;
+  const int c = P.cnt[u];
+  const int64_t w = P.wp[u];
+  const int32_t first = t < kListCap ? P.lst[u * kListCap + t] : -1;
+  const int kept = c < P.B ? c : P.B;
+#pragma unroll
+  for (int q = 0; q < kWordsPerThread; ++q) bitmap[t * kWordsPerThread + q] = 0u;
+  __syncthreads();
+  if (first >= 0) atomicOr(&bitmap[first >> 5], 1u << (first & 31));
+  for (int j0 = 0;;) {
+#pragma unroll
+    for (int r = 0; r < kScanUnroll; ++r)
+      if (pr[r].x == u) atomicOr(&bitmap[pr[r].y >> 5], 1u << (pr[r].y & 31));
+    j0 += kScanUnroll * kThreads;
+    if (j0 >= novf) break;
+    load_pairs(P, j0, novf, pr);
+  }
+  __syncthreads();
+  // set bits in later words: own words, wave suffix scan, later waves' totals
+  int own = 0;
+#pragma unroll
+  for (int q = 0; q < kWordsPerThread; ++q) own += __popc(bitmap[t * kWordsPerThread + q]);
+  int suf = own;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int y = __shfl_down(suf, off, kWave);
+    if (lane + off < kWave) suf += y;
+  }
+  if (lane == 0) wsum[wv] = suf;
+  __syncthreads();
+  int k = suf - own;
+  for (int w2 = wv + 1; w2 < kCommitWaves; ++w2) k += wsum[w2];
+  for (int q = kWordsPerThread - 1; q >= 0 && k < kept; --q) {
+    uint32_t word = bitmap[t * kWordsPerThread + q];
+    while (word != 0u && k < kept) {
+      const int bit = 31 - __clz(static_cast<int>(word));
+      R[k++] = (t * kWordsPerThread + q) * 32 + bit;
+      word &= ~(1u << bit);
+    }
+  }
+  __syncthreads();
+  write_kept<VEC>(P, R, u, kept, w, t, kThreads);
+  if (t == 0) {
+    P.wp[u] = w + kept;
+    P.cnt[u] = 0;
+  }
+  __syncthreads();  // the next group rewrites R and the bitmap
+}
+
+// blocks [0, ga): singletons; [ga, ga+gb): groups of c <= kListCap, one per
+// wavefront; [ga+gb, ...): larger groups, one per workgroup
+template <int VEC>
+__global__ __launch_bounds__(kThreads) void fast_commit(AppendParams P) {
+  __shared__ uint32_t bitmap[kFastWords];
+  __shared__ int32_t rows[kCommitWaves][TGX_MAX_SLOTS];
+  __shared__ int32_t wsum[kCommitWaves];
+  const int blk = static_cast<int>(blockIdx.x);
+  const int wv = threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  if (blk < P.ga) {
+    commit_singletons<VEC>(P, blk);
+  } else {
+    const uint64_t cur = *reinterpret_cast<const uint64_t*>(P.ctl + kCtlFCursor);
+    if (blk < P.ga + P.gb) {
+      const int ngroups = field(cur, kFGroups);
+      for (int gid = (blk - P.ga) * kCommitWaves + wv; gid < ngroups;
+           gid += P.gb * kCommitWaves) {  // wave-uniform
+        const int64_t u = P.groups[gid];
+        const int c = P.cnt[u];
+        const int64_t w = P.wp[u];
+        const int32_t idx = lane < kListCap ? P.lst[u * kListCap + lane] : -1;
+        // a larger group has its own role; its counter reads c > kListCap, or 0
+        // once that role restored it
+        if (c < 2 || c > kListCap) continue;
+        commit_small<VEC>(P, u, c, lane < c ? idx : -1, w, rows[wv]);
+      }
+    } else {
+      const int nlarge = field(cur, kFLarge);
+      const int novf = field(cur, kFOvf);
+      const int gstride = static_cast<int>(gridDim.x) - P.ga - P.gb;
+      for (int gid = blk - P.ga - P.gb; gid < nlarge; gid += gstride)  // workgroup-uniform
+        fast_large<VEC>(P, P.large + gid, novf, bitmap, rows[0], wsum);
+    }
+  }
+  // the last workgroup to finish (every other one has read the cursors) reports
+  // the plan's diagnostics and clears the cursors for the next plan
+  __syncthreads();
+  if (threadIdx.x == 0 && atomicAdd(&P.ctl[kCtlFDone], 1) == static_cast<int>(gridDim.x) - 1) {
+    commit_diagnostics(P);
+    *reinterpret_cast<uint64_t*>(P.ctl + kCtlFCursor) = 0;
+    P.ctl[kCtlFDone] = 0;
+  }
+}
+
+// ---- discard: restore the scratch of a planned batch without committing it ----
+__global__ __launch_bounds__(kThreads) void append_discard(AppendParams P) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i == 0) {
+    P.ctl[kCtlTimeOk] = 0;
+    P.ctl[kCtlBad] = 0;
+    *reinterpret_cast<uint64_t*>(P.ctl + kCtlFCursor) = 0;
+  }
+  if (i >= P.n) return;
+  const int64_t u = entry_node(P.src, P.dst, i, P.b);
+  if (u >= 0 && u < P.N) P.cnt[u] = 0;
 }
 
 size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+// ring scratch: counters [N] | lists [N, kListCap] | ctl (16-byte aligned)
+int64_t ctl_offset(int64_t num_nodes) { return ((1 + kListCap) * num_nodes + 3) & ~int64_t(3); }
 
 }  // namespace
 }  // namespace tgx
@@ -371,45 +644,45 @@ using namespace tgx;
 extern "C" size_t tgx_ring_append_workspace_size(int64_t b) {
   if (b <= 0) return 256;
   const size_t n = static_cast<size_t>(2 * b);
-  return 2 * align256(n * 4) + align256((n / 2 + 1) * 4) + align256((n / 65 + 1) * 4);
+  // ticket | overflow pairs (four-launch: list) | groups | large
+  return align256(n * 4) + align256(n * 8) + align256((n / 2 + 1) * 4) +
+         align256((n / (kListCap + 1) + 1) * 4);
 }
 
 extern "C" size_t tgx_ring_scratch_size(int64_t num_nodes) {
   if (num_nodes < 0) return 0;
-  return static_cast<size_t>(2 * num_nodes + 16) * sizeof(int32_t);
+  return static_cast<size_t>(ctl_offset(num_nodes) + kCtlWords) * sizeof(int32_t);
 }
 
-extern "C" int tgx_ring_append(const tgx_ring* ring, const int64_t* src, const int64_t* dst,
-                               const double* time, const void* feat, int64_t b,
-                               int64_t eid_base, void* workspace, size_t workspace_bytes,
-                               int32_t* status, void* stream_) {
-  hipStream_t stream = static_cast<hipStream_t>(stream_);
-  if (ring == nullptr) return fail(TGX_ERR_ARG, "tgx_ring_append: ring is NULL");
-  if (b < 0) return fail(TGX_ERR_ARG, "tgx_ring_append: negative batch size %lld", (long long)b);
+namespace {
+
+// argument checks and the kernel parameters shared by plan / commit / discard
+int setup_append(const char* who, const tgx_ring* ring, const int64_t* src, const int64_t* dst,
+                 const double* time, const void* feat, int64_t b, int64_t eid_base, void* workspace,
+                 size_t workspace_bytes, int32_t* status, AppendParams& P, int& vec, bool need_time) {
+  if (ring == nullptr) return fail(TGX_ERR_ARG, "%s: ring is NULL", who);
+  if (b < 0) return fail(TGX_ERR_ARG, "%s: negative batch size %lld", who, (long long)b);
   if (b == 0) return TGX_OK;
-  if (src == nullptr || dst == nullptr || time == nullptr)
-    return fail(TGX_ERR_ARG, "tgx_ring_append: src/dst/time must not be NULL");
+  if (src == nullptr || dst == nullptr || (need_time && time == nullptr))
+    return fail(TGX_ERR_ARG, "%s: src/dst/time must not be NULL", who);
   if (ring->ids == nullptr || ring->times == nullptr || ring->write_pos == nullptr ||
       ring->scratch == nullptr || (ring->feats == nullptr && ring->feat_dim > 0))
-    return fail(TGX_ERR_ARG,
-                "tgx_ring_append: ring arrays (ids, times, feats, write_pos, scratch) must not be NULL");
+    return fail(TGX_ERR_ARG, "%s: ring arrays (ids, times, feats, write_pos, scratch) must not be NULL",
+                who);
   const int esz = feat_elem_bytes(ring->feat_dtype);
-  if (esz == 0) return fail(TGX_ERR_DTYPE, "tgx_ring_append: unsupported feat dtype %d", ring->feat_dtype);
+  if (esz == 0) return fail(TGX_ERR_DTYPE, "%s: unsupported feat dtype %d", who, ring->feat_dtype);
   if (ring->num_nodes <= 0 || ring->num_nodes >= (int64_t(1) << 31))
-    return fail(TGX_ERR_LIMIT, "tgx_ring_append: num_nodes %lld outside [1, 2^31)",
-                (long long)ring->num_nodes);
+    return fail(TGX_ERR_LIMIT, "%s: num_nodes %lld outside [1, 2^31)", who, (long long)ring->num_nodes);
   if (ring->slots < 1 || ring->slots > TGX_MAX_SLOTS)
-    return fail(TGX_ERR_LIMIT, "tgx_ring_append: slots %d outside [1, %d]", ring->slots,
-                TGX_MAX_SLOTS);
-  if (ring->feat_dim < 0) return fail(TGX_ERR_ARG, "tgx_ring_append: negative feat_dim");
+    return fail(TGX_ERR_LIMIT, "%s: slots %d outside [1, %d]", who, ring->slots, TGX_MAX_SLOTS);
+  if (ring->feat_dim < 0) return fail(TGX_ERR_ARG, "%s: negative feat_dim", who);
   const int64_t n = 2 * b;
-  if (n >= (int64_t(1) << 30)) return fail(TGX_ERR_LIMIT, "tgx_ring_append: batch too large");
+  if (n >= (int64_t(1) << 30)) return fail(TGX_ERR_LIMIT, "%s: batch too large", who);
   const size_t need = tgx_ring_append_workspace_size(b);
   if (workspace == nullptr || workspace_bytes < need)
-    return fail(TGX_ERR_ARG, "tgx_ring_append: workspace of %zu bytes needed, got %zu", need,
-                workspace_bytes);
+    return fail(TGX_ERR_ARG, "%s: workspace of %zu bytes needed, got %zu", who, need, workspace_bytes);
 
-  AppendParams P{};
+  P = AppendParams{};
   P.src = src;
   P.dst = dst;
   P.time = time;
@@ -426,17 +699,20 @@ extern "C" int tgx_ring_append(const tgx_ring* ring, const int64_t* src, const i
   P.wp = ring->write_pos;
   P.eids = ring->eids;
   P.cnt = ring->scratch;
-  P.nbase = ring->scratch + ring->num_nodes;
-  P.ctl = ring->scratch + 2 * ring->num_nodes;
+  P.lst = ring->scratch + ring->num_nodes;
+  P.nbase = P.lst;
+  P.ctl = ring->scratch + ctl_offset(ring->num_nodes);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
+  const size_t o_ovf = align256(static_cast<size_t>(n) * 4);
+  const size_t o_groups = o_ovf + align256(static_cast<size_t>(n) * 8);
   P.ticket = reinterpret_cast<int32_t*>(ws);
-  P.list = reinterpret_cast<int32_t*>(ws + align256(static_cast<size_t>(n) * 4));
-  P.groups = reinterpret_cast<int32_t*>(ws + 2 * align256(static_cast<size_t>(n) * 4));
-  P.large = reinterpret_cast<int32_t*>(ws + 2 * align256(static_cast<size_t>(n) * 4) +
-                                       align256(static_cast<size_t>(n / 2 + 1) * 4));
+  P.ovf = reinterpret_cast<int2*>(ws + o_ovf);
+  P.list = reinterpret_cast<int32_t*>(ws + o_ovf);
+  P.groups = reinterpret_cast<int32_t*>(ws + o_groups);
+  P.large = reinterpret_cast<int32_t*>(ws + o_groups + align256(static_cast<size_t>(n / 2 + 1) * 4));
   P.status = status;
 
-  int vec = 2;
+  vec = 2;
   if (P.row_bytes % 16 == 0 && aligned16(ring->feats) && (feat == nullptr || aligned16(feat)))
     vec = 16;
   else if (P.row_bytes % 4 == 0 && (reinterpret_cast<uintptr_t>(ring->feats) & 3u) == 0 &&
@@ -448,28 +724,104 @@ extern "C" int tgx_ring_append(const tgx_ring* ring, const int64_t* src, const i
   P.tpe_log2 = tpe_log2;
   const int64_t epb = kThreads >> tpe_log2;
   P.ga = static_cast<int>((n + epb - 1) / epb);
-  P.gb = static_cast<int>((n / 2 + kCommitWaves) / kCommitWaves);  // at most n/2 groups
-  const int64_t gc = n / (kWave + 1) + 1;                              // at most n/65 large
-  const dim3 grid1(static_cast<unsigned>((n + kThreads - 1) / kThreads));
-  const dim3 grid4(static_cast<unsigned>(P.ga + P.gb + gc));
+  // small / large group roles loop over the device-side group counts, so their
+  // block counts are capped instead of sized for the worst case (n/2, n/65 groups)
+  P.gb = static_cast<int>(std::min<int64_t>((n / 2 + kCommitWaves) / kCommitWaves, kSmallGroupBlocks));
+  return TGX_OK;
+}
 
+bool two_launch(const AppendParams& P) { return P.n <= kFastMaxEntries; }
+
+int launch_plan(const AppendParams& P, hipStream_t stream) {
+  const dim3 grid1(static_cast<unsigned>((P.n + kThreads - 1) / kThreads));
+  if (two_launch(P)) {
+    hipLaunchKernelGGL(fast_plan, grid1, dim3(kThreads), 0, stream, P);
+    return check_launch("fast_plan");
+  }
   hipLaunchKernelGGL(append_count, grid1, dim3(kThreads), 0, stream, P);
   int rc = check_launch("append_count");
   if (rc) return rc;
   hipLaunchKernelGGL(append_groups, grid1, dim3(kThreads), 0, stream, P);
   if ((rc = check_launch("append_groups"))) return rc;
   hipLaunchKernelGGL(append_fill, grid1, dim3(kThreads), 0, stream, P);
-  if ((rc = check_launch("append_fill"))) return rc;
+  return check_launch("append_fill");
+}
+
+template <int VEC>
+void launch_commit_vec(const AppendParams& P, hipStream_t stream) {
+  if (two_launch(P)) {
+    const int64_t gc = std::min<int64_t>(P.n / (kListCap + 1) + 1, kFastLargeBlocks);
+    hipLaunchKernelGGL(fast_commit<VEC>, dim3(static_cast<unsigned>(P.ga + P.gb + gc)),
+                       dim3(kThreads), 0, stream, P);
+  } else {
+    const int64_t gc = std::min<int64_t>(P.n / (kWave + 1) + 1, kLargeGroupBlocks);
+    hipLaunchKernelGGL(append_commit<VEC>, dim3(static_cast<unsigned>(P.ga + P.gb + gc)),
+                       dim3(kThreads), 0, stream, P);
+  }
+}
+
+int launch_commit(const AppendParams& P, int vec, hipStream_t stream) {
   switch (vec) {
     case 16:
-      hipLaunchKernelGGL(append_commit<16>, grid4, dim3(kThreads), 0, stream, P);
+      launch_commit_vec<16>(P, stream);
       break;
     case 4:
-      hipLaunchKernelGGL(append_commit<4>, grid4, dim3(kThreads), 0, stream, P);
+      launch_commit_vec<4>(P, stream);
       break;
     default:
-      hipLaunchKernelGGL(append_commit<2>, grid4, dim3(kThreads), 0, stream, P);
+      launch_commit_vec<2>(P, stream);
       break;
   }
-  return check_launch("append_commit");
+  return check_launch(two_launch(P) ? "fast_commit" : "append_commit");
+}
+
+}  // namespace
+
+extern "C" int tgx_ring_append(const tgx_ring* ring, const int64_t* src, const int64_t* dst,
+                               const double* time, const void* feat, int64_t b,
+                               int64_t eid_base, void* workspace, size_t workspace_bytes,
+                               int32_t* status, void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  AppendParams P;
+  int vec;
+  int rc = setup_append("tgx_ring_append", ring, src, dst, time, feat, b, eid_base, workspace,
+                        workspace_bytes, status, P, vec, true);
+  if (rc != TGX_OK || b == 0) return rc;
+  if ((rc = launch_plan(P, stream))) return rc;
+  return launch_commit(P, vec, stream);
+}
+
+extern "C" int tgx_ring_plan(const tgx_ring* ring, const int64_t* src, const int64_t* dst,
+                             const double* time, int64_t b, void* workspace, size_t workspace_bytes,
+                             void* stream_) {
+  AppendParams P;
+  int vec;
+  int rc = setup_append("tgx_ring_plan", ring, src, dst, time, nullptr, b, 0, workspace,
+                        workspace_bytes, nullptr, P, vec, true);
+  if (rc != TGX_OK || b == 0) return rc;
+  return launch_plan(P, static_cast<hipStream_t>(stream_));
+}
+
+extern "C" int tgx_ring_commit(const tgx_ring* ring, const int64_t* src, const int64_t* dst,
+                               const double* time, const void* feat, int64_t b, int64_t eid_base,
+                               void* workspace, size_t workspace_bytes, int32_t* status,
+                               void* stream_) {
+  AppendParams P;
+  int vec;
+  int rc = setup_append("tgx_ring_commit", ring, src, dst, time, feat, b, eid_base, workspace,
+                        workspace_bytes, status, P, vec, true);
+  if (rc != TGX_OK || b == 0) return rc;
+  return launch_commit(P, vec, static_cast<hipStream_t>(stream_));
+}
+
+extern "C" int tgx_ring_discard(const tgx_ring* ring, const int64_t* src, const int64_t* dst,
+                                int64_t b, void* workspace, size_t workspace_bytes, void* stream_) {
+  AppendParams P;
+  int vec;
+  int rc = setup_append("tgx_ring_discard", ring, src, dst, nullptr, nullptr, b, 0, workspace,
+                        workspace_bytes, nullptr, P, vec, false);
+  if (rc != TGX_OK || b == 0) return rc;
+  const dim3 grid1(static_cast<unsigned>((P.n + kThreads - 1) / kThreads));
+  hipLaunchKernelGGL(append_discard, grid1, dim3(kThreads), 0, static_cast<hipStream_t>(stream_), P);
+  return check_launch("append_discard");
 }

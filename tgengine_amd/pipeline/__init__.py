@@ -57,6 +57,11 @@ class DataPipeline:
         self.graph = graph
         self.time_encoder = time_encoder
         self.queries_per_workgroup = int(queries_per_workgroup)
+        # opt-in: start the ring update of each prepared batch on a side stream
+        # (TemporalGraph.plan_append) for advance() to commit.  Off by default:
+        # on ROCm the two cross-stream event handshakes per batch cost more host
+        # time (about 40 us) than the overlapped plan saves on the device.
+        self.plan_updates = False
         self._plans: dict = {}
         self._te: dict = {}
 
@@ -139,6 +144,9 @@ class DataPipeline:
         device = raw_batch.device
         b = raw_batch.src.shape[0]
         names, qgroups, sizes, per_event = self._query_groups(raw_batch)
+        if self.plan_updates:
+            # before the gather launch, so the plan does not wait for it
+            self.graph.plan_append(raw_batch.src, raw_batch.dst, raw_batch.time)
 
         if spec.edge_ids and not self.graph.track_edge_ids:
             raise ValueError("GatherSpec.edge_ids needs a TemporalGraph built with track_edge_ids=True")
