@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define TGX_ABI_VERSION 5
+#define TGX_ABI_VERSION 6
 
 /* status codes */
 #define TGX_OK 0
@@ -152,6 +152,19 @@ typedef struct tgx_recent_args {
    * end of the kernel's execution); both NULL = plain launch */
   void* timing_start;
   void* timing_stop;
+  /* optional ring plan run by the same launch (append_b > 0): tgx_ring_plan of
+   * the batch append_src/dst/time (append_b events, append_workspace of
+   * tgx_ring_append_workspace_size(append_b) bytes) that the caller appends
+   * next, through tgx_ring_commit (or drops through tgx_ring_discard).  The plan
+   * writes only the ring's scratch and the workspace, so it runs beside the
+   * gather; batches above 16384 events are planned by launches of their own
+   * after the gather.  append_b == 0: no plan. */
+  const int64_t* append_src;
+  const int64_t* append_dst;
+  const double* append_time;
+  int64_t append_b;
+  void* append_workspace;
+  size_t append_workspace_bytes;
 } tgx_recent_args;
 
 #define TGX_MAX_SLOTS 64

@@ -1,0 +1,149 @@
+"""The ring plan that DataPipeline.prepare runs inside its gather launch.
+
+prepare(batch) plans the batch's ring update in the same launch as its gather;
+advance() of the same tensors commits the plan, anything else discards it and
+runs the whole update.  Every case compares the gathered neighbours and the ring
+with the CPU oracle bit for bit: batches the fused plan covers, batches above
+its size (planned by launches of their own), a second prepare before advance, a
+query between plan and commit, advance with other tensors, and the
+AsyncDataPipeline, whose plan is enqueued on its prefetch stream.
+"""
+import dataclasses
+
+import numpy as np
+import pytest
+import torch
+
+import stream_check as S
+from oracle import spec as O
+from tgengine_amd import AsyncDataPipeline, RawBatch
+from tgengine_amd.synthetic import CONFIGS, gen_batch
+
+pytestmark = pytest.mark.gpu
+
+C1 = CONFIGS["c1"]
+
+
+def _setup(cfg):
+    fdt = np.uint16 if cfg.feat_dtype == "bf16" else np.float32
+    g = S.make_graph(cfg)
+    pipe = S.make_pipeline(cfg, g)
+    ring = O.Ring.empty(cfg.num_nodes, cfg.buffer_size, cfg.feat_dim, fdt)
+    return g, pipe, ring
+
+
+def _advance_both(g, ring, rb, bt):
+    g.advance(rb.src, rb.dst, rb.time, rb.edge_feat)
+    O.ring_advance(ring, bt["src"], bt["dst"], bt["time"], bt["feat"])
+
+
+def _check_ring(g, ring, bt, where):
+    S.compare_ring(g, ring, np.concatenate([bt["src"], bt["dst"]]), where)
+    N = g.num_nodes
+    assert int(g._ov_scratch[:N].abs().sum()) == 0, f"{where}: node counters not restored"
+
+
+def _check_status(g):
+    st = g.status()
+    assert st == {"bad_event_nodes": 0, "key_collisions": 0, "bad_query_nodes": 0}, st
+
+
+@pytest.mark.parametrize("batch", [200, 17000])  # fused plan / plan launched after the gather
+def test_prepare_advance_plans_match_the_oracle(batch):
+    cfg = dataclasses.replace(C1, batch=batch)
+    g, pipe, ring = _setup(cfg)
+    w = O.time_weights(100)
+    for i in range(4):
+        bt = gen_batch(cfg, i)
+        rb = S.to_raw(cfg, bt)
+        pb = pipe.prepare(rb)
+        assert (g._plan is not None) == (i > 0)  # the ring exists from the first advance on
+        S.compare_prepared(cfg, pb, bt, ring if i > 0 else None, w, f"batch {i}")
+        _advance_both(g, ring, rb, bt)
+        assert g._plan is None
+        _check_ring(g, ring, bt, f"ring after {i}")
+    _check_status(g)
+
+
+def test_second_prepare_replans_and_queries_between_plan_and_commit():
+    cfg = C1
+    g, pipe, ring = _setup(cfg)
+    w = O.time_weights(100)
+    for i in range(5):
+        bt = gen_batch(cfg, i)
+        rb = S.to_raw(cfg, bt)
+        pipe.prepare(rb)
+        pb = pipe.prepare(rb)  # the first plan is dropped, this one is committed
+        # a plain query sees the ring before this batch while the plan is pending
+        nodes, qt = S.queries_of(bt)
+        nd = g.recent(torch.from_numpy(nodes).cuda(), torch.from_numpy(qt).cuda(), cfg.k)
+        ref = O.recent(nodes, qt, cfg.k, None, ring if i > 0 else None, cfg.feat_dim, np.float32)
+        assert np.array_equal(nd.neighbor_ids.cpu().numpy(), ref.ids), f"batch {i}: recent ids"
+        S.compare_prepared(cfg, pb, bt, ring if i > 0 else None, w, f"batch {i}")
+        _advance_both(g, ring, rb, bt)
+        _check_ring(g, ring, bt, f"ring after {i}")
+    _check_status(g)
+
+
+def test_advance_with_other_tensors_discards_the_plan():
+    cfg = C1
+    g, pipe, ring = _setup(cfg)
+    for i in range(5):
+        bt = gen_batch(cfg, i)
+        rb = S.to_raw(cfg, bt)
+        pipe.prepare(rb)
+        if i % 2:
+            # equal values in other tensors: the plan is dropped, the batch still applies
+            g.advance(rb.src.clone(), rb.dst.clone(), rb.time.clone(), rb.edge_feat)
+            O.ring_advance(ring, bt["src"], bt["dst"], bt["time"], bt["feat"])
+        else:
+            _advance_both(g, ring, rb, bt)
+        assert g._plan is None
+        _check_ring(g, ring, bt, f"ring after {i}")
+    _check_status(g)
+
+
+def test_plan_updates_off_gives_the_same_ring():
+    cfg = C1
+    g, pipe, ring = _setup(cfg)
+    pipe.plan_updates = False
+    for i in range(4):
+        bt = gen_batch(cfg, i)
+        rb = S.to_raw(cfg, bt)
+        pipe.prepare(rb)
+        assert g._plan is None
+        _advance_both(g, ring, rb, bt)
+        _check_ring(g, ring, bt, f"ring after {i}")
+    _check_status(g)
+
+
+class _GivenNegatives:
+    """Negative strategy returning the generator's negatives of each batch."""
+
+    def __init__(self):
+        self.queue = []
+
+    def sample(self, src, dst, time, graph, edge_indices):
+        return self.queue.pop(0)
+
+
+def test_async_pipeline_plans_on_its_prefetch_stream():
+    cfg = C1
+    g = S.make_graph(cfg)
+    neg = _GivenNegatives()
+    spec = S.make_pipeline(cfg, g).spec
+    ap = AsyncDataPipeline(spec, g, neg)
+    ring = O.Ring.empty(cfg.num_nodes, cfg.buffer_size, cfg.feat_dim, np.float32)
+    w = O.time_weights(100)
+    bts = [gen_batch(cfg, i) for i in range(6)]
+    raws = [S.to_raw(cfg, bt) for bt in bts]
+    for i, (bt, rb) in enumerate(zip(bts, raws)):
+        neg.queue.append(rb.neg)
+        ap.start_prefetch(RawBatch(src=rb.src, dst=rb.dst, time=rb.time, edge_feat=rb.edge_feat))
+        rb2, pb = ap.get()
+        S.compare_prepared(cfg, pb, bt, ring if i > 0 else None, w, f"async batch {i}")
+        g.advance(rb2.src, rb2.dst, rb2.time, rb2.edge_feat)
+        O.ring_advance(ring, bt["src"], bt["dst"], bt["time"], bt["feat"])
+        assert g._plan is None
+        _check_ring(g, ring, bt, f"async ring after {i}")
+    _check_status(g)

@@ -61,7 +61,10 @@ class TgxRecentArgs(ctypes.Structure):
                 ("co_mode", c_i32), ("co_a", c_vp), ("co_c", c_vp), ("co_pair", c_vp),
                 ("status", c_vp), ("num_query_groups", c_i32),
                 ("query_groups", TgxQueryGroup * TGX_MAX_QUERY_GROUPS),
-                ("timing_start", c_vp), ("timing_stop", c_vp)]
+                ("timing_start", c_vp), ("timing_stop", c_vp),
+                ("append_src", c_vp), ("append_dst", c_vp), ("append_time", c_vp),
+                ("append_b", c_i64), ("append_workspace", c_vp),
+                ("append_workspace_bytes", ctypes.c_size_t)]
 
 
 # every symbol include/tgx.h declares, with its ctypes signature
@@ -108,7 +111,7 @@ def lib() -> ctypes.CDLL:
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
-        if handle.tgx_abi_version() != 5:
+        if handle.tgx_abi_version() != 6:
             raise RuntimeError("libtgx ABI version mismatch")
         _lib = handle
         return _lib

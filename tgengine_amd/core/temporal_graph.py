@@ -53,19 +53,27 @@ class Snapshot:
     overflow_eids: Optional[Tensor] = None
 
 
-@dataclass
 class _Plan:
-    """A ring update planned by plan_append, waiting for its advance()."""
+    """A ring update planned ahead of its advance() (plan_append, or the plan
+    fused into a gather launch): the batch's tensors, their version counters
+    at planning time and the raw handle of the stream the plan was enqueued on."""
 
-    key: tuple
-    src: Tensor
-    dst: Tensor
-    time: Tensor
-    done: "torch.cuda.Event"
+    __slots__ = ("src", "dst", "time", "versions", "stream")
 
+    def __init__(self, src: Tensor, dst: Tensor, time: Tensor, stream: int):
+        self.src, self.dst, self.time = src, dst, time
+        self.versions = (src._version, dst._version, time._version)
+        self.stream = stream
 
-def _plan_key(*ts: Tensor) -> tuple:
-    return tuple((t.data_ptr(), tuple(t.shape), t.dtype, t._version) for t in ts)
+    def matches(self, src: Tensor, dst: Tensor, time: Tensor) -> bool:
+        """The same tensors (or views of the same storage, shape, strides and
+        dtype), unmodified since the plan (version counters unchanged)."""
+        if not (src is self.src and dst is self.dst and time is self.time):
+            for a, p in ((src, self.src), (dst, self.dst), (time, self.time)):
+                if (a.data_ptr() != p.data_ptr() or a.shape != p.shape or a.dtype != p.dtype
+                        or a.stride() != p.stride()):
+                    return False
+        return (src._version, dst._version, time._version) == self.versions
 
 
 try:
@@ -147,7 +155,6 @@ class TemporalGraph:
         # a ring update planned ahead of its advance() (see plan_append)
         self._plan: Optional[_Plan] = None
         self._plan_ws: Optional[Tensor] = None
-        self._plan_stream = None
         self._plan_lock = threading.Lock()
         self._ring_struct: Optional[_lib.TgxRing] = None
         self._csr_struct: Optional[_lib.TgxCsr] = None
@@ -216,64 +223,72 @@ class TemporalGraph:
         return self._ws
 
     # ------------------------------------------------------------------ planned updates
-    def plan_append(self, src: Tensor, dst: Tensor, time: Tensor) -> bool:
-        """Start the first half of the ring update of a batch that advance() will
-        receive next, on a side stream, so it overlaps the caller's current-stream
-        work (DataPipeline.prepare calls it before its gather launch).
-
-        The plan (tgx_ring_plan: per-node counts and entry lists) reads only
-        src/dst/time and the ring's scratch, never the ring arrays.  advance()
-        commits it when it receives the very same src/dst/time tensors unchanged
-        (same storage, shape, dtype and version counter), otherwise it discards
-        it and runs the whole update.  Returns whether a plan was started."""
+    def _plannable(self, src: Tensor, dst: Tensor, time: Tensor) -> bool:
+        """Whether the batch can be planned ahead: a frozen graph on the GPU whose
+        ring exists, and int64 / float64 contiguous 1-D device inputs."""
         if not self._frozen or self._ov_ids is None or self.device.type != "cuda":
             return False
         b = int(src.shape[0])
-        ok = (b > 0 and dst.shape[0] == b and time.shape[0] == b and src.dim() == 1 and dst.dim() == 1
-              and time.dim() == 1 and src.dtype == torch.int64 and dst.dtype == torch.int64
-              and time.dtype == torch.float64
-              and all(t.device == self.device and t.is_contiguous() for t in (src, dst, time)))
-        if not ok:
+        return (b > 0 and dst.shape[0] == b and time.shape[0] == b and src.dim() == 1
+                and dst.dim() == 1 and time.dim() == 1 and src.dtype == torch.int64
+                and dst.dtype == torch.int64 and time.dtype == torch.float64
+                and all(t.device == self.device and t.is_contiguous() for t in (src, dst, time)))
+
+    def _plan_workspace(self, b: int) -> Tensor:
+        need = int(_lib.lib().tgx_ring_append_workspace_size(b))
+        if self._plan_ws is None or self._plan_ws.numel() < need:
+            self._plan_ws = torch.empty(max(need, 1 << 16), dtype=torch.uint8, device=self.device)
+        return self._plan_ws
+
+    def _order_after(self, stream: int) -> int:
+        """Raw handle of the current stream, made to wait for ``stream`` first when
+        that is another stream."""
+        cur = _stream_handle(self.device)
+        if stream != cur:
+            torch.cuda.current_stream(self.device).wait_stream(
+                torch.cuda.ExternalStream(stream, device=self.device))
+        return cur
+
+    def plan_append(self, src: Tensor, dst: Tensor, time: Tensor) -> bool:
+        """Enqueue the first half of the ring update of a batch that advance()
+        will receive next (tgx_ring_plan, on the current stream).
+
+        The plan (per-node counts and entry lists) reads only src/dst/time and
+        writes only the ring's scratch, never the ring arrays, so queries may run
+        between the plan and its advance.  DataPipeline.prepare runs the same
+        plan inside its gather launch.  advance() commits the plan when it
+        receives the very same src/dst/time tensors unchanged (same storage,
+        shape, dtype and version counter), otherwise it discards it and runs the
+        whole update.  Returns whether a plan was enqueued."""
+        if not self._plannable(src, dst, time):
             return False
         with self._plan_lock:
-            main = torch.cuda.current_stream(self.device)
-            side = self._side_stream()
-            ready = torch.cuda.Event()
-            ready.record(main)          # the batch's inputs and the last commit are enqueued
-            side.wait_event(ready)
             if self._plan is not None:  # an earlier plan nobody advanced: drop it first
-                self._discard_plan(side)
-            need = int(_lib.lib().tgx_ring_append_workspace_size(b))
-            if self._plan_ws is None or self._plan_ws.numel() < need:
-                self._plan_ws = torch.empty(max(need, 1 << 16), dtype=torch.uint8, device=self.device)
-                self._plan_ws.record_stream(side)
-            for t in (src, dst, time):
-                t.record_stream(side)
-            _host().ring_plan(ctypes.addressof(self._ring()), src, dst, time, self._plan_ws,
-                              side.cuda_stream)
-            done = torch.cuda.Event()
-            done.record(side)
-            self._plan = _Plan(_plan_key(src, dst, time), src, dst, time, done)
+                self._discard_plan()
+            stream = _stream_handle(self.device)
+            ws = self._plan_workspace(int(src.shape[0]))
+            _host().ring_plan(ctypes.addressof(self._ring()), src, dst, time, ws, stream)
+            self._plan = _Plan(src, dst, time, stream)
         return True
 
-    def _side_stream(self):
-        if self._plan_stream is None:
-            self._plan_stream = torch.cuda.Stream(device=self.device)
-        return self._plan_stream
-
-    def _discard_plan(self, stream) -> None:
-        """Discard the pending plan on ``stream`` (ordered after the plan)."""
-        plan, self._plan = self._plan, None
-        stream.wait_event(plan.done)
-        _host().ring_discard(ctypes.addressof(self._ring()), plan.src, plan.dst, self._plan_ws,
-                             stream.cuda_stream)
-
-    def _drop_plan(self) -> None:
-        """Discard a pending plan on the current stream (before the ring or its
-        scratch is replaced)."""
+    def _adopt_plan(self, stream) -> None:
+        """The caller has ordered ``stream`` (a torch stream) after the pending
+        plan's stream: a commit or discard on ``stream`` needs no further wait."""
         with self._plan_lock:
             if self._plan is not None:
-                self._discard_plan(torch.cuda.current_stream(self.device))
+                self._plan.stream = stream.cuda_stream
+
+    def _discard_plan(self) -> None:
+        """Discard the pending plan on the current stream (ordered after the plan)."""
+        plan, self._plan = self._plan, None
+        stream = self._order_after(plan.stream)
+        _host().ring_discard(ctypes.addressof(self._ring()), plan.src, plan.dst, self._plan_ws, stream)
+
+    def _drop_plan(self) -> None:
+        """Discard a pending plan (before the ring or its scratch is replaced)."""
+        with self._plan_lock:
+            if self._plan is not None:
+                self._discard_plan()
 
     def advance(self, src: Tensor, dst: Tensor, time: Tensor,
                 edge_feat: Optional[Tensor] = None) -> None:
@@ -284,18 +299,16 @@ class TemporalGraph:
         if self._plan is not None:
             with self._plan_lock:
                 plan = self._plan
-                if plan is not None and self._frozen and plan.key == _plan_key(src, dst, time):
+                if plan is not None and self._frozen and plan.matches(src, dst, time):
                     self._plan = None
                     feat = self._feat_in(edge_feat, b)
-                    main = torch.cuda.current_stream(self.device)
-                    main.wait_event(plan.done)
+                    stream = self._order_after(plan.stream)
                     _host().ring_commit(ctypes.addressof(self._ring()), src, dst, time, feat,
-                                        self._num_edges, self._plan_ws, self._status,
-                                        main.cuda_stream)
+                                        self._num_edges, self._plan_ws, self._status, stream)
                     self._num_edges += b
                     return
                 if plan is not None:
-                    self._discard_plan(torch.cuda.current_stream(self.device))
+                    self._discard_plan()
         if not self._frozen:
             feat = (torch.zeros((b, self.edge_feat_dim), dtype=self.feat_dtype)
                     if edge_feat is None else self._feat_in(edge_feat, b).cpu())
@@ -366,13 +379,15 @@ class TemporalGraph:
                group: int = 1, num_groups: Optional[int] = None, d_t: int = 0,
                te_w: Optional[Tensor] = None, te_b: Optional[Tensor] = None,
                dt_mode: int = _lib.TGX_DT_DYGFORMER, co_mode: int = _lib.TGX_CO_NONE,
-               want_eids: bool = False) -> dict:
+               want_eids: bool = False, append: Optional[tuple] = None) -> dict:
         """One tgx_recent launch.
 
         Queries come either as ``nodes``/``times`` or as ``groups``: a list of
         (nodes, times, times_per) read in place and concatenated in order.  Returns
         lists of per-group views under "ids", "times", "feats", "mask" (bool), and
         "eids" / "te" when asked for, plus "co_a", "co_c", "co_pair" with co-occurrence.
+        ``append``: (src, dst, time) of the batch the caller advances next; when it
+        can be planned (see plan_append) the same launch also plans its ring update.
         """
         if not self._frozen:
             self.freeze_csr()
@@ -390,13 +405,22 @@ class TemporalGraph:
         ev0 = ev1 = 0
         if self.kernel_timer is not None:
             ev0, ev1 = self.kernel_timer.events()
-        res = _host().recent(
-            ctypes.addressof(ring) if ring is not None else 0,
-            ctypes.addressof(csr) if csr is not None else 0,
-            [g[0] for g in groups], [g[1] for g in groups], [int(g[2]) for g in groups],
-            k, self.edge_feat_dim, self.feat_dtype, plan, group,
-            -1 if num_groups is None else int(num_groups), int(d_t), te_w, te_b, int(dt_mode),
-            int(co_mode), bool(want_eids), self._status, _stream_handle(self.device), ev0, ev1)
+        if append is not None and (ring is None or self.device.type != "cuda"):
+            append = None
+        if append is None:
+            res = self._launch_recent(ring, csr, groups, k, plan, group, num_groups, d_t, te_w,
+                                      te_b, dt_mode, co_mode, want_eids, ev0, ev1, None, None)
+        else:
+            # the extension plans the batch when its tensors allow it (int64 /
+            # float64 contiguous 1-D device tensors of one non-zero length)
+            with self._plan_lock:
+                if self._plan is not None:  # an earlier plan nobody advanced: drop it first
+                    self._discard_plan()
+                ws = self._plan_workspace(int(append[0].shape[0]))
+                res = self._launch_recent(ring, csr, groups, k, plan, group, num_groups, d_t, te_w,
+                                          te_b, dt_mode, co_mode, want_eids, ev0, ev1, append, ws)
+                if res[7]:
+                    self._plan = _Plan(append[0], append[1], append[2], _stream_handle(self.device))
         out = {"ids": res[0], "times": res[1], "feats": res[2], "mask": res[3]}
         if want_eids:
             out["eids"] = res[4]
@@ -405,6 +429,18 @@ class TemporalGraph:
         if co_mode != _lib.TGX_CO_NONE:
             out["co_a"], out["co_c"], out["co_pair"] = res[6]
         return out
+
+    def _launch_recent(self, ring, csr, groups, k, plan, group, num_groups, d_t, te_w, te_b,
+                       dt_mode, co_mode, want_eids, ev0, ev1, append, ws):
+        a_src, a_dst, a_time = append if append is not None else (None, None, None)
+        return _host().recent(
+            ctypes.addressof(ring) if ring is not None else 0,
+            ctypes.addressof(csr) if csr is not None else 0,
+            [g[0] for g in groups], [g[1] for g in groups], [int(g[2]) for g in groups],
+            k, self.edge_feat_dim, self.feat_dtype, plan, group,
+            -1 if num_groups is None else int(num_groups), int(d_t), te_w, te_b, int(dt_mode),
+            int(co_mode), bool(want_eids), self._status, _stream_handle(self.device), ev0, ev1,
+            a_src, a_dst, a_time, ws)
 
     def recent(self, nodes: Tensor, times: Tensor, k: int) -> NeighborData:
         """Most recent k neighbours before each query time (reference :183-280)."""

@@ -28,16 +28,35 @@ int64_t ptr(const c10::optional<at::Tensor>& t) {
   return t.has_value() ? reinterpret_cast<int64_t>(t->data_ptr()) : 0;
 }
 
+// 1-D view of t (t itself when it already is 1-D)
+at::Tensor flat(const at::Tensor& t) { return t.dim() == 1 ? t : t.reshape({-1}); }
+
+// the ring plan of a batch can run in the gather launch: int64 / int64 /
+// float64 contiguous 1-D tensors of one non-zero length on the launch's device
+bool plannable(const at::Tensor& s, const at::Tensor& d, const at::Tensor& t, const at::Device& dev) {
+  const int64_t b = s.numel();
+  auto ok = [&](const at::Tensor& x, at::ScalarType st) {
+    return x.defined() && x.dim() == 1 && x.numel() == b && x.scalar_type() == st &&
+           x.device() == dev && x.is_contiguous();
+  };
+  return b > 0 && ok(s, at::kLong) && ok(d, at::kLong) && ok(t, at::kDouble);
+}
+
 // Queries arrive as groups (nodes, times, times_per) read in place by the kernel.
+// append_src/dst/time + append_ws (all or none): the caller's next ring batch,
+// planned by the same launch when plannable() allows.
 // Returns [ids, times, feats, mask(bool), eids|None-placeholder, te|placeholder,
-//          co_a, co_c, co_pair] as lists of per-group views (co_* unsplit).
+//          co_a, co_c, co_pair, planned] as lists of per-group views (co_*
+// unsplit); planned holds one tensor when the batch was planned, else nothing.
 std::vector<std::vector<at::Tensor>> recent(
     int64_t ring_addr, int64_t csr_addr, const std::vector<at::Tensor>& gnodes,
     const std::vector<at::Tensor>& gtimes, const std::vector<int64_t>& gper, int64_t k,
     int64_t feat_dim, at::ScalarType feat_dtype, const c10::optional<at::Tensor>& plan,
     int64_t group, int64_t num_groups, int64_t d_t, const c10::optional<at::Tensor>& te_w,
     const c10::optional<at::Tensor>& te_b, int64_t dt_mode, int64_t co_mode, bool want_eids,
-    const at::Tensor& status, int64_t stream, int64_t ev0, int64_t ev1) {
+    const at::Tensor& status, int64_t stream, int64_t ev0, int64_t ev1,
+    const c10::optional<at::Tensor>& append_src, const c10::optional<at::Tensor>& append_dst,
+    const c10::optional<at::Tensor>& append_time, const c10::optional<at::Tensor>& append_ws) {
   const size_t ng = gnodes.size();
   if (ng == 0 || ng > TGX_MAX_QUERY_GROUPS || gtimes.size() != ng || gper.size() != ng)
     throw std::invalid_argument("recent: 1..4 query groups with matching times");
@@ -46,8 +65,8 @@ std::vector<std::vector<at::Tensor>> recent(
   std::vector<int64_t> sizes(ng);
   int64_t Q = 0;
   for (size_t g = 0; g < ng; ++g) {
-    n[g] = as_dev(gnodes[g].reshape({-1}), at::kLong, dev);
-    t[g] = as_dev(gtimes[g].reshape({-1}), at::kDouble, dev);
+    n[g] = as_dev(flat(gnodes[g]), at::kLong, dev);
+    t[g] = as_dev(flat(gtimes[g]), at::kDouble, dev);
     if (n[g].numel() != t[g].numel() * gper[g])
       throw std::invalid_argument("recent: query group node/time sizes do not match");
     sizes[g] = n[g].numel();
@@ -98,7 +117,21 @@ std::vector<std::vector<at::Tensor>> recent(
   }
   a.timing_start = reinterpret_cast<void*>(ev0);
   a.timing_stop = reinterpret_cast<void*>(ev1);
-  if (Q > 0)
+  bool planned = false;
+  if (append_src.has_value()) {
+    if (!append_dst.has_value() || !append_time.has_value() || !append_ws.has_value())
+      throw std::invalid_argument("recent: append_src/dst/time/ws come together");
+    planned = plannable(*append_src, *append_dst, *append_time, dev);
+  }
+  if (planned) {
+    a.append_src = append_src->data_ptr<int64_t>();
+    a.append_dst = append_dst->data_ptr<int64_t>();
+    a.append_time = append_time->data_ptr<double>();
+    a.append_b = append_src->numel();
+    a.append_workspace = append_ws->data_ptr();
+    a.append_workspace_bytes = static_cast<size_t>(append_ws->numel());
+  }
+  if (Q > 0 || a.append_b > 0)
     check(tgx_recent(reinterpret_cast<const tgx_ring*>(ring_addr),
                      reinterpret_cast<const tgx_csr*>(csr_addr), &a,
                      reinterpret_cast<void*>(stream)),
@@ -114,6 +147,8 @@ std::vector<std::vector<at::Tensor>> recent(
   out.push_back(eids.has_value() ? split(*eids) : std::vector<at::Tensor>{});
   out.push_back(te.has_value() ? split(*te) : std::vector<at::Tensor>{});
   if (co_mode != TGX_CO_NONE) out.push_back({*co_a, *co_c, *co_pair});
+  else out.push_back({});
+  if (planned) out.push_back({*append_src});
   else out.push_back({});
   return out;
 }

@@ -46,6 +46,7 @@
 #include <tuple>
 
 #include "tgx_cos.h"
+#include "tgx_ring_plan.h"
 
 namespace tgx {
 namespace {
@@ -109,6 +110,9 @@ struct Params {
   // work decomposition: m queries per wavefront in sub-groups of 2^lg_bp lanes
   int m, lg_bp;
   int split;  // wavefronts per query (m == 1): each writes every split-th output chunk
+  // fused ring plan: workgroups [0, plan_blocks) plan the caller's next batch
+  PlanParams pl;
+  int plan_blocks;
 };
 
 template <int VEC>
@@ -382,7 +386,12 @@ __global__ __launch_bounds__(kMaxWaves * kWave) __attribute__((amdgpu_waves_per_
   extern __shared__ __align__(16) uint8_t smem[];
   const int lane = threadIdx.x & (kWave - 1);
   const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
-  const int64_t g = blockIdx.x;
+  if (static_cast<int>(blockIdx.x) < P.plan_blocks) {
+    // the plan touches only the ring's scratch, never the arrays gathered here
+    plan_block(P.pl, blockIdx.x, *reinterpret_cast<PlanLds*>(smem));
+    return;
+  }
+  const int64_t g = static_cast<int64_t>(blockIdx.x) - P.plan_blocks;
   const int K = P.K;
   const int B = P.B;
   const int C = P.cand_cap;
@@ -793,7 +802,16 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
     return fail(TGX_ERR_LIMIT, "tgx_recent: group=%d outside [1, %d]", a->group, TGX_MAX_GROUP);
   if (a->num_groups >= (int64_t(1) << 31))
     return fail(TGX_ERR_LIMIT, "tgx_recent: too many groups");
-  if (a->num_queries == 0 || a->num_groups == 0) return TGX_OK;
+  // the caller's next ring batch, planned in this launch (or on its own)
+  PlanParams pl{};
+  const bool want_plan = a->append_b != 0;
+  if (want_plan) {
+    if (ring == nullptr) return fail(TGX_ERR_ARG, "tgx_recent: an append plan needs the ring");
+    const int rc = plan_setup("tgx_recent", ring, a->append_src, a->append_dst, a->append_time,
+                              a->append_b, a->append_workspace, a->append_workspace_bytes, pl);
+    if (rc != TGX_OK) return rc;
+  }
+  if (a->num_queries == 0 || a->num_groups == 0) return want_plan ? launch_plan(pl, stream) : TGX_OK;
   if (a->num_query_groups < 0 || a->num_query_groups > TGX_MAX_QUERY_GROUPS)
     return fail(TGX_ERR_LIMIT, "tgx_recent: %d query groups outside [0, %d]", a->num_query_groups,
                 TGX_MAX_QUERY_GROUPS);
@@ -971,7 +989,12 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
   if ((ev0 == nullptr) != (ev1 == nullptr))
     return fail(TGX_ERR_ARG, "tgx_recent: timing_start and timing_stop must both be set or both NULL");
 
-  const dim3 grid(static_cast<unsigned>(nblocks));
+  // fused plan: one plan workgroup per blockDim entries, dispatched first
+  const bool fuse_plan = want_plan && plan_fused_ok(pl);
+  P.pl = pl;
+  P.plan_blocks = fuse_plan ? static_cast<int>((pl.n + kWave * waves - 1) / (kWave * waves)) : 0;
+  const size_t lds_launch = fuse_plan ? std::max(lds, sizeof(PlanLds)) : lds;
+  const dim3 grid(static_cast<unsigned>(nblocks + P.plan_blocks));
   const dim3 block(kWave * waves);
   static std::once_flag attr_once;
   std::call_once(attr_once, [] {
@@ -986,9 +1009,9 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
   });
   auto launch = [&](auto kernel) {
     if (ev0 != nullptr)
-      hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, ev0, ev1, 0, P);
+      hipExtLaunchKernelGGL(kernel, grid, block, lds_launch, stream, ev0, ev1, 0, P);
     else
-      hipLaunchKernelGGL(kernel, grid, block, lds, stream, P);
+      hipLaunchKernelGGL(kernel, grid, block, lds_launch, stream, P);
   };
   if (vec == 16) {
     if (nreg == 2)
@@ -1002,7 +1025,9 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
   } else {
     launch(recent_fused<2, 0>);
   }
-  return check_launch("recent_fused");
+  const int rc = check_launch("recent_fused");
+  if (rc != TGX_OK || !want_plan || fuse_plan) return rc;
+  return launch_plan(pl, stream);  // batches beyond the fused plan's size
 }
 
 extern "C" int tgx_co_occurrence(const int32_t* a_ids, const int32_t* c_ids, int64_t pairs,

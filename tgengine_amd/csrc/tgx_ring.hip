@@ -38,7 +38,7 @@
 //            windows walked down from the top of the batch.
 // Every path writes the kept entries, restores count[u] to zero and advances
 // write_pos.  Feature rows move as 16-byte vectors when the row allows it.
-#include "tgx_internal.h"
+#include "tgx_ring_plan.h"
 
 #include <algorithm>
 
@@ -50,27 +50,8 @@ constexpr int kCommitWaves = kThreads / kWave;
 constexpr int kWinBits = 8192;                 // bitmap window (indices)
 constexpr int kWinWords = kWinBits / 32;       // 256 words = 1 KB
 static_assert(kWinWords == kThreads, "one bitmap word per thread");
-// ctl words (ring scratch): four-launch cursors, shared diagnostics, two-launch cursors
-enum {
-  kCtlCursor = 0, kCtlGroups = 1, kCtlTimeOk = 2, kCtlLarge = 3, kCtlBad = 4,
-  kCtlFCursor = 8,  // uint64 over words 8, 9: two-launch overflow | groups | large counts
-  kCtlFDone = 10
-};
-// fields of the two-launch cursor word (every count is at most n <= 2^15)
-constexpr int kFieldBits = 21;
-constexpr uint64_t kFieldMask = (uint64_t(1) << kFieldBits) - 1;
-__host__ __device__ constexpr int field(uint64_t x, int f) {
-  return static_cast<int>((x >> (f * kFieldBits)) & kFieldMask);
-}
-enum { kFOvf = 0, kFGroups = 1, kFLarge = 2 };
-constexpr int kCtlWords = 16;
-constexpr int kHashBits = 9;                 // tickets: LDS hash of 2*kThreads slots
-constexpr int kHash = 1 << kHashBits;
-static_assert(kHash >= 2 * kThreads, "hash table at most half full");
 constexpr int64_t kSmallGroupBlocks = 256;  // commit blocks for small groups (4 waves each)
 constexpr int64_t kLargeGroupBlocks = 64;   // four-launch commit blocks for large groups
-constexpr int kListCap = 8;                 // node-indexed list entries per node
-constexpr int64_t kFastMaxEntries = 32768;  // two-launch path up to this many entries
 constexpr int kFastWords = kFastMaxEntries / 32;  // two-launch bitmap of the whole batch
 constexpr int kWordsPerThread = kFastWords / kThreads;
 static_assert(kWordsPerThread * kThreads == kFastWords, "bitmap words split evenly");
@@ -84,11 +65,6 @@ __device__ __forceinline__ int64_t ring_slot(int64_t w, int off, int B) {
   if (x < (uint64_t(1) << 32))
     return static_cast<int64_t>(static_cast<uint32_t>(x) % static_cast<uint32_t>(B));
   return static_cast<int64_t>(x % static_cast<uint64_t>(B));
-}
-
-__device__ __forceinline__ int64_t entry_node(const int64_t* src, const int64_t* dst, int64_t i,
-                                              int64_t b) {
-  return i < b ? src[i] : dst[i - b];
 }
 
 __device__ __forceinline__ void wave_sync_lds() {
@@ -112,14 +88,8 @@ struct VecT<2> {
   using T = uint16_t;
 };
 
-struct AppendParams {
-  const int64_t* src;
-  const int64_t* dst;
-  const double* time;
+struct AppendParams : PlanParams {
   const uint8_t* feat;  // [b, row_bytes] or null (zero rows)
-  int64_t b;
-  int64_t n;
-  int64_t N;
   int B;
   int64_t row_bytes;
   int64_t eid_base;
@@ -128,74 +98,13 @@ struct AppendParams {
   uint8_t* feats;
   int64_t* wp;
   int64_t* eids;
-  int32_t* cnt;     // [N] per-node counters (zero between calls)
-  int32_t* lst;     // [N, kListCap] two-launch lists
-  int32_t* nbase;   // [N] four-launch list base of multi-entry nodes (aliases lst)
-  int32_t* ctl;     // [kCtlWords] cursors and diagnostics
-  int32_t* ticket;  // [n] four-launch tickets
-  int32_t* list;    // [n] four-launch lists
-  int2* ovf;        // [n] two-launch overflow (node, entry) pairs (over list)
-  int32_t* groups;  // [n/2 + 1] groups
-  int32_t* large;   // [n/(kListCap+1) + 1] large groups
+  int32_t* nbase;   // [N] four-launch list base of multi-entry nodes (over lst)
+  int32_t* list;    // [n] four-launch lists (over ovf)
   int32_t* status;
   int tpe_log2;     // lanes per entry (singleton copy)
   int ga;           // blocks of the singleton role in commit
   int gb;           // blocks of the small-group role
 };
-
-// node of entry i (-1 when outside [0, N): counted as a bad entry) and whether
-// its event time keeps the reference key from*(int(max t)+2)+i lexicographic
-// (int(max t)+2 > n-1)
-__device__ __forceinline__ int32_t entry_prologue(const AppendParams& P, int64_t i, int& bad,
-                                                  bool& time_ok) {
-  bad = 0;
-  time_ok = false;
-  if (i >= P.n) return -1;
-  const int64_t uu = entry_node(P.src, P.dst, i, P.b);
-  if (i < P.b) time_ok = trunc(P.time[i]) > static_cast<double>(P.n - 3);
-  if (uu < 0 || uu >= P.N) {
-    bad = 1;
-    return -1;
-  }
-  return static_cast<int32_t>(uu);
-}
-
-// Ticket of the entry of node u (>= 0), or -1 for u < 0.  Equal nodes of the
-// workgroup are aggregated in an LDS hash table (open addressing, at most half
-// full): each lane takes a local rank from its node's slot, then one global
-// atomic per distinct node reserves the workgroup's tickets.
-__device__ __forceinline__ int32_t node_ticket(const AppendParams& P, int32_t u, int32_t* hkey,
-                                               int32_t* hcnt, int32_t* hbase) {
-  for (int s = threadIdx.x; s < kHash; s += kThreads) {
-    hkey[s] = -1;
-    hcnt[s] = 0;
-  }
-  __syncthreads();
-  int hs = -1, rank = 0;
-  if (u >= 0) {
-    hs = static_cast<int>((static_cast<uint32_t>(u) * 2654435761u) >> (32 - kHashBits));
-    while (true) {  // terminates: fewer keys than slots
-      const int32_t old = atomicCAS(&hkey[hs], -1, u);
-      if (old == -1 || old == u) break;
-      hs = (hs + 1) & (kHash - 1);
-    }
-    rank = atomicAdd(&hcnt[hs], 1);
-  }
-  __syncthreads();
-  for (int s = threadIdx.x; s < kHash; s += kThreads)
-    if (hkey[s] >= 0) hbase[s] = atomicAdd(&P.cnt[hkey[s]], hcnt[s]);
-  __syncthreads();
-  return u >= 0 ? hbase[hs] + rank : -1;
-}
-
-__device__ __forceinline__ void report_diagnostics(const AppendParams& P, int bad, bool time_ok) {
-  const uint64_t bm = __ballot(bad);
-  const uint64_t tm = __ballot(time_ok);
-  if ((threadIdx.x & (kWave - 1)) == 0) {
-    if (bm) atomicAdd(&P.ctl[kCtlBad], __popcll(bm));
-    if (tm) atomicOr(&P.ctl[kCtlTimeOk], 1);
-  }
-}
 
 // the plan's diagnostics reach the status words only when the batch commits
 __device__ __forceinline__ void commit_diagnostics(const AppendParams& P) {
@@ -208,10 +117,8 @@ __device__ __forceinline__ void commit_diagnostics(const AppendParams& P) {
 }
 
 // ---- four-launch 1. count ----------------------------------------------------
-__global__ __launch_bounds__(kThreads) void append_count(AppendParams P) {
-  __shared__ int32_t hkey[kHash];
-  __shared__ int32_t hcnt[kHash];
-  __shared__ int32_t hbase[kHash];
+__global__ __launch_bounds__(kThreads) void append_count(PlanParams P) {
+  __shared__ PlanLds L;
   const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   if (i == 0) {
     P.ctl[kCtlCursor] = 0;
@@ -221,55 +128,15 @@ __global__ __launch_bounds__(kThreads) void append_count(AppendParams P) {
   int bad;
   bool time_ok;
   const int32_t u = entry_prologue(P, i, bad, time_ok);
-  const int32_t t = node_ticket(P, u, hkey, hcnt, hbase);
+  const int32_t t = node_ticket(P, u, L);
   if (i < P.n) P.ticket[i] = t;
   report_diagnostics(P, bad, time_ok);
 }
 
 // ---- two-launch 1. plan -------------------------------------------------------
-__global__ __launch_bounds__(kThreads) void fast_plan(AppendParams P) {
-  __shared__ int32_t hkey[kHash];
-  __shared__ int32_t hcnt[kHash];
-  __shared__ int32_t hbase[kHash];
-  __shared__ uint64_t wofs[kCommitWaves + 1];
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  const int wv = threadIdx.x / kWave;
-  const int lane = threadIdx.x & (kWave - 1);
-  int bad;
-  bool time_ok;
-  const int32_t u = entry_prologue(P, i, bad, time_ok);
-  const int32_t t = node_ticket(P, u, hkey, hcnt, hbase);
-  if (t >= 0 && t < kListCap) P.lst[static_cast<int64_t>(u) * kListCap + t] = static_cast<int32_t>(i);
-  // appends to the overflow, group and large-group lists: wave counts packed in
-  // one word, a workgroup prefix in LDS, one cursor atomic per workgroup
-  const uint64_t om = __ballot(t >= kListCap);
-  const uint64_t gm = __ballot(t == 1);
-  const uint64_t lm = __ballot(t == kListCap);
-  if (lane == 0)
-    wofs[wv] = static_cast<uint64_t>(__popcll(om)) |
-               (static_cast<uint64_t>(__popcll(gm)) << (kFGroups * kFieldBits)) |
-               (static_cast<uint64_t>(__popcll(lm)) << (kFLarge * kFieldBits));
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint64_t tot = 0;
-    for (int w = 0; w < kCommitWaves; ++w) {
-      const uint64_t c = wofs[w];
-      wofs[w] = tot;
-      tot += c;
-    }
-    wofs[kCommitWaves] =
-        tot != 0 ? atomicAdd(reinterpret_cast<unsigned long long*>(P.ctl + kCtlFCursor),
-                             static_cast<unsigned long long>(tot))
-                 : 0;
-  }
-  __syncthreads();
-  const uint64_t below = (uint64_t(1) << lane) - 1;
-  const uint64_t at = wofs[kCommitWaves] + wofs[wv];
-  if (t >= kListCap)
-    P.ovf[field(at, kFOvf) + __popcll(om & below)] = make_int2(u, static_cast<int32_t>(i));
-  if (t == 1) P.groups[field(at, kFGroups) + __popcll(gm & below)] = u;
-  if (t == kListCap) P.large[field(at, kFLarge) + __popcll(lm & below)] = u;
-  report_diagnostics(P, bad, time_ok);
+__global__ __launch_bounds__(kThreads) void fast_plan(PlanParams P) {
+  __shared__ PlanLds L;
+  plan_block(P, blockIdx.x, L);
 }
 
 // ---- four-launch 2. groups --------------------------------------------------------------
@@ -619,7 +486,7 @@ __global__ __launch_bounds__(kThreads) void fast_commit(AppendParams P) {
 }
 
 // ---- discard: restore the scratch of a planned batch without committing it ----
-__global__ __launch_bounds__(kThreads) void append_discard(AppendParams P) {
+__global__ __launch_bounds__(kThreads) void append_discard(PlanParams P) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   if (i == 0) {
     P.ctl[kCtlTimeOk] = 0;
@@ -632,9 +499,6 @@ __global__ __launch_bounds__(kThreads) void append_discard(AppendParams P) {
 }
 
 size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
-
-// ring scratch: counters [N] | lists [N, kListCap] | ctl (16-byte aligned)
-int64_t ctl_offset(int64_t num_nodes) { return ((1 + kListCap) * num_nodes + 3) & ~int64_t(3); }
 
 }  // namespace
 }  // namespace tgx
@@ -654,42 +518,83 @@ extern "C" size_t tgx_ring_scratch_size(int64_t num_nodes) {
   return static_cast<size_t>(ctl_offset(num_nodes) + kCtlWords) * sizeof(int32_t);
 }
 
-namespace {
+namespace tgx {
 
-// argument checks and the kernel parameters shared by plan / commit / discard
-int setup_append(const char* who, const tgx_ring* ring, const int64_t* src, const int64_t* dst,
-                 const double* time, const void* feat, int64_t b, int64_t eid_base, void* workspace,
-                 size_t workspace_bytes, int32_t* status, AppendParams& P, int& vec, bool need_time) {
+int plan_setup(const char* who, const tgx_ring* ring, const int64_t* src, const int64_t* dst,
+               const double* time, int64_t b, void* workspace, size_t workspace_bytes,
+               PlanParams& P) {
+  P = PlanParams{};
   if (ring == nullptr) return fail(TGX_ERR_ARG, "%s: ring is NULL", who);
   if (b < 0) return fail(TGX_ERR_ARG, "%s: negative batch size %lld", who, (long long)b);
   if (b == 0) return TGX_OK;
-  if (src == nullptr || dst == nullptr || (need_time && time == nullptr))
+  if (src == nullptr || dst == nullptr || time == nullptr)
     return fail(TGX_ERR_ARG, "%s: src/dst/time must not be NULL", who);
-  if (ring->ids == nullptr || ring->times == nullptr || ring->write_pos == nullptr ||
-      ring->scratch == nullptr || (ring->feats == nullptr && ring->feat_dim > 0))
-    return fail(TGX_ERR_ARG, "%s: ring arrays (ids, times, feats, write_pos, scratch) must not be NULL",
-                who);
-  const int esz = feat_elem_bytes(ring->feat_dtype);
-  if (esz == 0) return fail(TGX_ERR_DTYPE, "%s: unsupported feat dtype %d", who, ring->feat_dtype);
+  if (ring->scratch == nullptr) return fail(TGX_ERR_ARG, "%s: ring scratch must not be NULL", who);
   if (ring->num_nodes <= 0 || ring->num_nodes >= (int64_t(1) << 31))
     return fail(TGX_ERR_LIMIT, "%s: num_nodes %lld outside [1, 2^31)", who, (long long)ring->num_nodes);
-  if (ring->slots < 1 || ring->slots > TGX_MAX_SLOTS)
-    return fail(TGX_ERR_LIMIT, "%s: slots %d outside [1, %d]", who, ring->slots, TGX_MAX_SLOTS);
-  if (ring->feat_dim < 0) return fail(TGX_ERR_ARG, "%s: negative feat_dim", who);
   const int64_t n = 2 * b;
   if (n >= (int64_t(1) << 30)) return fail(TGX_ERR_LIMIT, "%s: batch too large", who);
   const size_t need = tgx_ring_append_workspace_size(b);
   if (workspace == nullptr || workspace_bytes < need)
     return fail(TGX_ERR_ARG, "%s: workspace of %zu bytes needed, got %zu", who, need, workspace_bytes);
-
-  P = AppendParams{};
   P.src = src;
   P.dst = dst;
   P.time = time;
-  P.feat = static_cast<const uint8_t*>(feat);
   P.b = b;
   P.n = n;
   P.N = ring->num_nodes;
+  P.cnt = ring->scratch;
+  P.lst = ring->scratch + ring->num_nodes;
+  P.ctl = ring->scratch + ctl_offset(ring->num_nodes);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  const size_t o_ovf = align256(static_cast<size_t>(n) * 4);
+  const size_t o_groups = o_ovf + align256(static_cast<size_t>(n) * 8);
+  P.ticket = reinterpret_cast<int32_t*>(ws);
+  P.ovf = reinterpret_cast<int2*>(ws + o_ovf);
+  P.groups = reinterpret_cast<int32_t*>(ws + o_groups);
+  P.large = reinterpret_cast<int32_t*>(ws + o_groups + align256(static_cast<size_t>(n / 2 + 1) * 4));
+  return TGX_OK;
+}
+
+int launch_plan(const PlanParams& P, hipStream_t stream) {
+  const dim3 grid1(static_cast<unsigned>((P.n + kThreads - 1) / kThreads));
+  if (plan_fused_ok(P)) {
+    hipLaunchKernelGGL(fast_plan, grid1, dim3(kThreads), 0, stream, P);
+    return check_launch("fast_plan");
+  }
+  // the four-launch plan: groups and fill also read the lists' aliases
+  AppendParams A{};
+  static_cast<PlanParams&>(A) = P;
+  A.nbase = P.lst;
+  A.list = reinterpret_cast<int32_t*>(P.ovf);
+  hipLaunchKernelGGL(append_count, grid1, dim3(kThreads), 0, stream, static_cast<const PlanParams&>(A));
+  int rc = check_launch("append_count");
+  if (rc) return rc;
+  hipLaunchKernelGGL(append_groups, grid1, dim3(kThreads), 0, stream, A);
+  if ((rc = check_launch("append_groups"))) return rc;
+  hipLaunchKernelGGL(append_fill, grid1, dim3(kThreads), 0, stream, A);
+  return check_launch("append_fill");
+}
+
+namespace {
+
+// argument checks and the kernel parameters shared by append / commit
+int setup_append(const char* who, const tgx_ring* ring, const int64_t* src, const int64_t* dst,
+                 const double* time, const void* feat, int64_t b, int64_t eid_base, void* workspace,
+                 size_t workspace_bytes, int32_t* status, AppendParams& P, int& vec) {
+  P = AppendParams{};
+  int rc = plan_setup(who, ring, src, dst, time, b, workspace, workspace_bytes, P);
+  if (rc != TGX_OK || b == 0) return rc;
+  if (ring->ids == nullptr || ring->times == nullptr || ring->write_pos == nullptr ||
+      (ring->feats == nullptr && ring->feat_dim > 0))
+    return fail(TGX_ERR_ARG, "%s: ring arrays (ids, times, feats, write_pos) must not be NULL", who);
+  const int esz = feat_elem_bytes(ring->feat_dtype);
+  if (esz == 0) return fail(TGX_ERR_DTYPE, "%s: unsupported feat dtype %d", who, ring->feat_dtype);
+  if (ring->slots < 1 || ring->slots > TGX_MAX_SLOTS)
+    return fail(TGX_ERR_LIMIT, "%s: slots %d outside [1, %d]", who, ring->slots, TGX_MAX_SLOTS);
+  if (ring->feat_dim < 0) return fail(TGX_ERR_ARG, "%s: negative feat_dim", who);
+  const int64_t n = P.n;
+  P.feat = static_cast<const uint8_t*>(feat);
   P.B = ring->slots;
   P.row_bytes = static_cast<int64_t>(ring->feat_dim) * esz;
   P.eid_base = eid_base;
@@ -698,18 +603,8 @@ int setup_append(const char* who, const tgx_ring* ring, const int64_t* src, cons
   P.feats = static_cast<uint8_t*>(ring->feats);
   P.wp = ring->write_pos;
   P.eids = ring->eids;
-  P.cnt = ring->scratch;
-  P.lst = ring->scratch + ring->num_nodes;
   P.nbase = P.lst;
-  P.ctl = ring->scratch + ctl_offset(ring->num_nodes);
-  uint8_t* ws = static_cast<uint8_t*>(workspace);
-  const size_t o_ovf = align256(static_cast<size_t>(n) * 4);
-  const size_t o_groups = o_ovf + align256(static_cast<size_t>(n) * 8);
-  P.ticket = reinterpret_cast<int32_t*>(ws);
-  P.ovf = reinterpret_cast<int2*>(ws + o_ovf);
-  P.list = reinterpret_cast<int32_t*>(ws + o_ovf);
-  P.groups = reinterpret_cast<int32_t*>(ws + o_groups);
-  P.large = reinterpret_cast<int32_t*>(ws + o_groups + align256(static_cast<size_t>(n / 2 + 1) * 4));
+  P.list = reinterpret_cast<int32_t*>(P.ovf);
   P.status = status;
 
   vec = 2;
@@ -730,26 +625,9 @@ int setup_append(const char* who, const tgx_ring* ring, const int64_t* src, cons
   return TGX_OK;
 }
 
-bool two_launch(const AppendParams& P) { return P.n <= kFastMaxEntries; }
-
-int launch_plan(const AppendParams& P, hipStream_t stream) {
-  const dim3 grid1(static_cast<unsigned>((P.n + kThreads - 1) / kThreads));
-  if (two_launch(P)) {
-    hipLaunchKernelGGL(fast_plan, grid1, dim3(kThreads), 0, stream, P);
-    return check_launch("fast_plan");
-  }
-  hipLaunchKernelGGL(append_count, grid1, dim3(kThreads), 0, stream, P);
-  int rc = check_launch("append_count");
-  if (rc) return rc;
-  hipLaunchKernelGGL(append_groups, grid1, dim3(kThreads), 0, stream, P);
-  if ((rc = check_launch("append_groups"))) return rc;
-  hipLaunchKernelGGL(append_fill, grid1, dim3(kThreads), 0, stream, P);
-  return check_launch("append_fill");
-}
-
 template <int VEC>
 void launch_commit_vec(const AppendParams& P, hipStream_t stream) {
-  if (two_launch(P)) {
+  if (plan_fused_ok(P)) {
     const int64_t gc = std::min<int64_t>(P.n / (kListCap + 1) + 1, kFastLargeBlocks);
     hipLaunchKernelGGL(fast_commit<VEC>, dim3(static_cast<unsigned>(P.ga + P.gb + gc)),
                        dim3(kThreads), 0, stream, P);
@@ -772,10 +650,11 @@ int launch_commit(const AppendParams& P, int vec, hipStream_t stream) {
       launch_commit_vec<2>(P, stream);
       break;
   }
-  return check_launch(two_launch(P) ? "fast_commit" : "append_commit");
+  return check_launch(plan_fused_ok(P) ? "fast_commit" : "append_commit");
 }
 
 }  // namespace
+}  // namespace tgx
 
 extern "C" int tgx_ring_append(const tgx_ring* ring, const int64_t* src, const int64_t* dst,
                                const double* time, const void* feat, int64_t b,
@@ -785,7 +664,7 @@ extern "C" int tgx_ring_append(const tgx_ring* ring, const int64_t* src, const i
   AppendParams P;
   int vec;
   int rc = setup_append("tgx_ring_append", ring, src, dst, time, feat, b, eid_base, workspace,
-                        workspace_bytes, status, P, vec, true);
+                        workspace_bytes, status, P, vec);
   if (rc != TGX_OK || b == 0) return rc;
   if ((rc = launch_plan(P, stream))) return rc;
   return launch_commit(P, vec, stream);
@@ -794,10 +673,8 @@ extern "C" int tgx_ring_append(const tgx_ring* ring, const int64_t* src, const i
 extern "C" int tgx_ring_plan(const tgx_ring* ring, const int64_t* src, const int64_t* dst,
                              const double* time, int64_t b, void* workspace, size_t workspace_bytes,
                              void* stream_) {
-  AppendParams P;
-  int vec;
-  int rc = setup_append("tgx_ring_plan", ring, src, dst, time, nullptr, b, 0, workspace,
-                        workspace_bytes, nullptr, P, vec, true);
+  PlanParams P;
+  int rc = plan_setup("tgx_ring_plan", ring, src, dst, time, b, workspace, workspace_bytes, P);
   if (rc != TGX_OK || b == 0) return rc;
   return launch_plan(P, static_cast<hipStream_t>(stream_));
 }
@@ -809,17 +686,17 @@ extern "C" int tgx_ring_commit(const tgx_ring* ring, const int64_t* src, const i
   AppendParams P;
   int vec;
   int rc = setup_append("tgx_ring_commit", ring, src, dst, time, feat, b, eid_base, workspace,
-                        workspace_bytes, status, P, vec, true);
+                        workspace_bytes, status, P, vec);
   if (rc != TGX_OK || b == 0) return rc;
   return launch_commit(P, vec, static_cast<hipStream_t>(stream_));
 }
 
 extern "C" int tgx_ring_discard(const tgx_ring* ring, const int64_t* src, const int64_t* dst,
                                 int64_t b, void* workspace, size_t workspace_bytes, void* stream_) {
-  AppendParams P;
-  int vec;
-  int rc = setup_append("tgx_ring_discard", ring, src, dst, nullptr, nullptr, b, 0, workspace,
-                        workspace_bytes, nullptr, P, vec, false);
+  // the plan's time array is not read by the discard
+  static const double kNoTime = 0.0;
+  PlanParams P;
+  int rc = plan_setup("tgx_ring_discard", ring, src, dst, &kNoTime, b, workspace, workspace_bytes, P);
   if (rc != TGX_OK || b == 0) return rc;
   const dim3 grid1(static_cast<unsigned>((P.n + kThreads - 1) / kThreads));
   hipLaunchKernelGGL(append_discard, grid1, dim3(kThreads), 0, static_cast<hipStream_t>(stream_), P);

@@ -57,11 +57,10 @@ class DataPipeline:
         self.graph = graph
         self.time_encoder = time_encoder
         self.queries_per_workgroup = int(queries_per_workgroup)
-        # opt-in: start the ring update of each prepared batch on a side stream
-        # (TemporalGraph.plan_append) for advance() to commit.  Off by default:
-        # on ROCm the two cross-stream event handshakes per batch cost more host
-        # time (about 40 us) than the overlapped plan saves on the device.
-        self.plan_updates = False
+        # plan the ring update of each prepared batch inside its gather launch
+        # (the plan writes only the ring's scratch); the following advance() of
+        # the same tensors then makes a single commit launch
+        self.plan_updates = True
         self._plans: dict = {}
         self._te: dict = {}
 
@@ -144,9 +143,7 @@ class DataPipeline:
         device = raw_batch.device
         b = raw_batch.src.shape[0]
         names, qgroups, sizes, per_event = self._query_groups(raw_batch)
-        if self.plan_updates:
-            # before the gather launch, so the plan does not wait for it
-            self.graph.plan_append(raw_batch.src, raw_batch.dst, raw_batch.time)
+        append = (raw_batch.src, raw_batch.dst, raw_batch.time) if self.plan_updates else None
 
         if spec.edge_ids and not self.graph.track_edge_ids:
             raise ValueError("GatherSpec.edge_ids needs a TemporalGraph built with track_edge_ids=True")
@@ -159,6 +156,8 @@ class DataPipeline:
         dt_mode = _DT_MODES[spec.dt_mode]
 
         if k2 > 0:
+            if append is not None:  # several launches here: the plan gets its own
+                self.graph.plan_append(*append)
             all_nodes = torch.cat([g[0].reshape(-1) for g in qgroups])
             all_times = torch.cat([g[1].repeat_interleave(g[2]) if g[2] > 1 else g[1]
                                    for g in qgroups])
@@ -176,7 +175,8 @@ class DataPipeline:
                 o2 = self._fused(qgroups, k, b, per_event, d_t, te_w, te_b, dt_mode, co_mode)
                 out.update({kk: o2[kk] for kk in ("te", "co_a", "co_c", "co_pair") if kk in o2})
         else:
-            out = self._fused(qgroups, k, b, per_event, d_t, te_w, te_b, dt_mode, co_mode)
+            out = self._fused(qgroups, k, b, per_event, d_t, te_w, te_b, dt_mode, co_mode,
+                              append=append)
             extra = {}
 
         parts = {kk: out.get(kk) for kk in ("ids", "times", "feats", "mask", "te", "eids")}
@@ -210,7 +210,8 @@ class DataPipeline:
             node_labels=raw_batch.node_labels, edge_labels=raw_batch.edge_labels,
             node_feat=raw_batch.node_feat, co_occurrence_freq=co_freq)
 
-    def _fused(self, qgroups, k, b, per_event, d_t, te_w, te_b, dt_mode, co_mode) -> dict:
+    def _fused(self, qgroups, k, b, per_event, d_t, te_w, te_b, dt_mode, co_mode,
+               append=None) -> dict:
         g = self.graph
         if co_mode != _lib.TGX_CO_NONE:
             # event-major groups: event p -> [src p, dst p, its negatives, neg_src p]
@@ -224,10 +225,10 @@ class DataPipeline:
             plan = self._plan(("ev", b, tuple(per_event)), b, offs)
             return g._query(None, None, k, groups=qgroups, plan=plan, group=G, num_groups=b,
                             d_t=d_t, te_w=te_w, te_b=te_b, dt_mode=dt_mode, co_mode=co_mode,
-                            want_eids=self.spec.edge_ids)
+                            want_eids=self.spec.edge_ids, append=append)
         return g._query(None, None, k, groups=qgroups, group=self.queries_per_workgroup,
                         d_t=d_t, te_w=te_w, te_b=te_b, dt_mode=dt_mode,
-                        want_eids=self.spec.edge_ids)
+                        want_eids=self.spec.edge_ids, append=append)
 
     @staticmethod
     def _co_occur_from_neighbors(src_nbrs: NeighborData, dst_nbrs: NeighborData) -> Tensor:

@@ -8,7 +8,8 @@ the side stream (the reference's native kernels ignore the current stream).
 Ordering protocol (unchanged): ``start_prefetch`` makes the side stream wait
 for the caller's stream, so it sees the graph after ``advance(i)``; ``get``
 joins the thread, re-raises its exception, and makes the caller's stream wait
-for the side stream.
+for the side stream (which also orders the ring plan that prepare() enqueued
+there before the caller's ``advance``).
 """
 from __future__ import annotations
 
@@ -73,7 +74,11 @@ class AsyncDataPipeline:
         if self._exc is not None:
             exc, self._exc = self._exc, None
             raise exc
-        torch.cuda.current_stream(self._graph.device).wait_stream(self._prefetch_stream)
+        caller = torch.cuda.current_stream(self._graph.device)
+        caller.wait_stream(self._prefetch_stream)
+        # the ring plan made by prepare() on the side stream is now ordered before
+        # the caller's stream, where advance() commits it
+        self._graph._adopt_plan(caller)
         result, self._result = self._result, None
         return result
 
