@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define TGX_ABI_VERSION 6
+#define TGX_ABI_VERSION 7
 
 /* status codes */
 #define TGX_OK 0
@@ -206,6 +206,41 @@ int tgx_ring_commit(const tgx_ring* ring, const int64_t* src, const int64_t* dst
                     void* workspace, size_t workspace_bytes, int32_t* status, void* stream);
 int tgx_ring_discard(const tgx_ring* ring, const int64_t* src, const int64_t* dst, int64_t b,
                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* Frozen-CSR build (TemporalGraph.freeze_csr, temporal_graph.py:133-181).
+ * The n directed entries of the pre-freeze advance() calls, in build order
+ * (per call: [src->dst for every event, dst->src for every event]), are sorted
+ * stably by time, then stably by node: a node's entries end up time-ascending
+ * with ties in build order.  Outputs (the tgx_csr arrays): out_offsets [N+1],
+ * out_ids int32 [n] (= to), out_times [n], out_feats [n, feat_dim] (row of the
+ * entry's event in feats, zero when feats is NULL), out_eids [n] (= event, may
+ * be NULL).  Entries whose node is outside [0, N), or whose event is outside
+ * [0, num_events) while feats is set, are counted in
+ * status[TGX_ST_BAD_EVENT_NODE] (out-of-range nodes sort after every node).
+ * workspace: tgx_csr_build_workspace_size(n) bytes, no initialisation needed. */
+typedef struct tgx_csr_build_args {
+  int64_t num_nodes;
+  int64_t num_entries;
+  const int64_t* from;     /* [n] node of each entry */
+  const int64_t* to;       /* [n] neighbour id */
+  const double* time;      /* [n] */
+  const int64_t* event;    /* [n] event of each entry: edge id and feature row (NULL when unused) */
+  const void* feats;       /* [num_events, feat_dim] in feat_dtype, or NULL */
+  int64_t num_events;
+  int32_t feat_dim;
+  int32_t feat_dtype;
+  int64_t* out_offsets;
+  int32_t* out_ids;
+  double* out_times;
+  void* out_feats;
+  int64_t* out_eids;
+  void* workspace;
+  size_t workspace_bytes;
+  int32_t* status;         /* [TGX_STATUS_WORDS] or NULL */
+} tgx_csr_build_args;
+
+size_t tgx_csr_build_workspace_size(int64_t num_entries);
+int tgx_csr_build(const tgx_csr_build_args* args, void* stream);
 
 /* Fused most-recent-K gather (+ time encoding, + co-occurrence) (kernels b, c).
  * ring and/or csr may be NULL (no candidates from that store). */

@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(L, n), n
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
-    assert L.tgx_abi_version() == 6
+    assert L.tgx_abi_version() == 7
     nm = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
                         text=True).stdout
     exported = set(re.findall(r"\bT (tgx_\w+)", nm))
@@ -51,6 +51,10 @@ int main(void) {
   F(tgx_recent_args, co_mode) F(tgx_recent_args, co_a) F(tgx_recent_args, status)
   F(tgx_recent_args, num_query_groups) F(tgx_recent_args, query_groups)
   F(tgx_recent_args, timing_start) F(tgx_recent_args, timing_stop)
+  F(tgx_recent_args, append_src) F(tgx_recent_args, append_b) F(tgx_recent_args, append_workspace_bytes)
+  S(tgx_csr_build_args) F(tgx_csr_build_args, num_entries) F(tgx_csr_build_args, event)
+  F(tgx_csr_build_args, num_events) F(tgx_csr_build_args, feat_dtype) F(tgx_csr_build_args, out_offsets)
+  F(tgx_csr_build_args, out_eids) F(tgx_csr_build_args, workspace_bytes) F(tgx_csr_build_args, status)
   return 0;
 }
 """
@@ -63,7 +67,8 @@ def test_struct_layouts_match_ctypes(tmp_path):
     subprocess.run(["gcc", "-std=c99", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)], check=True)
     out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout
     mirror = {"tgx_ring": _lib.TgxRing, "tgx_csr": _lib.TgxCsr,
-              "tgx_query_group": _lib.TgxQueryGroup, "tgx_recent_args": _lib.TgxRecentArgs}
+              "tgx_query_group": _lib.TgxQueryGroup, "tgx_recent_args": _lib.TgxRecentArgs,
+              "tgx_csr_build_args": _lib.TgxCsrBuildArgs}
     for line in out.splitlines():
         key, val = line.split()
         if "." in key:
@@ -174,6 +179,30 @@ def test_size_queries():
     # tickets, 8-byte overflow pairs (or lists), groups, large groups
     assert ws >= 4 * n + 8 * n + 4 * (n // 2 + 1) + 4 * (n // 65 + 1)
     assert L.tgx_ring_append_workspace_size(0) > 0
+
+
+def test_csr_build_argument_checks():
+    L = _lib.lib()
+    a = _lib.TgxCsrBuildArgs(num_nodes=0, num_entries=0)
+    assert L.tgx_csr_build(ctypes.byref(a), None) == 3 and "num_nodes" in _err()
+    a = _lib.TgxCsrBuildArgs(num_nodes=10, num_entries=-1)
+    assert L.tgx_csr_build(ctypes.byref(a), None) == 3
+    a = _lib.TgxCsrBuildArgs(num_nodes=10, num_entries=5, out_offsets=8)
+    assert L.tgx_csr_build(ctypes.byref(a), None) == 1 and "must not be NULL" in _err()
+    a = _lib.TgxCsrBuildArgs(num_nodes=10, num_entries=5, out_offsets=8, from_=8, to=8, time=8,
+                             out_ids=8, out_times=8, feat_dim=4, feat_dtype=_lib.TGX_F32)
+    assert L.tgx_csr_build(ctypes.byref(a), None) == 1 and "out_feats" in _err()
+    a.out_feats = 8
+    a.feats = 8
+    assert L.tgx_csr_build(ctypes.byref(a), None) == 1 and "event" in _err()
+    a.event = 8
+    assert L.tgx_csr_build(ctypes.byref(a), None) == 1 and "workspace" in _err()
+    a.feat_dtype = 9
+    assert L.tgx_csr_build(ctypes.byref(a), None) == 2
+    assert L.tgx_csr_build(None, None) == 1
+    # workspace: keys, values and node keys double-buffered, plus the digit counts
+    assert L.tgx_csr_build_workspace_size(1 << 20) >= (1 << 20) * 32 + 256 * 512 * 4
+    assert L.tgx_csr_build_workspace_size(0) > 0
 
 
 def test_co_occurrence_argument_checks():

@@ -67,6 +67,14 @@ class TgxRecentArgs(ctypes.Structure):
                 ("append_workspace_bytes", ctypes.c_size_t)]
 
 
+class TgxCsrBuildArgs(ctypes.Structure):
+    _fields_ = [("num_nodes", c_i64), ("num_entries", c_i64), ("from_", c_vp), ("to", c_vp),
+                ("time", c_vp), ("event", c_vp), ("feats", c_vp), ("num_events", c_i64),
+                ("feat_dim", c_i32), ("feat_dtype", c_i32), ("out_offsets", c_vp),
+                ("out_ids", c_vp), ("out_times", c_vp), ("out_feats", c_vp), ("out_eids", c_vp),
+                ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t), ("status", c_vp)]
+
+
 # every symbol include/tgx.h declares, with its ctypes signature
 SIGNATURES = {
     "tgx_ring_append": (c_i32, [ctypes.POINTER(TgxRing), c_vp, c_vp, c_vp, c_vp, c_i64, c_i64,
@@ -82,6 +90,8 @@ SIGNATURES = {
     "tgx_recent": (c_i32, [ctypes.POINTER(TgxRing), ctypes.POINTER(TgxCsr),
                            ctypes.POINTER(TgxRecentArgs), c_vp]),
     "tgx_co_occurrence": (c_i32, [c_vp, c_vp, c_i64, c_i32, c_vp, c_vp, c_vp, c_vp]),
+    "tgx_csr_build": (c_i32, [ctypes.POINTER(TgxCsrBuildArgs), c_vp]),
+    "tgx_csr_build_workspace_size": (ctypes.c_size_t, [c_i64]),
     "tgx_last_error": (ctypes.c_char_p, []),
     "tgx_abi_version": (c_i32, []),
 }
@@ -111,7 +121,7 @@ def lib() -> ctypes.CDLL:
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
-        if handle.tgx_abi_version() != 6:
+        if handle.tgx_abi_version() != 7:
             raise RuntimeError("libtgx ABI version mismatch")
         _lib = handle
         return _lib

@@ -135,7 +135,7 @@ class TemporalGraph:
         self.track_edge_ids = bool(track_edge_ids)
         self._num_edges = 0
 
-        self._build: list = []       # pre-freeze (src, dst, time, feat, eid_base) host chunks
+        self._build: list = []       # pre-freeze (src, dst, time, feat|None, eid_base) device copies
         self._frozen = False
         self._offsets: Optional[Tensor] = None
         self._nbr_ids: Optional[Tensor] = None
@@ -310,10 +310,14 @@ class TemporalGraph:
                 if plan is not None:
                     self._discard_plan()
         if not self._frozen:
-            feat = (torch.zeros((b, self.edge_feat_dim), dtype=self.feat_dtype)
-                    if edge_feat is None else self._feat_in(edge_feat, b).cpu())
-            self._build.append((src.detach().to("cpu", torch.int64), dst.detach().to("cpu", torch.int64),
-                                time.detach().to("cpu", torch.float64), feat, self._num_edges))
+            # the values at call time, as device copies (the reference copies them
+            # into host lists, temporal_graph.py:110-122)
+            dev = self.device
+            feat = (None if edge_feat is None
+                    else self._feat_in(edge_feat, b).detach().clone(memory_format=torch.contiguous_format))
+            self._build.append((src.detach().to(dev, torch.int64).clone(),
+                                dst.detach().to(dev, torch.int64).clone(),
+                                time.detach().to(dev, torch.float64).clone(), feat, self._num_edges))
         else:
             self._ensure_overflow()
             if b > 0:
@@ -329,46 +333,49 @@ class TemporalGraph:
 
     # ------------------------------------------------------------------ CSR
     def freeze_csr(self) -> None:
-        """Sort the pre-freeze events into the device CSR (reference :133-181).
+        """Build the frozen CSR on the device from the pre-freeze events
+        (reference :133-181), with tgx_csr_build.
 
         Build order per advance() call is [src->dst ..., dst->src ...]; entries
         are sorted stably by time, then stably by node, so a node's entries are
         time-ascending with ties in build order.
         """
         N, d, dev = self.num_nodes, self.edge_feat_dim, self.device
-        if not self._build:
-            self._offsets = torch.zeros(N + 1, dtype=torch.int64, device=dev)
-            self._nbr_ids = torch.empty(0, dtype=torch.int32, device=dev)
-            self._nbr_times = torch.empty(0, dtype=torch.float64, device=dev)
-            self._nbr_feats = torch.empty((0, d), dtype=self.feat_dtype, device=dev)
-            self._nbr_eids = torch.empty(0, dtype=torch.int64, device=dev) if self.track_edge_ids else None
-        else:
-            frm, to, tt, ff, ee = [], [], [], [], []
-            for (s, t_, tm, f, eb) in self._build:
-                bb = s.shape[0]
-                ev = torch.arange(bb, dtype=torch.int64) + eb
-                frm += [s, t_]
-                to += [t_, s]
-                tt += [tm, tm]
-                ff += [f, f]
-                ee += [ev, ev]
-            frm_t = torch.cat(frm)
-            if frm_t.numel() and (int(frm_t.min()) < 0 or int(frm_t.max()) >= N):
+        batches = [x for x in self._build if x[0].shape[0] > 0]
+        n = 2 * sum(int(x[0].shape[0]) for x in batches)
+        self._offsets = torch.zeros(N + 1, dtype=torch.int64, device=dev)
+        self._nbr_ids = torch.empty(n, dtype=torch.int32, device=dev)
+        self._nbr_times = torch.empty(n, dtype=torch.float64, device=dev)
+        self._nbr_feats = torch.empty((n, d), dtype=self.feat_dtype, device=dev)
+        self._nbr_eids = torch.empty(n, dtype=torch.int64, device=dev) if self.track_edge_ids else None
+        if n > 0:
+            # directed entries in build order (gathered once more by the build)
+            frm = torch.cat([t for (s_, t_, _, _, _) in batches for t in (s_, t_)])
+            if int(frm.min()) < 0 or int(frm.max()) >= N:
                 raise IndexError("advance() got node ids outside [0, num_nodes)")
-            to_t = torch.cat(to).to(torch.int32)
-            tt_t = torch.cat(tt)
-            ff_t = torch.cat(ff)
-            ee_t = torch.cat(ee)
-            perm = torch.argsort(tt_t, stable=True)
-            perm = perm[torch.argsort(frm_t[perm], stable=True)]
-            counts = torch.bincount(frm_t, minlength=N)
-            offsets = torch.zeros(N + 1, dtype=torch.int64)
-            offsets[1:] = counts.cumsum(0)
-            self._offsets = offsets.to(dev)
-            self._nbr_ids = to_t[perm].to(dev)
-            self._nbr_times = tt_t[perm].to(dev)
-            self._nbr_feats = ff_t[perm].to(dev).contiguous()
-            self._nbr_eids = ee_t[perm].to(dev) if self.track_edge_ids else None
+            to = torch.cat([t for (s_, t_, _, _, _) in batches for t in (t_, s_)])
+            tt = torch.cat([tm for (_, _, tm, _, _) in batches for _ in (0, 1)])
+            ev = torch.cat([torch.arange(eb, eb + s_.shape[0], dtype=torch.int64, device=dev)
+                            for (s_, _, _, _, eb) in batches for _ in (0, 1)])
+            # event-major feature rows (row eb + i of the event), zeros for None
+            feats = None
+            if d > 0 and any(f is not None for (_, _, _, f, _) in batches):
+                feats = torch.cat([f if f is not None else
+                                   torch.zeros((s_.shape[0], d), dtype=self.feat_dtype, device=dev)
+                                   for (s_, _, _, f, _) in batches])
+            ws = torch.empty(int(_lib.lib().tgx_csr_build_workspace_size(n)), dtype=torch.uint8, device=dev)
+            a = _lib.TgxCsrBuildArgs(
+                num_nodes=N, num_entries=n, from_=frm.data_ptr(), to=to.data_ptr(),
+                time=tt.data_ptr(), event=ev.data_ptr(),
+                feats=feats.data_ptr() if feats is not None else None,
+                num_events=int(feats.shape[0]) if feats is not None else 0,
+                feat_dim=d, feat_dtype=_DTYPES[self.feat_dtype],
+                out_offsets=self._offsets.data_ptr(), out_ids=self._nbr_ids.data_ptr(),
+                out_times=self._nbr_times.data_ptr(),
+                out_feats=self._nbr_feats.data_ptr() if d > 0 else None,
+                out_eids=_lib.ptr(self._nbr_eids), workspace=ws.data_ptr(),
+                workspace_bytes=ws.numel(), status=self._status.data_ptr())
+            _lib.check(_lib.lib().tgx_csr_build(ctypes.byref(a), _stream_handle(dev)), "tgx_csr_build")
         self._frozen = True
         self._build = []
         self._csr_struct = None

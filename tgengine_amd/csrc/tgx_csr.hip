@@ -1,0 +1,426 @@
+// Frozen-CSR build (reference TemporalGraph.freeze_csr, temporal_graph.py:133-181).
+//
+// The n directed entries of the pre-freeze advance() calls, in build order j
+// (per call: [src->dst for every event, dst->src for every event]), are sorted
+// stably by time and then stably by node, so a node's entries end up
+// time-ascending with ties in build order (the reference's two stable
+// argsorts, :156-158).  The same permutation comes out of a stable LSD radix
+// sort: eight 8-bit passes over an order-preserving 64-bit image of the time,
+// then ceil(log2 N / 8) passes over the node id.
+//
+// A pass is three steps over tiles of kTile keys:
+//   hist    : per-tile digit counts, stored digit-major (count[d][tile]);
+//   scan    : exclusive prefix of the counts (tile scans, recursively over
+//             the tile sums), so count[d][tile] becomes the tile's first
+//             output position for digit d;
+//   scatter : the tile's keys in order, kThreads at a time; each wavefront
+//             ranks equal digits among its lanes with eight ballots, the
+//             workgroup adds the earlier wavefronts' and rounds' counts, and
+//             every key lands at its stable position.
+// Then offsets[u] = lower_bound(sorted nodes, u), and one gather writes the
+// ids, times, edge ids and feature rows (16-byte vectors where aligned).
+#include "tgx_internal.h"
+
+#include <algorithm>
+#include <type_traits>
+#include <vector>
+
+namespace tgx {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kItems = 8;                 // keys per thread per tile
+constexpr int kTile = kThreads * kItems;  // keys per tile (and scan tile)
+constexpr int kBins = 256;                // 8-bit digits
+static_assert(kBins == kThreads, "one digit per thread in the prefix step");
+
+// order-preserving image of a float64: -0.0 maps to +0.0 and every NaN to one
+// NaN above +inf, so ties are exactly the ties of a float comparison
+__device__ __forceinline__ uint64_t time_key(double t) {
+  uint64_t u;
+  if (t != t)
+    u = 0x7ff8000000000000ull;
+  else if (t == 0.0)
+    u = 0;
+  else
+    u = static_cast<uint64_t>(__double_as_longlong(t));
+  return (u >> 63) ? ~u : (u | 0x8000000000000000ull);
+}
+
+__global__ __launch_bounds__(kThreads) void csr_init(const double* __restrict__ time, int64_t n,
+                                                     uint64_t* __restrict__ tkey,
+                                                     uint32_t* __restrict__ idx) {
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (j >= n) return;
+  tkey[j] = time_key(time[j]);
+  idx[j] = static_cast<uint32_t>(j);
+}
+
+template <typename K>
+__device__ __forceinline__ int digit_of(K k, int shift) {
+  return static_cast<int>((k >> shift) & (kBins - 1));
+}
+
+template <typename K>
+__global__ __launch_bounds__(kThreads) void radix_hist(const K* __restrict__ keys, int64_t n,
+                                                       int shift, int64_t ntiles,
+                                                       uint32_t* __restrict__ count) {
+  __shared__ uint32_t h[kBins];
+  h[threadIdx.x] = 0;
+  __syncthreads();
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile;
+#pragma unroll
+  for (int r = 0; r < kItems; ++r) {
+    const int64_t j = base + r * kThreads + threadIdx.x;
+    if (j < n) atomicAdd(&h[digit_of(keys[j], shift)], 1u);
+  }
+  __syncthreads();
+  count[static_cast<int64_t>(threadIdx.x) * ntiles + blockIdx.x] = h[threadIdx.x];
+}
+
+// exclusive scan of data[tile * kTile, +kTile) in place; the tile total goes
+// to sums[tile]
+__global__ __launch_bounds__(kThreads) void scan_tiles(uint32_t* __restrict__ data, int64_t L,
+                                                       uint32_t* __restrict__ sums) {
+  __shared__ uint32_t wtot[kWaves];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = threadIdx.x / kWave;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile + static_cast<int64_t>(threadIdx.x) * kItems;
+  uint32_t v[kItems];
+  uint32_t s = 0;
+#pragma unroll
+  for (int r = 0; r < kItems; ++r) {
+    v[r] = base + r < L ? data[base + r] : 0u;
+    s += v[r];
+  }
+  uint32_t incl = s;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const uint32_t y = __shfl_up(incl, off, kWave);
+    if (lane >= off) incl += y;
+  }
+  if (lane == kWave - 1) wtot[wv] = incl;
+  __syncthreads();
+  uint32_t before = 0, total = 0;
+  for (int w = 0; w < kWaves; ++w) {
+    if (w < wv) before += wtot[w];
+    total += wtot[w];
+  }
+  uint32_t run = before + incl - s;
+#pragma unroll
+  for (int r = 0; r < kItems; ++r) {
+    if (base + r < L) data[base + r] = run;
+    run += v[r];
+  }
+  if (threadIdx.x == 0) sums[blockIdx.x] = total;
+}
+
+__global__ __launch_bounds__(kThreads) void scan_add(uint32_t* __restrict__ data, int64_t L,
+                                                     const uint32_t* __restrict__ sums) {
+  const uint32_t add = sums[blockIdx.x];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile;
+#pragma unroll
+  for (int r = 0; r < kItems; ++r) {
+    const int64_t j = base + r * kThreads + threadIdx.x;
+    if (j < L) data[j] += add;
+  }
+}
+
+template <typename K>
+__global__ __launch_bounds__(kThreads) void radix_scatter(const K* __restrict__ kin,
+                                                          const uint32_t* __restrict__ vin,
+                                                          K* __restrict__ kout,
+                                                          uint32_t* __restrict__ vout, int64_t n,
+                                                          int shift, int64_t ntiles,
+                                                          const uint32_t* __restrict__ count) {
+  __shared__ uint32_t dbase[kBins];          // next output position per digit
+  __shared__ uint32_t wcnt[kWaves][kBins];   // this round's count per wave and digit
+  __shared__ uint32_t wpos[kWaves][kBins];   // this round's first position per wave and digit
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = threadIdx.x / kWave;
+  const uint64_t lt = (uint64_t(1) << lane) - 1;
+  dbase[threadIdx.x] = count[static_cast<int64_t>(threadIdx.x) * ntiles + blockIdx.x];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile;
+  for (int r = 0; r < kItems; ++r) {
+    const int64_t j = base + r * kThreads + threadIdx.x;
+    const bool valid = j < n;
+    const K k = valid ? kin[j] : K(0);
+    const uint32_t v = valid ? vin[j] : 0u;
+    const int d = digit_of(k, shift);
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) wcnt[w][threadIdx.x] = 0;
+    __syncthreads();
+    // lanes with the same digit: AND of the eight bit ballots
+    uint64_t peers = __ballot(valid);
+#pragma unroll
+    for (int bit = 0; bit < 8; ++bit) {
+      const bool on = (d >> bit) & 1;
+      const uint64_t m = __ballot(on);
+      peers &= on ? m : ~m;
+    }
+    const uint32_t rank = static_cast<uint32_t>(__popcll(peers & lt));
+    if (valid && rank == 0) wcnt[wv][d] = static_cast<uint32_t>(__popcll(peers));
+    __syncthreads();
+    {  // digit threadIdx.x: positions of the waves in order, then advance the base
+      const int dd = threadIdx.x;
+      uint32_t p = dbase[dd];
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        wpos[w][dd] = p;
+        p += wcnt[w][dd];
+      }
+      dbase[dd] = p;
+    }
+    __syncthreads();
+    if (valid) {
+      const uint32_t at = wpos[wv][d] + rank;
+      kout[at] = k;
+      vout[at] = v;
+    }
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void csr_node_keys(const int64_t* __restrict__ from,
+                                                          const uint32_t* __restrict__ idx,
+                                                          int64_t n, int64_t N,
+                                                          uint32_t* __restrict__ nkey,
+                                                          int32_t* __restrict__ status) {
+  const int64_t p = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  bool bad = false;
+  if (p < n) {
+    const int64_t u = from[idx[p]];
+    bad = u < 0 || u >= N;
+    nkey[p] = bad ? 0xffffffffu : static_cast<uint32_t>(u);
+  }
+  const uint64_t bm = __ballot(bad);
+  if ((threadIdx.x & (kWave - 1)) == 0 && bm != 0 && status != nullptr)
+    atomicAdd(&status[TGX_ST_BAD_EVENT_NODE], __popcll(bm));
+}
+
+// offsets[u] = #sorted node keys < u, u in [0, N]
+__global__ __launch_bounds__(kThreads) void csr_offsets(const uint32_t* __restrict__ nkey, int64_t n,
+                                                        int64_t N, int64_t* __restrict__ offsets) {
+  const int64_t u = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (u > N) return;
+  int64_t lo = 0, hi = n;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (static_cast<int64_t>(nkey[mid]) < u)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  offsets[u] = lo;
+}
+
+// out[p] = entry perm[p]: id, time, edge id, feature row (tpe lanes per row)
+template <int VEC>
+__global__ __launch_bounds__(kThreads) void csr_gather(
+    const uint32_t* __restrict__ perm, int64_t n, const int64_t* __restrict__ to,
+    const double* __restrict__ time, const int64_t* __restrict__ event, int64_t num_events,
+    const uint8_t* __restrict__ feats, int64_t row_bytes, int tpe_log2,
+    int32_t* __restrict__ out_ids, double* __restrict__ out_times, int64_t* __restrict__ out_eids,
+    uint8_t* __restrict__ out_feats, int32_t* __restrict__ status) {
+  using V = typename std::conditional<VEC == 16, uint4, typename std::conditional<VEC == 4, uint32_t, uint16_t>::type>::type;
+  const int tpe = 1 << tpe_log2;
+  const int64_t p = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) >> tpe_log2;
+  const int l = threadIdx.x & (tpe - 1);
+  bool bad = false;
+  if (p < n) {
+    const int64_t j = perm[p];
+    const int64_t ev = event != nullptr ? event[j] : -1;
+    if (l == 0) {
+      out_ids[p] = static_cast<int32_t>(to[j]);
+      out_times[p] = time[j];
+      if (out_eids != nullptr) out_eids[p] = ev;
+    }
+    if (out_feats != nullptr && row_bytes > 0) {
+      const int nv = static_cast<int>(row_bytes / VEC);
+      V* drow = reinterpret_cast<V*>(out_feats + p * row_bytes);
+      const bool have = feats != nullptr && ev >= 0 && ev < num_events;
+      bad = feats != nullptr && !have;
+      const V* srow = have ? reinterpret_cast<const V*>(feats + ev * row_bytes) : nullptr;
+      for (int c = l; c < nv; c += tpe) drow[c] = have ? srow[c] : V{};
+    }
+  }
+  const uint64_t bm = __ballot(bad && l == 0);
+  if ((threadIdx.x & (kWave - 1)) == 0 && bm != 0 && status != nullptr)
+    atomicAdd(&status[TGX_ST_BAD_EVENT_NODE], __popcll(bm));
+}
+
+size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// scan levels: L counts, then the tile sums of each level until one tile is left
+std::vector<int64_t> scan_levels(int64_t L) {
+  std::vector<int64_t> lv;
+  int64_t m = L;
+  while (true) {
+    const int64_t t = cdiv(m, kTile);
+    lv.push_back(t);
+    if (t <= 1) break;
+    m = t;
+  }
+  return lv;
+}
+
+struct Layout {
+  int64_t ntiles = 0;
+  size_t tkey = 0, idx = 0, nkey = 0, count = 0, sums = 0, total = 0;
+  std::vector<int64_t> levels;
+};
+
+Layout layout(int64_t n) {
+  Layout w;
+  w.ntiles = std::max<int64_t>(cdiv(n, kTile), 1);
+  const size_t un = static_cast<size_t>(std::max<int64_t>(n, 1));
+  w.tkey = 0;
+  w.idx = w.tkey + 2 * align256(un * 8);
+  w.nkey = w.idx + 2 * align256(un * 4);
+  w.count = w.nkey + 2 * align256(un * 4);
+  const int64_t L = static_cast<int64_t>(kBins) * w.ntiles;
+  w.levels = scan_levels(L);
+  size_t nsums = 0;
+  for (int64_t t : w.levels) nsums += static_cast<size_t>(t);
+  w.sums = w.count + align256(static_cast<size_t>(L) * 4);
+  w.total = w.sums + align256(nsums * 4 + 4);
+  return w;
+}
+
+// exclusive scan of data[0, L) with the tile-sum levels at `sums`
+int scan_exclusive(uint32_t* data, int64_t L, uint32_t* sums, const std::vector<int64_t>& levels,
+                   size_t level, hipStream_t stream) {
+  const int64_t t = levels[level];
+  hipLaunchKernelGGL(scan_tiles, dim3(static_cast<unsigned>(t)), dim3(kThreads), 0, stream, data, L, sums);
+  int rc = check_launch("scan_tiles");
+  if (rc || t <= 1) return rc;
+  if ((rc = scan_exclusive(sums, t, sums + t, levels, level + 1, stream))) return rc;
+  hipLaunchKernelGGL(scan_add, dim3(static_cast<unsigned>(t)), dim3(kThreads), 0, stream, data, L,
+                     static_cast<const uint32_t*>(sums));
+  return check_launch("scan_add");
+}
+
+template <typename K>
+int radix_pass(const K* kin, const uint32_t* vin, K* kout, uint32_t* vout, int64_t n, int shift,
+               const Layout& w, uint8_t* ws, hipStream_t stream) {
+  uint32_t* count = reinterpret_cast<uint32_t*>(ws + w.count);
+  uint32_t* sums = reinterpret_cast<uint32_t*>(ws + w.sums);
+  const dim3 grid(static_cast<unsigned>(w.ntiles));
+  hipLaunchKernelGGL(radix_hist<K>, grid, dim3(kThreads), 0, stream, kin, n, shift, w.ntiles, count);
+  int rc = check_launch("radix_hist");
+  if (rc) return rc;
+  if ((rc = scan_exclusive(count, static_cast<int64_t>(kBins) * w.ntiles, sums, w.levels, 0, stream)))
+    return rc;
+  hipLaunchKernelGGL(radix_scatter<K>, grid, dim3(kThreads), 0, stream, kin, vin, kout, vout, n, shift,
+                     w.ntiles, static_cast<const uint32_t*>(count));
+  return check_launch("radix_scatter");
+}
+
+}  // namespace
+}  // namespace tgx
+
+using namespace tgx;
+
+extern "C" size_t tgx_csr_build_workspace_size(int64_t n) {
+  if (n < 0) return 0;
+  return layout(n).total;
+}
+
+extern "C" int tgx_csr_build(const tgx_csr_build_args* a, void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (a == nullptr) return fail(TGX_ERR_ARG, "tgx_csr_build: args is NULL");
+  const int64_t n = a->num_entries, N = a->num_nodes;
+  if (N <= 0 || N >= (int64_t(1) << 31))
+    return fail(TGX_ERR_LIMIT, "tgx_csr_build: num_nodes %lld outside [1, 2^31)", (long long)N);
+  if (n < 0 || n >= (int64_t(1) << 31))
+    return fail(TGX_ERR_LIMIT, "tgx_csr_build: %lld entries outside [0, 2^31)", (long long)n);
+  if (a->feat_dim < 0) return fail(TGX_ERR_ARG, "tgx_csr_build: negative feat_dim");
+  const int esz = feat_elem_bytes(a->feat_dtype);
+  if (esz == 0) return fail(TGX_ERR_DTYPE, "tgx_csr_build: unsupported feat dtype %d", a->feat_dtype);
+  if (a->out_offsets == nullptr) return fail(TGX_ERR_ARG, "tgx_csr_build: out_offsets is NULL");
+  const int64_t row_bytes = static_cast<int64_t>(a->feat_dim) * esz;
+  if (n > 0) {
+    if (a->from == nullptr || a->to == nullptr || a->time == nullptr || a->out_ids == nullptr ||
+        a->out_times == nullptr)
+      return fail(TGX_ERR_ARG, "tgx_csr_build: from/to/time/out_ids/out_times must not be NULL");
+    if (row_bytes > 0 && a->out_feats == nullptr)
+      return fail(TGX_ERR_ARG, "tgx_csr_build: out_feats is NULL with feat_dim > 0");
+    if ((a->feats != nullptr || a->out_eids != nullptr) && a->event == nullptr)
+      return fail(TGX_ERR_ARG, "tgx_csr_build: feats / out_eids need the event index array");
+    if (a->feats != nullptr && a->num_events < 0)
+      return fail(TGX_ERR_ARG, "tgx_csr_build: negative num_events");
+  }
+  const Layout w = layout(n);
+  if (a->workspace == nullptr || a->workspace_bytes < w.total)
+    return fail(TGX_ERR_ARG, "tgx_csr_build: workspace of %zu bytes needed, got %zu", w.total,
+                a->workspace_bytes);
+  uint8_t* ws = static_cast<uint8_t*>(a->workspace);
+  const unsigned g1 = static_cast<unsigned>(std::max<int64_t>(cdiv(n, kThreads), 1));
+  int rc;
+  if (n == 0) {
+    hipLaunchKernelGGL(csr_offsets, dim3(static_cast<unsigned>(cdiv(N + 1, kThreads))), dim3(kThreads),
+                       0, stream, static_cast<const uint32_t*>(nullptr), n, N, a->out_offsets);
+    return check_launch("csr_offsets");
+  }
+  const size_t un = static_cast<size_t>(n);
+  uint64_t* tk[2] = {reinterpret_cast<uint64_t*>(ws + w.tkey),
+                     reinterpret_cast<uint64_t*>(ws + w.tkey + align256(un * 8))};
+  uint32_t* ix[2] = {reinterpret_cast<uint32_t*>(ws + w.idx),
+                     reinterpret_cast<uint32_t*>(ws + w.idx + align256(un * 4))};
+  uint32_t* nk[2] = {reinterpret_cast<uint32_t*>(ws + w.nkey),
+                     reinterpret_cast<uint32_t*>(ws + w.nkey + align256(un * 4))};
+  hipLaunchKernelGGL(csr_init, dim3(g1), dim3(kThreads), 0, stream, a->time, n, tk[0], ix[0]);
+  if ((rc = check_launch("csr_init"))) return rc;
+  // stable by time: 8 passes, ping-pong ending in buffer 0
+  int cur = 0;
+  for (int shift = 0; shift < 64; shift += 8) {
+    if ((rc = radix_pass<uint64_t>(tk[cur], ix[cur], tk[1 - cur], ix[1 - cur], n, shift, w, ws, stream)))
+      return rc;
+    cur = 1 - cur;
+  }
+  // then stable by node over ceil(log2 N) bits (out-of-range ids sort last)
+  hipLaunchKernelGGL(csr_node_keys, dim3(g1), dim3(kThreads), 0, stream, a->from,
+                     static_cast<const uint32_t*>(ix[cur]), n, N, nk[0], a->status);
+  if ((rc = check_launch("csr_node_keys"))) return rc;
+  uint32_t* perm_in = ix[cur];
+  uint32_t* perm_out = ix[1 - cur];
+  int bits = 1;
+  while ((int64_t(1) << bits) < N + 1) ++bits;  // + 1: the out-of-range key 0xffffffff
+  int ncur = 0;
+  if (bits > 24) bits = 32;
+  for (int shift = 0; shift < bits; shift += 8) {
+    if ((rc = radix_pass<uint32_t>(nk[ncur], perm_in, nk[1 - ncur], perm_out, n, shift, w, ws, stream)))
+      return rc;
+    ncur = 1 - ncur;
+    std::swap(perm_in, perm_out);
+  }
+  hipLaunchKernelGGL(csr_offsets, dim3(static_cast<unsigned>(cdiv(N + 1, kThreads))), dim3(kThreads), 0,
+                     stream, static_cast<const uint32_t*>(nk[ncur]), n, N, a->out_offsets);
+  if ((rc = check_launch("csr_offsets"))) return rc;
+  int vec = 2;
+  const bool fe = row_bytes > 0;
+  auto al = [](const void* p, unsigned m) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & m) == 0; };
+  if (row_bytes % 16 == 0 && (!fe || (al(a->feats, 15) && al(a->out_feats, 15))))
+    vec = 16;
+  else if (row_bytes % 4 == 0 && (!fe || (al(a->feats, 3) && al(a->out_feats, 3))))
+    vec = 4;
+  const int64_t nchunks = fe ? row_bytes / vec : 1;
+  int tpe_log2 = 0;
+  while ((int64_t(1) << tpe_log2) < nchunks && tpe_log2 < 6) ++tpe_log2;
+  const dim3 gg(static_cast<unsigned>(cdiv(n << tpe_log2, kThreads)));
+  auto gather = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, gg, dim3(kThreads), 0, stream, static_cast<const uint32_t*>(perm_in), n,
+                       a->to, a->time, a->event, a->num_events,
+                       static_cast<const uint8_t*>(a->feats), fe ? row_bytes : 0, tpe_log2, a->out_ids,
+                       a->out_times, a->out_eids, static_cast<uint8_t*>(fe ? a->out_feats : nullptr),
+                       a->status);
+  };
+  if (vec == 16)
+    gather(csr_gather<16>);
+  else if (vec == 4)
+    gather(csr_gather<4>);
+  else
+    gather(csr_gather<2>);
+  return check_launch("csr_gather");
+}
