@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define TGX_ABI_VERSION 7
+#define TGX_ABI_VERSION 8
 
 /* status codes */
 #define TGX_OK 0
@@ -107,12 +107,16 @@ typedef struct tgx_csr {
  * at time times[l / times_per] (times_per = negatives per event for a (b, n)
  * row-major negative block, else 1). */
 typedef struct tgx_query_group {
-  const int64_t* nodes;
+  const void* nodes;       /* [count] node ids: int64, or int32 with TGX_QG_NODES_I32 */
   const double* times;
   int64_t count;
   int32_t times_per;
-  int32_t reserved;
+  int32_t flags;           /* TGX_QG_* bits */
+  const uint8_t* valid;    /* [count] or NULL; a 0 makes that query padding only
+                              (no candidates, no status count): the 2-hop queries
+                              under invalid hop-1 slots */
 } tgx_query_group;
+#define TGX_QG_NODES_I32 1
 
 #define TGX_MAX_QUERY_GROUPS 4
 

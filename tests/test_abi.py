@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(L, n), n
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
-    assert L.tgx_abi_version() == 7
+    assert L.tgx_abi_version() == 8
     nm = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
                         text=True).stdout
     exported = set(re.findall(r"\bT (tgx_\w+)", nm))
@@ -45,6 +45,7 @@ int main(void) {
   F(tgx_ring, scratch)
   S(tgx_csr) F(tgx_csr, offsets) F(tgx_csr, eids)
   S(tgx_query_group) F(tgx_query_group, count) F(tgx_query_group, times_per)
+  F(tgx_query_group, flags) F(tgx_query_group, valid)
   S(tgx_recent_args) F(tgx_recent_args, k) F(tgx_recent_args, plan) F(tgx_recent_args, group)
   F(tgx_recent_args, num_groups) F(tgx_recent_args, out_eids) F(tgx_recent_args, d_t)
   F(tgx_recent_args, te_w) F(tgx_recent_args, dt_mode) F(tgx_recent_args, out_te)

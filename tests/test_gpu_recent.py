@@ -325,21 +325,59 @@ def test_pipeline_negatives_2d_and_neg_src():
     assert np.max(np.abs(te - exp)) <= TE_ATOL
 
 
-def test_recent_2hop_matches_oracle_composition():
-    rng, g, csr, ring, tmax = _build(17, 15, 8, 3, 5, True, True)
-    nodes = rng.integers(0, 15, 30)
-    qt = np.full(30, tmax + 1.0)
+@pytest.mark.parametrize("with_pre,with_ring,bf16", [(True, True, False), (False, True, True),
+                                                   (True, False, False)])
+def test_recent_2hop_matches_oracle_composition(with_pre, with_ring, bf16):
+    """hop 2 = recent() of every hop-1 slot's (id, time), padding under invalid hop-1
+    slots (reference temporal_graph.py:453-472): ids, times, rows and masks of both
+    hops bit-exact, padding query ids (< 0) included, no status counts."""
+    N, d = 15, 3
+    rng, g, csr, ring, tmax = _build(17, N, 8, d, 5, with_pre, with_ring, bf16)
+    fdt = np.uint16 if bf16 else np.float32
+    Q = 40
+    nodes = rng.integers(-1, N, Q)
+    qt = rng.uniform(tmax - 40.0, tmax + 1.0, Q)
     r = g.recent_2hop(cu(nodes), cu(qt), 5, 4)
-    h1 = O.recent(nodes, qt, 5, csr, ring, 3)
-    h2 = O.recent(h1.ids.reshape(-1).astype(np.int64), h1.times.reshape(-1), 4, csr, ring, 3)
-    m2 = h2.mask.reshape(30, 5, 4) & h1.mask[:, :, None]
+    h1 = O.recent(nodes, qt, 5, csr, ring, d, fdt)
+    h2 = O.recent(h1.ids.reshape(-1).astype(np.int64), h1.times.reshape(-1), 4, csr, ring, d, fdt)
+    m2 = h2.mask.reshape(Q, 5, 4) & h1.mask[:, :, None]
     assert np.array_equal(r.neighbor_ids.cpu().numpy(), h1.ids)
+    assert np.array_equal(r.mask.cpu().numpy(), h1.mask)
     assert np.array_equal(r.hop2_mask.cpu().numpy(), m2)
-    assert np.array_equal(r.hop2_ids.cpu().numpy(), np.where(m2, h2.ids.reshape(30, 5, 4), -1))
+    assert np.array_equal(r.hop2_ids.cpu().numpy(), np.where(m2, h2.ids.reshape(Q, 5, 4), -1))
+    assert np.array_equal(r.hop2_times.cpu().numpy().view(np.int64),
+                          np.where(m2, h2.times.reshape(Q, 5, 4), 0.0).view(np.int64))
+    f2 = np.where(m2[..., None], h2.feats.reshape(Q, 5, 4, d), np.zeros((), fdt))
+    assert np.array_equal(_feats_np(r.hop2_feats).view(np.uint8), f2.view(np.uint8))
+    assert g.status() == {"bad_event_nodes": 0, "key_collisions": 0, "bad_query_nodes": 0}
     pipe = DataPipeline(GatherSpec(neighbors=NeighborSpec(k=5, k2=4)), g)
-    pb = pipe.prepare(RawBatch(src=cu(nodes[:10]), dst=cu(nodes[10:20]), time=cu(qt[:10]),
-                               neg=cu(nodes[20:])))
+    nn = np.clip(nodes, 0, None)
+    pb = pipe.prepare(RawBatch(src=cu(nn[:10]), dst=cu(nn[10:20]), time=cu(qt[:10]),
+                               neg=cu(nn[20:30])))
     assert pb.src_neighbors.hop2_ids.shape == (10, 5, 4)
+
+
+def test_int32_query_nodes_and_validity_mask():
+    """A query group of int32 ids gives what int64 ids give; a False in its validity
+    array makes that query padding only, with no bad-query count even for an
+    out-of-range id."""
+    rng, g, csr, ring, tmax = _build(18, 20, 8, 4, 6, True, True)
+    Q = 64
+    nodes = rng.integers(0, 20, Q)
+    qt = rng.uniform(tmax - 30.0, tmax + 1.0, Q)
+    valid = rng.random(Q) < 0.6
+    n32 = nodes.astype(np.int32)
+    n32[~valid & (np.arange(Q) % 2 == 0)] = 1000  # out of range, but masked
+    ref = g._query(cu(nodes), cu(qt), 6)
+    got = g._query(None, None, 6, groups=[(cu(n32), cu(qt), 1, cu(valid))])
+    v = valid[:, None]
+    for key, pad in (("ids", -1), ("times", 0.0), ("mask", False)):
+        a = got[key][0].cpu().numpy()
+        b = ref[key][0].cpu().numpy()
+        assert np.array_equal(a, np.where(v, b, pad)), key
+    fa, fb = got["feats"][0].cpu().numpy(), ref["feats"][0].cpu().numpy()
+    assert np.array_equal(fa, np.where(v[..., None], fb, 0.0))
+    assert g.status()["bad_query_nodes"] == 0
 
 
 def test_edge_ids_need_a_tracking_graph():

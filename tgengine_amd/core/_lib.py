@@ -15,6 +15,7 @@ LIB_PATH = Path(__file__).resolve().parent.parent / "_lib" / "libtgx.so"
 TGX_OK = 0
 TGX_F32 = 0
 TGX_BF16 = 1
+TGX_QG_NODES_I32 = 1
 TGX_DT_DYGFORMER = 0
 TGX_DT_TGN = 1
 TGX_CO_NONE = 0
@@ -49,7 +50,7 @@ TGX_MAX_QUERY_GROUPS = 4
 
 class TgxQueryGroup(ctypes.Structure):
     _fields_ = [("nodes", c_vp), ("times", c_vp), ("count", c_i64), ("times_per", c_i32),
-                ("reserved", c_i32)]
+                ("flags", c_i32), ("valid", c_vp)]
 
 
 class TgxRecentArgs(ctypes.Structure):
@@ -121,7 +122,7 @@ def lib() -> ctypes.CDLL:
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
-        if handle.tgx_abi_version() != 7:
+        if handle.tgx_abi_version() != 8:
             raise RuntimeError("libtgx ABI version mismatch")
         _lib = handle
         return _lib

@@ -390,7 +390,8 @@ class TemporalGraph:
         """One tgx_recent launch.
 
         Queries come either as ``nodes``/``times`` or as ``groups``: a list of
-        (nodes, times, times_per) read in place and concatenated in order.  Returns
+        (nodes, times, times_per[, valid]) read in place and concatenated in order
+        (int64 or int32 nodes; a False in ``valid`` makes that query padding only).  Returns
         lists of per-group views under "ids", "times", "feats", "mask" (bool), and
         "eids" / "te" when asked for, plus "co_a", "co_c", "co_pair" with co-occurrence.
         ``append``: (src, dst, time) of the batch the caller advances next; when it
@@ -444,6 +445,7 @@ class TemporalGraph:
             ctypes.addressof(ring) if ring is not None else 0,
             ctypes.addressof(csr) if csr is not None else 0,
             [g[0] for g in groups], [g[1] for g in groups], [int(g[2]) for g in groups],
+            [g[3] if len(g) > 3 else None for g in groups] if any(len(g) > 3 for g in groups) else [],
             k, self.edge_feat_dim, self.feat_dtype, plan, group,
             -1 if num_groups is None else int(num_groups), int(d_t), te_w, te_b, int(dt_mode),
             int(co_mode), bool(want_eids), self._status, _stream_handle(self.device), ev0, ev1,
@@ -457,18 +459,18 @@ class TemporalGraph:
                             edge_ids=o["eids"][0] if "eids" in o else None)
 
     def recent_2hop(self, nodes: Tensor, times: Tensor, k1: int, k2: int) -> NeighborData:
-        """1-hop and 2-hop neighbours (reference :397-473): the 2-hop query of slot
-        (b, i) is (hop1 id, hop1 time); positions under an invalid hop-1 slot are padding."""
+        """1-hop and 2-hop neighbours (reference :397-473), in two launches like the
+        reference's CUDA path (hop 1, then one query per hop-1 slot): the 2-hop query
+        of slot (b, i) is (hop1 id, hop1 time), read in place from the hop-1 outputs;
+        slots under an invalid hop-1 neighbour come out as padding."""
         hop1 = self.recent(nodes, times, k1)
         N, K1 = hop1.neighbor_ids.shape
-        hop2 = self.recent(hop1.neighbor_ids.reshape(-1).to(torch.int64),
-                           hop1.timestamps.reshape(-1), k2)
-        h2_mask = hop2.mask.reshape(N, K1, k2) & hop1.mask.unsqueeze(-1)
-        hop1.hop2_mask = h2_mask
-        hop1.hop2_ids = hop2.neighbor_ids.reshape(N, K1, k2).masked_fill(~h2_mask, self.PADDING_ID)
-        hop1.hop2_times = hop2.timestamps.reshape(N, K1, k2).masked_fill(~h2_mask, 0.0)
-        hop1.hop2_feats = hop2.edge_feats.reshape(N, K1, k2, self.edge_feat_dim).masked_fill(
-            ~h2_mask.unsqueeze(-1), 0.0)
+        o = self._query(None, None, k2, groups=[(hop1.neighbor_ids.reshape(-1), hop1.timestamps.reshape(-1),
+                                                 1, hop1.mask.reshape(-1))])
+        hop1.hop2_ids = o["ids"][0].reshape(N, K1, k2)
+        hop1.hop2_times = o["times"][0].reshape(N, K1, k2)
+        hop1.hop2_feats = o["feats"][0].reshape(N, K1, k2, self.edge_feat_dim)
+        hop1.hop2_mask = o["mask"][0].reshape(N, K1, k2)
         return hop1
 
     def co_neighbors(self, src: Tensor, dst: Tensor, times: Tensor, k: int = 32) -> Tensor:

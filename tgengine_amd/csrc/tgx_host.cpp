@@ -50,7 +50,8 @@ bool plannable(const at::Tensor& s, const at::Tensor& d, const at::Tensor& t, co
 // unsplit); planned holds one tensor when the batch was planned, else nothing.
 std::vector<std::vector<at::Tensor>> recent(
     int64_t ring_addr, int64_t csr_addr, const std::vector<at::Tensor>& gnodes,
-    const std::vector<at::Tensor>& gtimes, const std::vector<int64_t>& gper, int64_t k,
+    const std::vector<at::Tensor>& gtimes, const std::vector<int64_t>& gper,
+    const std::vector<c10::optional<at::Tensor>>& gvalid, int64_t k,
     int64_t feat_dim, at::ScalarType feat_dtype, const c10::optional<at::Tensor>& plan,
     int64_t group, int64_t num_groups, int64_t d_t, const c10::optional<at::Tensor>& te_w,
     const c10::optional<at::Tensor>& te_b, int64_t dt_mode, int64_t co_mode, bool want_eids,
@@ -58,17 +59,25 @@ std::vector<std::vector<at::Tensor>> recent(
     const c10::optional<at::Tensor>& append_src, const c10::optional<at::Tensor>& append_dst,
     const c10::optional<at::Tensor>& append_time, const c10::optional<at::Tensor>& append_ws) {
   const size_t ng = gnodes.size();
-  if (ng == 0 || ng > TGX_MAX_QUERY_GROUPS || gtimes.size() != ng || gper.size() != ng)
+  if (ng == 0 || ng > TGX_MAX_QUERY_GROUPS || gtimes.size() != ng || gper.size() != ng ||
+      (!gvalid.empty() && gvalid.size() != ng))
     throw std::invalid_argument("recent: 1..4 query groups with matching times");
   const at::Device dev = status.device();
-  std::vector<at::Tensor> n(ng), t(ng);
+  std::vector<at::Tensor> n(ng), t(ng), v(ng);
   std::vector<int64_t> sizes(ng);
   int64_t Q = 0;
   for (size_t g = 0; g < ng; ++g) {
-    n[g] = as_dev(flat(gnodes[g]), at::kLong, dev);
+    // int32 node ids are read as they are (the 2-hop queries are hop-1 ids)
+    const at::Tensor fn = flat(gnodes[g]);
+    n[g] = as_dev(fn, fn.scalar_type() == at::kInt ? at::kInt : at::kLong, dev);
     t[g] = as_dev(flat(gtimes[g]), at::kDouble, dev);
     if (n[g].numel() != t[g].numel() * gper[g])
       throw std::invalid_argument("recent: query group node/time sizes do not match");
+    if (!gvalid.empty() && gvalid[g].has_value()) {
+      v[g] = as_dev(flat(*gvalid[g]), at::kBool, dev);
+      if (v[g].numel() != n[g].numel())
+        throw std::invalid_argument("recent: query group validity size does not match its nodes");
+    }
     sizes[g] = n[g].numel();
     Q += sizes[g];
   }
@@ -110,10 +119,12 @@ std::vector<std::vector<at::Tensor>> recent(
   a.status = status.data_ptr<int32_t>();
   a.num_query_groups = static_cast<int32_t>(ng);
   for (size_t g = 0; g < ng; ++g) {
-    a.query_groups[g].nodes = n[g].data_ptr<int64_t>();
+    a.query_groups[g].nodes = n[g].data_ptr();
+    a.query_groups[g].flags = n[g].scalar_type() == at::kInt ? TGX_QG_NODES_I32 : 0;
     a.query_groups[g].times = t[g].data_ptr<double>();
     a.query_groups[g].count = sizes[g];
     a.query_groups[g].times_per = static_cast<int32_t>(gper[g]);
+    a.query_groups[g].valid = v[g].defined() ? reinterpret_cast<const uint8_t*>(v[g].data_ptr<bool>()) : nullptr;
   }
   a.timing_start = reinterpret_cast<void*>(ev0);
   a.timing_stop = reinterpret_cast<void*>(ev1);

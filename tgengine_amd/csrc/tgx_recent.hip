@@ -75,7 +75,9 @@ struct Params {
   const int64_t* nodes;
   const double* qtimes;
   int ngroups;
-  const int64_t* gn[TGX_MAX_QUERY_GROUPS];
+  const void* gn[TGX_MAX_QUERY_GROUPS];
+  const uint8_t* gv[TGX_MAX_QUERY_GROUPS];  // per-query validity or null
+  int gi32[TGX_MAX_QUERY_GROUPS];           // int32 node ids
   const double* gt[TGX_MAX_QUERY_GROUPS];
   int64_t goff[TGX_MAX_QUERY_GROUPS + 1];
   int gdiv[TGX_MAX_QUERY_GROUPS];
@@ -214,36 +216,46 @@ __device__ __forceinline__ int64_t query_of(const Params& P, int64_t g, int j) {
   return (q >= 0 && q < P.Q) ? q : -1;
 }
 
-// node and time of query q; the query group is chosen with compares against the
-// group offsets (constant indices only, so the arguments stay in registers)
-__device__ __forceinline__ void query_load(const Params& P, int64_t q, int64_t& node, double& qt) {
+// node and time of query q, and whether it is a query at all (a group's
+// validity array can turn it into padding output only); the query group is
+// chosen with compares against the group offsets (constant indices only, so the
+// arguments stay in registers)
+__device__ __forceinline__ void query_load(const Params& P, int64_t q, int64_t& node, double& qt,
+                                           bool& valid) {
+  valid = true;
   if (P.ngroups == 0) {
     node = P.nodes[q];
     qt = P.qtimes[q];
     return;
   }
-  const int64_t* np = P.gn[0];
+  const void* np = P.gn[0];
   const double* tp = P.gt[0];
+  const uint8_t* vp = P.gv[0];
   int64_t off = 0;
   int div = P.gdiv[0];
+  int i32 = P.gi32[0];
 #pragma unroll
   for (int g = 1; g < TGX_MAX_QUERY_GROUPS; ++g) {
     if (g < P.ngroups && q >= P.goff[g]) {
       np = P.gn[g];
       tp = P.gt[g];
+      vp = P.gv[g];
       off = P.goff[g];
       div = P.gdiv[g];
+      i32 = P.gi32[g];
     }
   }
   const int64_t l = q - off;
-  node = np[l];
+  node = i32 ? static_cast<int64_t>(static_cast<const int32_t*>(np)[l]) : static_cast<const int64_t*>(np)[l];
   qt = tp[div == 1 ? l : static_cast<int64_t>(static_cast<uint32_t>(l) / static_cast<uint32_t>(div))];
+  if (vp != nullptr) valid = vp[l] != 0;
 }
 
 __device__ __forceinline__ int64_t query_node(const Params& P, int64_t q) {
   int64_t node;
   double qt;
-  query_load(P, q, node, qt);
+  bool valid;
+  query_load(P, q, node, qt, valid);
   return node;
 }
 
@@ -438,11 +450,12 @@ __global__ __launch_bounds__(kMaxWaves * kWave) __attribute__((amdgpu_waves_per_
   }
   int64_t node = -1;
   double qt = 0.0;
-  if (q >= 0) query_load(P, q, node, qt);
-  const bool bad = q >= 0 && node >= P.N;
+  bool qvalid = true;
+  if (q >= 0) query_load(P, q, node, qt, qvalid);
+  const bool bad = q >= 0 && qvalid && node >= P.N;
   if (bad && sl == 0 && part == 0 && P.status != nullptr) atomicAdd(&P.status[TGX_ST_BAD_QUERY_NODE], 1);
   const int64_t ur = node < 0 ? 0 : node;
-  const bool live = q >= 0 && !bad;
+  const bool live = q >= 0 && qvalid && !bad;
 
   // ---- ring slot sl of query h, its feature row (NREG > 0) and write position ----
   int32_t rid = -1;
@@ -876,9 +889,12 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
     int64_t off = 0;
     for (int g = 0; g < a->num_query_groups; ++g) {
       const tgx_query_group& qg = a->query_groups[g];
-      if (qg.count < 0 || qg.times_per < 1 || (qg.count > 0 && (qg.nodes == nullptr || qg.times == nullptr)))
+      if (qg.count < 0 || qg.times_per < 1 || (qg.count > 0 && (qg.nodes == nullptr || qg.times == nullptr)) ||
+          (qg.flags & ~TGX_QG_NODES_I32) != 0)
         return fail(TGX_ERR_ARG, "tgx_recent: bad query group %d", g);
       P.gn[g] = qg.nodes;
+      P.gv[g] = qg.valid;
+      P.gi32[g] = (qg.flags & TGX_QG_NODES_I32) != 0;
       P.gt[g] = qg.times;
       P.gdiv[g] = qg.times_per;
       P.goff[g] = off;
