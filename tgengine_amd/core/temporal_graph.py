@@ -82,6 +82,17 @@ except AttributeError:  # pragma: no cover - older torch
     _raw_stream = None
 
 
+_WS_SIZES: dict = {}
+
+
+def _ws_size(b: int) -> int:
+    """tgx_ring_append_workspace_size(b), remembered per batch length."""
+    n = _WS_SIZES.get(b)
+    if n is None:
+        n = _WS_SIZES[b] = int(_lib.lib().tgx_ring_append_workspace_size(b))
+    return n
+
+
 def _stream_handle(device: torch.device) -> int:
     """hipStream_t of the caller's current stream on ``device``."""
     if _raw_stream is not None:
@@ -235,7 +246,7 @@ class TemporalGraph:
                 and all(t.device == self.device and t.is_contiguous() for t in (src, dst, time)))
 
     def _plan_workspace(self, b: int) -> Tensor:
-        need = int(_lib.lib().tgx_ring_append_workspace_size(b))
+        need = _ws_size(b)
         if self._plan_ws is None or self._plan_ws.numel() < need:
             self._plan_ws = torch.empty(max(need, 1 << 16), dtype=torch.uint8, device=self.device)
         return self._plan_ws
@@ -441,12 +452,19 @@ class TemporalGraph:
     def _launch_recent(self, ring, csr, groups, k, plan, group, num_groups, d_t, te_w, te_b,
                        dt_mode, co_mode, want_eids, ev0, ev1, append, ws):
         a_src, a_dst, a_time = append if append is not None else (None, None, None)
+        gn, gt, gp, gv = [], [], [], []
+        for grp in groups:
+            gn.append(grp[0])
+            gt.append(grp[1])
+            gp.append(grp[2])
+            if len(grp) > 3:
+                gv.append(grp[3])
+        if gv and len(gv) != len(groups):
+            gv = [grp[3] if len(grp) > 3 else None for grp in groups]
         return _host().recent(
             ctypes.addressof(ring) if ring is not None else 0,
             ctypes.addressof(csr) if csr is not None else 0,
-            [g[0] for g in groups], [g[1] for g in groups], [int(g[2]) for g in groups],
-            [g[3] if len(g) > 3 else None for g in groups] if any(len(g) > 3 for g in groups) else [],
-            k, self.edge_feat_dim, self.feat_dtype, plan, group,
+            gn, gt, gp, gv, k, self.edge_feat_dim, self.feat_dtype, plan, group,
             -1 if num_groups is None else int(num_groups), int(d_t), te_w, te_b, int(dt_mode),
             int(co_mode), bool(want_eids), self._status, _stream_handle(self.device), ev0, ev1,
             a_src, a_dst, a_time, ws)

@@ -105,9 +105,9 @@ class DataPipeline:
             names.append("dst"); qgroups.append((raw_batch.dst, raw_batch.time, 1))
             sizes.append(b); per_event.append(1)
         if "neg" in fn and raw_batch.neg is not None:
-            neg = raw_batch.neg
+            neg = raw_batch.neg  # a (b, n) block is read row-major (the host glue flattens it)
             per = neg.shape[1] if neg.ndim > 1 else 1
-            names.append("neg"); qgroups.append((neg.reshape(-1), raw_batch.time, per))
+            names.append("neg"); qgroups.append((neg, raw_batch.time, per))
             sizes.append(neg.numel()); per_event.append(per)
         if "neg" in fn and raw_batch.neg_src is not None:
             names.append("neg_src"); qgroups.append((raw_batch.neg_src, raw_batch.time, 1))
