@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define TGX_ABI_VERSION 8
+#define TGX_ABI_VERSION 9
 
 /* status codes */
 #define TGX_OK 0
@@ -245,6 +245,30 @@ typedef struct tgx_csr_build_args {
 
 size_t tgx_csr_build_workspace_size(int64_t num_entries);
 int tgx_csr_build(const tgx_csr_build_args* args, void* stream);
+
+/* Historical negative pool (HistoricalNegPool, pipeline/negatives.py:14-126).
+ * pool int32 [num_nodes, pool_size] (-1 = empty), count int64 [num_nodes]
+ * (edges seen per source), both zero-/minus-one-filled by the caller once.
+ * update: edge j of the batch, the r-th from its source u in batch order, is
+ * u's e-th edge (e = count[u] + r + 1): e <= pool_size fills slot e-1, else it
+ * replaces slot rand % pool_size with probability pool_size/e (float32); the
+ * later edge of the batch wins a slot two edges take; count[u] grows by u's
+ * edges.  sample: out[q] = pool[u][int(U * min(count[u], pool_size))] (slot
+ * clamped to pool_size-1), or a random node in [0, num_nodes) for a node with
+ * no history.  Random numbers: rand64(seed, call, i, stream) =
+ * mix(mix(mix(seed ^ 0x9e3779b97f4a7c15) ^ call) ^ (4i + stream)), mix the
+ * splitmix64 finalizer, U = (rand64 >> 40) * 2^-24; streams 0/1 (update accept /
+ * slot), 2/3 (sample slot / fallback node).  Out-of-range ids are skipped
+ * (update) or sampled as nodes without history (sample) and counted in status.
+ * workspace: tgx_negpool_update_workspace_size(n) bytes. */
+size_t tgx_negpool_update_workspace_size(int64_t n);
+int tgx_negpool_update(int32_t* pool, int64_t* count, int64_t num_nodes, int32_t pool_size,
+                       const int64_t* src, const int64_t* dst, int64_t n, uint64_t seed,
+                       uint64_t call, void* workspace, size_t workspace_bytes, int32_t* status,
+                       void* stream);
+int tgx_negpool_sample(const int32_t* pool, const int64_t* count, int64_t num_nodes,
+                       int32_t pool_size, const int64_t* src, int64_t n, uint64_t seed,
+                       uint64_t call, int64_t* out, int32_t* status, void* stream);
 
 /* Fused most-recent-K gather (+ time encoding, + co-occurrence) (kernels b, c).
  * ring and/or csr may be NULL (no candidates from that store). */

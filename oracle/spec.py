@@ -411,3 +411,106 @@ def co_dygformer(a_full, c_full):
     a_freq = np.stack([a_self.sum(1), cross.sum(2)], axis=2)
     c_freq = np.stack([cross.sum(1), c_self.sum(1)], axis=2)
     return a_freq.astype(np.int32), c_freq.astype(np.int32)
+
+
+# ---------------------------------------------------------------- negative pool
+# HistoricalNegPool (reference pipeline/negatives.py:14-126) with the library's
+# counter-based random numbers in place of torch.rand / torch.randint.
+
+_M64 = (1 << 64) - 1
+_GOLDEN = 0x9E3779B97F4A7C15
+
+
+def mix64(z: int) -> int:
+    """The splitmix64 finalizer (Steele, Lea, Flood 2014; Vigna's splitmix64.c)."""
+    z &= _M64
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & _M64
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & _M64
+    return z ^ (z >> 31)
+
+
+def rand64(seed: int, call: int, i: int, stream: int) -> int:
+    return mix64(mix64(mix64((seed ^ _GOLDEN) & _M64) ^ (call & _M64)) ^ ((4 * i + stream) & _M64))
+
+
+def uniform01(h: int) -> np.float32:
+    return np.float32(h >> 40) * np.float32(2.0 ** -24)
+
+
+def negpool_update(pool: np.ndarray, count: np.ndarray, src, dst, seed: int, call: int) -> None:
+    """One update, edge by edge in batch order (negatives.py:45-103): edge j, the
+    r-th of its source u in the batch, is u's e-th edge, e = count[u] + r + 1
+    (count from before the batch); e <= P fills slot e-1, else it replaces slot
+    rand % P with probability P/e in float32.  Sequential writes: a later edge
+    overwrites an earlier one's slot.  count[u] grows by u's edges."""
+    N, P = pool.shape
+    seen: dict = {}
+    for j in range(len(src)):
+        u = int(src[j])
+        if u < 0 or u >= N:
+            continue
+        r = seen.get(u, 0)
+        seen[u] = r + 1
+        e = int(count[u]) + r + 1
+        if e <= P:
+            slot = e - 1
+        elif uniform01(rand64(seed, call, j, 0)) < np.float32(P) / np.float32(e):
+            slot = rand64(seed, call, j, 1) % P
+        else:
+            continue
+        pool[u, slot] = np.int32(dst[j])
+    for u, c in seen.items():
+        count[u] += c
+
+
+def negpool_update_sorted(pool: np.ndarray, count: np.ndarray, src, dst, seed: int, call: int) -> None:
+    """The same update as the device computes it: a stable sort by source gives
+    r, a stable sort of accepted edges by (u, slot) keeps the latest per slot."""
+    N, P = pool.shape
+    src = np.asarray(src, np.int64)
+    dst = np.asarray(dst, np.int64)
+    n = len(src)
+    ok = (src >= 0) & (src < N)
+    idx = np.nonzero(ok)[0]
+    order = idx[np.argsort(src[idx], kind="stable")]
+    su = src[order]
+    start = np.searchsorted(su, su, side="left")
+    r = np.arange(len(order)) - start
+    e = count[su] + r + 1
+    keys, vals = [], []
+    for p in range(len(order)):
+        j = int(order[p])
+        if e[p] <= P:
+            slot = int(e[p]) - 1
+        elif uniform01(rand64(seed, call, j, 0)) < np.float32(P) / np.float32(e[p]):
+            slot = rand64(seed, call, j, 1) % P
+        else:
+            continue
+        keys.append(int(su[p]) * P + slot)
+        vals.append(j)
+    keys = np.asarray(keys, np.int64)
+    vals = np.asarray(vals, np.int64)
+    o = np.argsort(keys, kind="stable")
+    keys, vals = keys[o], vals[o]
+    last = np.ones(len(keys), bool)
+    last[:-1] = keys[1:] != keys[:-1]
+    pool.reshape(-1)[keys[last]] = dst[vals[last]].astype(np.int32)
+    np.add.at(count, su, 1)
+
+
+def negpool_sample(pool: np.ndarray, count: np.ndarray, src, seed: int, call: int) -> np.ndarray:
+    """negatives.py:105-126: a uniform slot among the valid ones (a prefix of
+    min(count, P) slots), int(f32(U) * f32(v)) clamped to P-1; a random node when
+    the source has no history."""
+    N, P = pool.shape
+    out = np.empty(len(src), np.int64)
+    for q in range(len(src)):
+        u = int(src[q])
+        c = int(count[u]) if 0 <= u < N else 0
+        v = min(c, P)
+        if v > 0:
+            s = min(int(uniform01(rand64(seed, call, q, 2)) * np.float32(v)), P - 1)
+            out[q] = pool[u, s]
+        else:
+            out[q] = rand64(seed, call, q, 3) % N
+    return out

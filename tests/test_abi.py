@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(L, n), n
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
-    assert L.tgx_abi_version() == 8
+    assert L.tgx_abi_version() == 9
     nm = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
                         text=True).stdout
     exported = set(re.findall(r"\bT (tgx_\w+)", nm))
@@ -204,6 +204,22 @@ def test_csr_build_argument_checks():
     # workspace: keys, values and node keys double-buffered, plus the digit counts
     assert L.tgx_csr_build_workspace_size(1 << 20) >= (1 << 20) * 32 + 256 * 512 * 4
     assert L.tgx_csr_build_workspace_size(0) > 0
+
+
+def test_negpool_argument_checks():
+    L = _lib.lib()
+    assert L.tgx_negpool_update(None, None, 10, 4, 8, 8, 1, 0, 0, 8, 1 << 20, None, None) == 1
+    assert L.tgx_negpool_update(8, 8, 0, 4, 8, 8, 1, 0, 0, 8, 1 << 20, None, None) == 3
+    assert L.tgx_negpool_update(8, 8, 10, 0, 8, 8, 1, 0, 0, 8, 1 << 20, None, None) == 3
+    assert "pool_size" in _err()
+    assert L.tgx_negpool_update(8, 8, 10, 4, None, 8, 1, 0, 0, 8, 1 << 20, None, None) == 1
+    assert L.tgx_negpool_update(8, 8, 10, 4, 8, 8, 100, 0, 0, 8, 16, None, None) == 1
+    assert "workspace" in _err()
+    assert L.tgx_negpool_update(8, 8, 10, 4, 8, 8, 0, 0, 0, None, 0, None, None) == 0  # empty batch
+    assert L.tgx_negpool_sample(8, 8, 10, 4, None, 5, 0, 0, 8, None, None) == 1
+    assert L.tgx_negpool_sample(8, 8, 10, 4, 8, -1, 0, 0, 8, None, None) == 1
+    # keys, values, composite keys and values double-buffered, plus digit counts
+    assert L.tgx_negpool_update_workspace_size(1 << 16) >= (1 << 16) * 40
 
 
 def test_co_occurrence_argument_checks():

@@ -325,3 +325,69 @@ def test_planted_cos_mistake_is_caught():
     exact = O.time_encode_exact(dt, w)
     wrong = np.cos(dt[..., None].astype(np.float64) * w.astype(np.float64))
     assert np.max(np.abs(exact - wrong)) > 1e-6
+
+
+# ---------------------------------------------------------------- negative pool
+def test_splitmix64_known_outputs():
+    """mix64 is the splitmix64 finalizer: its outputs on the states G, 2G, 3G are
+    the published first three values of splitmix64 seeded with 0."""
+    G = 0x9E3779B97F4A7C15
+    m = (1 << 64) - 1
+    assert [O.mix64(k * G & m) for k in (1, 2, 3)] == [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4,
+                                                      0x06C45D188009454F]
+    assert O.uniform01(0) == 0.0 and O.uniform01(m) == np.float32(1 - 2.0 ** -24)
+
+
+@pytest.mark.parametrize("P", [1, 4, 16])
+def test_negpool_sorted_restatement_matches_sequential(P):
+    """The device's two-sort formulation equals the edge-by-edge update, across the
+    fill/replace boundary inside a batch, hot sources, same-slot collisions and
+    out-of-range ids."""
+    rng = np.random.default_rng(P)
+    N = 30
+    a = np.full((N, P), -1, np.int32)
+    b = a.copy()
+    ca = np.zeros(N, np.int64)
+    cb = ca.copy()
+    for call in range(12):
+        n = int(rng.integers(0, 80))
+        src = rng.integers(-1, N + 1, n)
+        src[: n // 3] = 2  # a hot source
+        dst = rng.integers(0, 1000, n)
+        O.negpool_update(a, ca, src, dst, 77, call)
+        O.negpool_update_sorted(b, cb, src, dst, 77, call)
+        assert np.array_equal(a, b) and np.array_equal(ca, cb), call
+    assert ca[2] > P  # the hot source went past the fill phase
+
+
+def test_negpool_reservoir_keeps_every_edge_with_probability_p_over_n():
+    """Reservoir sampling (negatives.py:45-53): after T edges of one source each
+    edge is in the pool with probability P/T."""
+    P, T, trials = 8, 64, 600
+    hits = np.zeros(T)
+    for seed in range(trials):
+        pool = np.full((1, P), -1, np.int32)
+        cnt = np.zeros(1, np.int64)
+        for call, s in enumerate(range(0, T, 16)):
+            O.negpool_update(pool, cnt, np.zeros(16, np.int64), np.arange(s, s + 16), seed, call)
+        assert cnt[0] == T and (pool >= 0).all()
+        hits[pool[0]] += 1
+    p = hits / trials
+    # each edge: binomial(600, 1/8), sd 0.0135; the mean is exact
+    assert abs(p.mean() - P / T) < 1e-12
+    assert np.abs(p - P / T).max() < 0.065
+    assert abs(p[:T // 2].mean() - p[T // 2:].mean()) < 0.02  # old and new edges alike
+
+
+def test_negpool_sample_is_uniform_over_valid_slots_and_falls_back():
+    P, N = 16, 50
+    pool = np.full((N, P), -1, np.int32)
+    cnt = np.zeros(N, np.int64)
+    pool[3, :5] = np.arange(100, 105)
+    cnt[3] = 5
+    out = O.negpool_sample(pool, cnt, np.full(5000, 3), 9, 0)
+    vals, freq = np.unique(out, return_counts=True)
+    assert list(vals) == list(range(100, 105))
+    assert np.abs(freq / 5000 - 0.2).max() < 0.03
+    fb = O.negpool_sample(pool, cnt, np.array([7, 7, 60, -1]), 9, 1)  # no history / out of range
+    assert ((fb >= 0) & (fb < N)).all()

@@ -18,7 +18,7 @@ CSRC = PKG / "csrc"
 INCLUDE = ROOT / "include"
 OUT_DIR = PKG / "_lib"
 LIB = OUT_DIR / "libtgx.so"
-SOURCES = ["tgx_common.hip", "tgx_ring.hip", "tgx_recent.hip", "tgx_csr.hip"]
+SOURCES = ["tgx_common.hip", "tgx_ring.hip", "tgx_recent.hip", "tgx_csr.hip", "tgx_negpool.hip"]
 
 ARCH = "gfx950"
 HIPCC_FLAGS = [

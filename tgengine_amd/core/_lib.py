@@ -93,6 +93,11 @@ SIGNATURES = {
     "tgx_co_occurrence": (c_i32, [c_vp, c_vp, c_i64, c_i32, c_vp, c_vp, c_vp, c_vp]),
     "tgx_csr_build": (c_i32, [ctypes.POINTER(TgxCsrBuildArgs), c_vp]),
     "tgx_csr_build_workspace_size": (ctypes.c_size_t, [c_i64]),
+    "tgx_negpool_update_workspace_size": (ctypes.c_size_t, [c_i64]),
+    "tgx_negpool_update": (c_i32, [c_vp, c_vp, c_i64, c_i32, c_vp, c_vp, c_i64, ctypes.c_uint64,
+                                   ctypes.c_uint64, c_vp, ctypes.c_size_t, c_vp, c_vp]),
+    "tgx_negpool_sample": (c_i32, [c_vp, c_vp, c_i64, c_i32, c_vp, c_i64, ctypes.c_uint64,
+                                   ctypes.c_uint64, c_vp, c_vp, c_vp]),
     "tgx_last_error": (ctypes.c_char_p, []),
     "tgx_abi_version": (c_i32, []),
 }
@@ -122,7 +127,7 @@ def lib() -> ctypes.CDLL:
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
-        if handle.tgx_abi_version() != 8:
+        if handle.tgx_abi_version() != 9:
             raise RuntimeError("libtgx ABI version mismatch")
         _lib = handle
         return _lib

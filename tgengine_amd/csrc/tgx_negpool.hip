@@ -1,0 +1,253 @@
+// Historical negative pool (reference pipeline/negatives.py:14-126): per node a
+// pool of P destination ids kept by reservoir sampling over every edge seen
+// from that node, and uniform draws from it.
+//
+// update(src, dst): edge j of the batch, the r-th of its source u in batch
+// order, is u's e-th edge overall, e = count[u] + r + 1.  While e <= P it fills
+// slot e-1; after that it replaces a random slot with probability P/e
+// (float32, as the reference computes it).  The reference resolves two
+// accepted edges on one (u, slot) by whichever index_put_ write lands last;
+// here the later edge of the batch wins.  count[u] += (edges of u).
+//
+//   1. stable radix sort of the edges by source (tgx_radix.h): r = position
+//      - start of the source's run;
+//   2. decide: fill / replace / skip, and the key u*P + slot of accepted edges;
+//   3. stable radix sort of accepted edges by that key: the last of each equal
+//      run is the latest edge, which writes the slot;
+//   4. counts: the last edge of each source run adds the run length.
+//
+// sample(src): with v = min(count[u], P) valid slots (slots fill in order, so
+// they are a prefix), slot = int(f32(U) * f32(v)) clamped to P-1, else a
+// random node when u has no history.
+//
+// Random numbers: rand64(seed, call, i, stream) = mix(mix(mix(seed ^ G) ^ call)
+// ^ (4 i + stream)) with mix the splitmix64 finalizer and G its golden-ratio
+// increment; U = (rand64 >> 40) * 2^-24.  Streams: 0 accept, 1 replacement
+// slot (update); 2 slot, 3 fallback node (sample).
+#include "tgx_radix.h"
+
+namespace tgx {
+namespace {
+
+constexpr uint64_t kGolden = 0x9e3779b97f4a7c15ull;
+
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ uint64_t rand64(uint64_t seed, uint64_t call, uint64_t i, uint64_t stream) {
+  return mix64(mix64(mix64(seed ^ kGolden) ^ call) ^ (4 * i + stream));
+}
+
+__device__ __forceinline__ float uniform01(uint64_t h) {
+  return static_cast<float>(h >> 40) * 5.9604644775390625e-08f;  // 2^-24
+}
+
+constexpr uint32_t kBadKey = 0xffffffffu;
+constexpr uint64_t kSkip = ~uint64_t(0);
+
+__global__ __launch_bounds__(kThreads) void np_keys(const int64_t* __restrict__ src, int64_t n, int64_t N,
+                                                    uint32_t* __restrict__ key, uint32_t* __restrict__ idx,
+                                                    int32_t* __restrict__ status) {
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  bool bad = false;
+  if (j < n) {
+    const int64_t u = src[j];
+    bad = u < 0 || u >= N;
+    key[j] = bad ? kBadKey : static_cast<uint32_t>(u);
+    idx[j] = static_cast<uint32_t>(j);
+  }
+  const uint64_t bm = __ballot(bad);
+  if ((threadIdx.x & (kWave - 1)) == 0 && bm != 0 && status != nullptr)
+    atomicAdd(&status[TGX_ST_BAD_EVENT_NODE], __popcll(bm));
+}
+
+// start of the run of key k in the sorted keys
+__device__ __forceinline__ int64_t run_start(const uint32_t* __restrict__ skey, int64_t n, uint32_t k) {
+  int64_t lo = 0, hi = n;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (skey[mid] < k)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  return lo;
+}
+
+__global__ __launch_bounds__(kThreads) void np_decide(const uint32_t* __restrict__ skey,
+                                                      const uint32_t* __restrict__ sidx, int64_t n,
+                                                      const int64_t* __restrict__ count, int P,
+                                                      uint64_t seed, uint64_t call,
+                                                      uint64_t* __restrict__ ckey,
+                                                      uint32_t* __restrict__ cval) {
+  const int64_t p = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (p >= n) return;
+  const uint32_t u = skey[p];
+  const uint32_t j = sidx[p];
+  uint64_t key = kSkip;
+  if (u != kBadKey) {
+    const int64_t r = p - run_start(skey, n, u);
+    const int64_t e = count[u] + r + 1;
+    int64_t slot = -1;
+    if (e <= P) {
+      slot = e - 1;
+    } else if (uniform01(rand64(seed, call, j, 0)) < static_cast<float>(P) / static_cast<float>(e)) {
+      slot = static_cast<int64_t>(rand64(seed, call, j, 1) % static_cast<uint64_t>(P));
+    }
+    if (slot >= 0) key = static_cast<uint64_t>(u) * static_cast<uint64_t>(P) + static_cast<uint64_t>(slot);
+  }
+  ckey[p] = key;
+  cval[p] = j;
+}
+
+__global__ __launch_bounds__(kThreads) void np_write(const uint64_t* __restrict__ ckey,
+                                                     const uint32_t* __restrict__ cval, int64_t n,
+                                                     const int64_t* __restrict__ dst,
+                                                     int32_t* __restrict__ pool) {
+  const int64_t q = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (q >= n) return;
+  const uint64_t k = ckey[q];
+  if (k == kSkip) return;
+  if (q + 1 < n && ckey[q + 1] == k) return;  // a later edge takes this slot
+  pool[k] = static_cast<int32_t>(dst[cval[q]]);
+}
+
+__global__ __launch_bounds__(kThreads) void np_count(const uint32_t* __restrict__ skey, int64_t n,
+                                                     int64_t* __restrict__ count) {
+  const int64_t p = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (p >= n) return;
+  const uint32_t u = skey[p];
+  if (u == kBadKey || (p + 1 < n && skey[p + 1] == u)) return;
+  count[u] += p - run_start(skey, n, u) + 1;
+}
+
+__global__ __launch_bounds__(kThreads) void np_sample(const int32_t* __restrict__ pool,
+                                                      const int64_t* __restrict__ count, int64_t N, int P,
+                                                      const int64_t* __restrict__ src, int64_t n,
+                                                      uint64_t seed, uint64_t call,
+                                                      int64_t* __restrict__ out,
+                                                      int32_t* __restrict__ status) {
+  const int64_t q = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  bool bad = false;
+  if (q < n) {
+    const int64_t u = src[q];
+    bad = u < 0 || u >= N;
+    const int64_t c = bad ? 0 : count[u];
+    const int64_t v = c < P ? c : P;
+    if (v > 0) {
+      int64_t s = static_cast<int64_t>(uniform01(rand64(seed, call, q, 2)) * static_cast<float>(v));
+      if (s > P - 1) s = P - 1;
+      out[q] = pool[u * P + s];
+    } else {
+      out[q] = static_cast<int64_t>(rand64(seed, call, q, 3) % static_cast<uint64_t>(N));
+    }
+  }
+  const uint64_t bm = __ballot(bad);
+  if ((threadIdx.x & (kWave - 1)) == 0 && bm != 0 && status != nullptr)
+    atomicAdd(&status[TGX_ST_BAD_QUERY_NODE], __popcll(bm));
+}
+
+struct NpLayout {
+  RadixScratch r;
+  size_t key = 0, idx = 0, ckey = 0, cval = 0, count = 0, sums = 0, total = 0;
+};
+
+NpLayout np_layout(int64_t n) {
+  NpLayout w;
+  w.r = radix_scratch(n);
+  const size_t un = static_cast<size_t>(std::max<int64_t>(n, 1));
+  w.key = 0;
+  w.idx = w.key + 2 * align256(un * 4);
+  w.ckey = w.idx + 2 * align256(un * 4);
+  w.cval = w.ckey + 2 * align256(un * 8);
+  w.count = w.cval + 2 * align256(un * 4);
+  w.sums = w.count + w.r.count_bytes;
+  w.total = w.sums + w.r.sums_bytes;
+  return w;
+}
+
+int bits_for(uint64_t max_plus_one) {  // 2^bits - 1 >= max_plus_one - 1 ... and above every valid key
+  int bits = 1;
+  while (bits < 64 && (uint64_t(1) << bits) < max_plus_one + 1) ++bits;
+  return bits;
+}
+
+int check_pool(const char* who, const int32_t* pool, const int64_t* count, int64_t N, int32_t P) {
+  if (pool == nullptr || count == nullptr) return fail(TGX_ERR_ARG, "%s: pool/count must not be NULL", who);
+  if (N <= 0 || N >= (int64_t(1) << 31))
+    return fail(TGX_ERR_LIMIT, "%s: num_nodes %lld outside [1, 2^31)", who, (long long)N);
+  if (P < 1 || P > (1 << 20)) return fail(TGX_ERR_LIMIT, "%s: pool_size %d outside [1, 2^20]", who, P);
+  return TGX_OK;
+}
+
+}  // namespace
+}  // namespace tgx
+
+using namespace tgx;
+
+extern "C" size_t tgx_negpool_update_workspace_size(int64_t n) {
+  if (n < 0) return 0;
+  return np_layout(n).total;
+}
+
+extern "C" int tgx_negpool_update(int32_t* pool, int64_t* count, int64_t num_nodes, int32_t pool_size,
+                                  const int64_t* src, const int64_t* dst, int64_t n, uint64_t seed,
+                                  uint64_t call, void* workspace, size_t workspace_bytes,
+                                  int32_t* status, void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  int rc = check_pool("tgx_negpool_update", pool, count, num_nodes, pool_size);
+  if (rc) return rc;
+  if (n < 0 || n >= (int64_t(1) << 31))
+    return fail(TGX_ERR_LIMIT, "tgx_negpool_update: %lld edges outside [0, 2^31)", (long long)n);
+  if (n == 0) return TGX_OK;
+  if (src == nullptr || dst == nullptr) return fail(TGX_ERR_ARG, "tgx_negpool_update: src/dst must not be NULL");
+  const NpLayout w = np_layout(n);
+  if (workspace == nullptr || workspace_bytes < w.total)
+    return fail(TGX_ERR_ARG, "tgx_negpool_update: workspace of %zu bytes needed, got %zu", w.total,
+                workspace_bytes);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  const size_t un = static_cast<size_t>(n);
+  uint32_t* key[2] = {reinterpret_cast<uint32_t*>(ws + w.key), reinterpret_cast<uint32_t*>(ws + w.key + align256(un * 4))};
+  uint32_t* idx[2] = {reinterpret_cast<uint32_t*>(ws + w.idx), reinterpret_cast<uint32_t*>(ws + w.idx + align256(un * 4))};
+  uint64_t* ck[2] = {reinterpret_cast<uint64_t*>(ws + w.ckey), reinterpret_cast<uint64_t*>(ws + w.ckey + align256(un * 8))};
+  uint32_t* cv[2] = {reinterpret_cast<uint32_t*>(ws + w.cval), reinterpret_cast<uint32_t*>(ws + w.cval + align256(un * 4))};
+  uint32_t* cnt = reinterpret_cast<uint32_t*>(ws + w.count);
+  uint32_t* sums = reinterpret_cast<uint32_t*>(ws + w.sums);
+  const dim3 g1(static_cast<unsigned>(cdiv(n, kThreads)));
+  hipLaunchKernelGGL(np_keys, g1, dim3(kThreads), 0, stream, src, n, num_nodes, key[0], idx[0], status);
+  if ((rc = check_launch("np_keys"))) return rc;
+  int cur = 0;
+  if ((rc = radix_sort<uint32_t>(key, idx, cur, n, bits_for(static_cast<uint64_t>(num_nodes)), w.r, cnt,
+                                 sums, stream)))
+    return rc;
+  hipLaunchKernelGGL(np_decide, g1, dim3(kThreads), 0, stream, static_cast<const uint32_t*>(key[cur]),
+                     static_cast<const uint32_t*>(idx[cur]), n, static_cast<const int64_t*>(count),
+                     static_cast<int>(pool_size), seed, call, ck[0], cv[0]);
+  if ((rc = check_launch("np_decide"))) return rc;
+  int ccur = 0;
+  const uint64_t cells = static_cast<uint64_t>(num_nodes) * static_cast<uint64_t>(pool_size);
+  if ((rc = radix_sort<uint64_t>(ck, cv, ccur, n, bits_for(cells), w.r, cnt, sums, stream))) return rc;
+  hipLaunchKernelGGL(np_write, g1, dim3(kThreads), 0, stream, static_cast<const uint64_t*>(ck[ccur]),
+                     static_cast<const uint32_t*>(cv[ccur]), n, dst, pool);
+  if ((rc = check_launch("np_write"))) return rc;
+  hipLaunchKernelGGL(np_count, g1, dim3(kThreads), 0, stream, static_cast<const uint32_t*>(key[cur]), n,
+                     count);
+  return check_launch("np_count");
+}
+
+extern "C" int tgx_negpool_sample(const int32_t* pool, const int64_t* count, int64_t num_nodes,
+                                  int32_t pool_size, const int64_t* src, int64_t n, uint64_t seed,
+                                  uint64_t call, int64_t* out, int32_t* status, void* stream_) {
+  int rc = check_pool("tgx_negpool_sample", pool, count, num_nodes, pool_size);
+  if (rc) return rc;
+  if (n < 0) return fail(TGX_ERR_ARG, "tgx_negpool_sample: negative size");
+  if (n == 0) return TGX_OK;
+  if (src == nullptr || out == nullptr) return fail(TGX_ERR_ARG, "tgx_negpool_sample: src/out must not be NULL");
+  hipLaunchKernelGGL(np_sample, dim3(static_cast<unsigned>(cdiv(n, kThreads))), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream_), pool, count, num_nodes, static_cast<int>(pool_size),
+                     src, n, seed, call, out, status);
+  return check_launch("np_sample");
+}

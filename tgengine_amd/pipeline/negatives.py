@@ -1,0 +1,127 @@
+"""Negative sampling: the drop-in for tgengine/pipeline/negatives.py.
+
+``HistoricalNegPool`` (reference :14-126) keeps, per source node, a pool of
+``pool_size`` destination ids by reservoir sampling over every edge seen from
+that node, on the device: ``update`` and ``sample`` are one libtgx call each
+(tgx_negpool_update / tgx_negpool_sample).  Random numbers come from the
+library's counter-based generator, seeded once per pool (from torch's global
+generator unless ``seed`` is given) and advanced by one call counter, so a
+pool replays identically for the same seed and calls.  The reference's
+``index_put_`` leaves a slot two accepted edges of one batch pick to whichever
+write lands last; here the later edge of the batch always takes it.
+"""
+from __future__ import annotations
+
+from abc import ABC, abstractmethod
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from tgengine_amd.core import _lib
+from tgengine_amd.core.temporal_graph import TemporalGraph, _stream_handle
+
+
+class HistoricalNegPool:
+    """Per-node bounded pool for historically-correct negative sampling.
+
+    Usage (as the reference):
+        pool = HistoricalNegPool(num_nodes, pool_size=512, device="cuda")
+        pool.update(src, dst)      # alongside graph.advance() for every batch
+        neg = pool.sample(src)     # (B,) int64
+    """
+
+    PADDING: int = -1
+
+    def __init__(self, num_nodes: int, pool_size: int = 512, device: str = "cuda",
+                 seed: Optional[int] = None):
+        self.num_nodes = int(num_nodes)
+        self.pool_size = int(pool_size)
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise RuntimeError("HistoricalNegPool runs on the GPU only (libtgx)")
+        if self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+        _lib.lib()
+        self._pool = torch.full((self.num_nodes, self.pool_size), self.PADDING, dtype=torch.int32,
+                                device=self.device)
+        self._count = torch.zeros(self.num_nodes, dtype=torch.int64, device=self.device)
+        self.seed = int(seed) if seed is not None else int(torch.randint(0, 2 ** 62, (1,)).item())
+        self._call = 0
+        self._status = torch.zeros(_lib.TGX_STATUS_WORDS, dtype=torch.int32, device=self.device)
+        self._ws: Optional[Tensor] = None
+
+    def _ids(self, t: Tensor) -> Tensor:
+        return t.detach().to(self.device, torch.int64).contiguous().reshape(-1)
+
+    def update(self, src: Tensor, dst: Tensor) -> None:
+        """Add (src_i -> dst_i) edges by reservoir sampling (reference :45-103)."""
+        n = int(src.shape[0])
+        if n == 0:
+            self._call += 1  # every update and sample call advances the counter
+            return
+        if dst.shape[0] != n:
+            raise ValueError("src and dst must have the same length")
+        s, d = self._ids(src), self._ids(dst)
+        need = int(_lib.lib().tgx_negpool_update_workspace_size(n))
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = torch.empty(need, dtype=torch.uint8, device=self.device)
+        _lib.check(_lib.lib().tgx_negpool_update(
+            self._pool.data_ptr(), self._count.data_ptr(), self.num_nodes, self.pool_size,
+            s.data_ptr(), d.data_ptr(), n, self.seed, self._call, self._ws.data_ptr(),
+            self._ws.numel(), self._status.data_ptr(), _stream_handle(self.device)), "tgx_negpool_update")
+        self._call += 1
+
+    def sample(self, src: Tensor) -> Tensor:
+        """One historical negative per source, uniform over its pool; a random node
+        for a source without history (reference :105-126)."""
+        s = self._ids(src)
+        out = torch.empty(s.shape[0], dtype=torch.int64, device=self.device)
+        if s.shape[0] > 0:
+            _lib.check(_lib.lib().tgx_negpool_sample(
+                self._pool.data_ptr(), self._count.data_ptr(), self.num_nodes, self.pool_size,
+                s.data_ptr(), s.shape[0], self.seed, self._call, out.data_ptr(),
+                self._status.data_ptr(), _stream_handle(self.device)), "tgx_negpool_sample")
+        self._call += 1
+        return out
+
+
+class NegativeStrategy(ABC):
+    """Base class for negative sampling strategies (reference :129-151)."""
+
+    @abstractmethod
+    def sample(self, src: Tensor, dst: Tensor, time: Tensor, graph: TemporalGraph,
+               edge_indices: Optional[Tensor] = None) -> Tensor:
+        """(B,) or (B, N_neg) negative node ids."""
+
+    def update(self, src: Tensor, dst: Tensor) -> None:
+        """Ingest new edges (called alongside graph.advance()). No-op by default."""
+
+
+class HistoricalNegative(NegativeStrategy):
+    """Per-source historical negatives from a device pool (reference :174-192)."""
+
+    def __init__(self, num_nodes: int, pool_size: int = 512, device: str = "cuda",
+                 seed: Optional[int] = None):
+        self._pool = HistoricalNegPool(num_nodes, pool_size=pool_size, device=device, seed=seed)
+        self.num_nodes = num_nodes
+
+    def update(self, src: Tensor, dst: Tensor) -> None:
+        self._pool.update(src, dst)
+
+    def sample(self, src: Tensor, dst: Tensor, time: Tensor, graph: TemporalGraph,
+               edge_indices: Optional[Tensor] = None) -> Tensor:
+        return self._pool.sample(src)
+
+
+class FixedNegative(NegativeStrategy):
+    """Fixed negative lists per global edge index (reference :212-229)."""
+
+    def __init__(self, neg_lists: Tensor):
+        self.neg_lists = neg_lists
+
+    def sample(self, src: Tensor, dst: Tensor, time: Tensor, graph: TemporalGraph,
+               edge_indices: Optional[Tensor] = None) -> Tensor:
+        if edge_indices is None:
+            raise ValueError("FixedNegative requires edge_indices in RawBatch")
+        return self.neg_lists[edge_indices.long()].to(src.device)
