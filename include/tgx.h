@@ -271,7 +271,9 @@ int tgx_negpool_sample(const int32_t* pool, const int64_t* count, int64_t num_no
                        uint64_t call, int64_t* out, int32_t* status, void* stream);
 
 /* Fused most-recent-K gather (+ time encoding, + co-occurrence) (kernels b, c).
- * ring and/or csr may be NULL (no candidates from that store). */
+ * ring and/or csr may be NULL (no candidates from that store); with both NULL
+ * every query is padding and out_feats must be NULL (the row width comes from
+ * them). */
 int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args* args,
                void* stream);
 

@@ -96,6 +96,10 @@ def test_recent_argument_checks():
     assert L.tgx_recent(None, None, ctypes.byref(a), None) == 1 and "must not be NULL" in _err()
     a = _lib.TgxRecentArgs(k=4, group=1, num_queries=5, num_groups=5, num_query_groups=5)
     assert L.tgx_recent(None, None, ctypes.byref(a), None) == 3 and "query groups" in _err()
+    # no ring and no CSR: nothing sizes the feature rows
+    a = _lib.TgxRecentArgs(k=4, group=1, num_queries=5, num_groups=5, nodes=8, times=8,
+                           out_ids=8, out_times=8, out_mask=8, out_feats=8)
+    assert L.tgx_recent(None, None, ctypes.byref(a), None) == 1 and "out_feats" in _err()
     ring = _lib.TgxRing(num_nodes=10, slots=65, feat_dim=2, feat_dtype=0, ids=8, times=8)
     a = _lib.TgxRecentArgs(k=4, group=1, num_queries=5, num_groups=5, nodes=8, times=8,
                            out_ids=8, out_times=8, out_mask=8)

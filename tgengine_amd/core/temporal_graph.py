@@ -419,27 +419,8 @@ class TemporalGraph:
             groups = [(nodes, times, 1)]
         if len(groups) > _lib.TGX_MAX_QUERY_GROUPS:
             raise ValueError(f"at most {_lib.TGX_MAX_QUERY_GROUPS} query groups")
-        ring = self._ring()
-        csr = self._csr()
-        ev0 = ev1 = 0
-        if self.kernel_timer is not None:
-            ev0, ev1 = self.kernel_timer.events()
-        if append is not None and (ring is None or self.device.type != "cuda"):
-            append = None
-        if append is None:
-            res = self._launch_recent(ring, csr, groups, k, plan, group, num_groups, d_t, te_w,
-                                      te_b, dt_mode, co_mode, want_eids, ev0, ev1, None, None)
-        else:
-            # the extension plans the batch when its tensors allow it (int64 /
-            # float64 contiguous 1-D device tensors of one non-zero length)
-            with self._plan_lock:
-                if self._plan is not None:  # an earlier plan nobody advanced: drop it first
-                    self._discard_plan()
-                ws = self._plan_workspace(int(append[0].shape[0]))
-                res = self._launch_recent(ring, csr, groups, k, plan, group, num_groups, d_t, te_w,
-                                          te_b, dt_mode, co_mode, want_eids, ev0, ev1, append, ws)
-                if res[7]:
-                    self._plan = _Plan(append[0], append[1], append[2], _stream_handle(self.device))
+        res = self._gather(groups, k, plan, group, num_groups, d_t, te_w, te_b, dt_mode, co_mode,
+                           want_eids, append)
         out = {"ids": res[0], "times": res[1], "feats": res[2], "mask": res[3]}
         if want_eids:
             out["eids"] = res[4]
@@ -449,8 +430,37 @@ class TemporalGraph:
             out["co_a"], out["co_c"], out["co_pair"] = res[6]
         return out
 
+    def _gather(self, groups, k, plan, group, num_groups, d_t, te_w, te_b, dt_mode, co_mode,
+                want_eids, append) -> list:
+        """One tgx_recent launch over checked query groups; the extension's result
+        list (per-group views: ids, times, feats, mask, eids, te; co-occurrence;
+        whether the ``append`` batch was planned).  When ``append`` is given and the
+        ring exists, the launch also plans that batch (see plan_append)."""
+        if not self._frozen:
+            self.freeze_csr()
+        ring = self._ring()
+        csr = self._csr()
+        ev0 = ev1 = 0
+        if self.kernel_timer is not None:
+            ev0, ev1 = self.kernel_timer.events()
+        stream = _stream_handle(self.device)
+        if append is None or ring is None:
+            return self._launch_recent(ring, csr, groups, k, plan, group, num_groups, d_t, te_w,
+                                       te_b, dt_mode, co_mode, want_eids, ev0, ev1, None, None, stream)
+        # the extension plans the batch when its tensors allow it (int64 / float64
+        # contiguous 1-D device tensors of one non-zero length)
+        with self._plan_lock:
+            if self._plan is not None:  # an earlier plan nobody advanced: drop it first
+                self._discard_plan()
+            ws = self._plan_workspace(int(append[0].shape[0]))
+            res = self._launch_recent(ring, csr, groups, k, plan, group, num_groups, d_t, te_w,
+                                      te_b, dt_mode, co_mode, want_eids, ev0, ev1, append, ws, stream)
+            if res[7]:
+                self._plan = _Plan(append[0], append[1], append[2], stream)
+        return res
+
     def _launch_recent(self, ring, csr, groups, k, plan, group, num_groups, d_t, te_w, te_b,
-                       dt_mode, co_mode, want_eids, ev0, ev1, append, ws):
+                       dt_mode, co_mode, want_eids, ev0, ev1, append, ws, stream):
         a_src, a_dst, a_time = append if append is not None else (None, None, None)
         gn, gt, gp, gv = [], [], [], []
         for grp in groups:
@@ -466,7 +476,7 @@ class TemporalGraph:
             ctypes.addressof(csr) if csr is not None else 0,
             gn, gt, gp, gv, k, self.edge_feat_dim, self.feat_dtype, plan, group,
             -1 if num_groups is None else int(num_groups), int(d_t), te_w, te_b, int(dt_mode),
-            int(co_mode), bool(want_eids), self._status, _stream_handle(self.device), ev0, ev1,
+            int(co_mode), bool(want_eids), self._status, stream, ev0, ev1,
             a_src, a_dst, a_time, ws)
 
     def recent(self, nodes: Tensor, times: Tensor, k: int) -> NeighborData:

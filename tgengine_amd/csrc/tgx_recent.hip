@@ -870,6 +870,9 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
     dtype = csr->feat_dtype;
   }
   if (ring == nullptr && csr == nullptr) {
+    // every query is padding; the rows' width comes from a ring or a CSR
+    if (a->out_feats != nullptr)
+      return fail(TGX_ERR_ARG, "tgx_recent: out_feats needs a ring or a CSR (their feat_dim sizes the rows)");
     P.N = INT64_MAX;
     feat_dim = 0;
     dtype = TGX_F32;

@@ -139,6 +139,8 @@ class DataPipeline:
 
     def prepare(self, raw_batch: RawBatch) -> PreparedBatch:
         spec = self.spec
+        if spec.neighbors.k2 == 0:
+            return self._prepare_1hop(raw_batch)
         k, k2 = spec.neighbors.k, spec.neighbors.k2
         device = raw_batch.device
         b = raw_batch.src.shape[0]
@@ -203,6 +205,65 @@ class DataPipeline:
         return PreparedBatch(
             src=raw_batch.src, dst=raw_batch.dst,
             neg=raw_batch.neg if raw_batch.neg is not None else torch.empty(0, device=device),
+            time=raw_batch.time,
+            src_neighbors=nbrs.get("src"), dst_neighbors=nbrs.get("dst"),
+            neg_neighbors=nbrs.get("neg"), neg_src_neighbors=nbrs.get("neg_src"),
+            neg_src=raw_batch.neg_src, co_occurrence=co_occur,
+            node_labels=raw_batch.node_labels, edge_labels=raw_batch.edge_labels,
+            node_feat=raw_batch.node_feat, co_occurrence_freq=co_freq)
+
+    def _prepare_1hop(self, raw_batch: RawBatch) -> PreparedBatch:
+        """prepare() of a 1-hop spec: one launch (gather, time encoding,
+        co-occurrence and the plan of this batch's ring update), its per-group
+        views put straight into the NeighborData of each group."""
+        spec = self.spec
+        g = self.graph
+        names, qgroups, _, per_event = self._query_groups(raw_batch)
+        if spec.edge_ids and not g.track_edge_ids:
+            raise ValueError("GatherSpec.edge_ids needs a TemporalGraph built with track_edge_ids=True")
+        want_co = spec.co_occurrence and "src" in names and "dst" in names
+        co_mode = _CO_MODES[spec.co_occurrence_mode] if want_co else _lib.TGX_CO_NONE
+        d_t = int(spec.time_encoding)
+        te_w = te_b = None
+        if d_t > 0:
+            te_w, te_b = self._te_params(d_t)
+        src = raw_batch.src
+        append = (src, raw_batch.dst, raw_batch.time) if self.plan_updates else None
+        k = spec.neighbors.k
+        b = src.shape[0]
+        if co_mode != _lib.TGX_CO_NONE:
+            offs, off = [], 0
+            for per in per_event:  # event-major groups: [src p, dst p, its negatives, neg_src p]
+                offs.append((off, per))
+                off += b * per
+            G = sum(per_event)
+            if G > _lib.TGX_MAX_GROUP:
+                raise ValueError(f"{G} queries per event exceed the fused group limit {_lib.TGX_MAX_GROUP}")
+            res = g._gather(qgroups, k, self._plan(("ev", b, tuple(per_event)), b, offs), G, b, d_t,
+                            te_w, te_b, _DT_MODES[spec.dt_mode], co_mode, spec.edge_ids, append)
+        else:
+            res = g._gather(qgroups, k, None, self.queries_per_workgroup, None, d_t, te_w, te_b,
+                            _DT_MODES[spec.dt_mode], co_mode, spec.edge_ids, append)
+        ids, tms, fts, msk, eids, te = res[0], res[1], res[2], res[3], res[4], res[5]
+        nbrs = {}
+        for i, name in enumerate(names):
+            nd = NeighborData(ids[i], tms[i], fts[i], msk[i])
+            if te:
+                nd.time_enc = te[i]
+            if eids:
+                nd.edge_ids = eids[i]
+            nbrs[name] = nd
+        co_occur = co_freq = None
+        if spec.co_occurrence:
+            if want_co:
+                co_a, co_c, co_occur = res[6]
+                co_freq = (co_a, co_c)
+            else:
+                co_occur = g.co_neighbors(src, raw_batch.dst, raw_batch.time, k=k)
+        neg = raw_batch.neg
+        return PreparedBatch(
+            src=src, dst=raw_batch.dst,
+            neg=neg if neg is not None else torch.empty(0, device=src.device),
             time=raw_batch.time,
             src_neighbors=nbrs.get("src"), dst_neighbors=nbrs.get("dst"),
             neg_neighbors=nbrs.get("neg"), neg_src_neighbors=nbrs.get("neg_src"),
