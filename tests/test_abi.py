@@ -177,8 +177,9 @@ def test_ring_plan_commit_discard_argument_checks():
 
 def test_size_queries():
     L = _lib.lib()
-    # per-node counter + 8-entry node list, and 16 control words
-    assert L.tgx_ring_scratch_size(1000) == (9 * 1000 + 16) * 4
+    # per-node counter + 8-entry node list, and 32 control words (16-byte aligned)
+    assert L.tgx_ring_scratch_size(1000) == (9 * 1000 + 32) * 4
+    assert L.tgx_ring_scratch_size(1001) == (9 * 1001 + 3 + 32) * 4
     n = 2 * 4000
     ws = L.tgx_ring_append_workspace_size(4000)
     # tickets, 8-byte overflow pairs (or lists), groups, large groups

@@ -25,8 +25,8 @@
 //            c <= kListCap is ranked by one wavefront from its node list; a
 //            larger group by a workgroup that marks its list and overflow
 //            entries in an LDS bitmap of the whole batch and takes the kept
-//            entries from the top.  The last workgroup to finish reports
-//            diagnostics and clears the cursors.
+//            entries from the top.  Workgroup 0 reports the diagnostics and
+//            clears the other cursor set for the next plan (two sets alternate).
 // Larger batches: four launches, whose lists are sized after counting.
 //   count  : tickets.
 //   groups : the ticket-0 entry of every node seen more than once reserves
@@ -106,14 +106,15 @@ struct AppendParams : PlanParams {
   int gb;           // blocks of the small-group role
 };
 
-// the plan's diagnostics reach the status words only when the batch commits
-__device__ __forceinline__ void commit_diagnostics(const AppendParams& P) {
+// the plan's diagnostics (words time_word, bad_word) reach the status words only
+// when the batch commits
+__device__ __forceinline__ void commit_diagnostics(const AppendParams& P, int time_word, int bad_word) {
   if (P.status != nullptr) {
-    if (P.ctl[kCtlBad] != 0) atomicAdd(&P.status[TGX_ST_BAD_EVENT_NODE], P.ctl[kCtlBad]);
-    if (P.ctl[kCtlTimeOk] == 0) atomicAdd(&P.status[TGX_ST_KEY_COLLISION], 1);
+    if (P.ctl[bad_word] != 0) atomicAdd(&P.status[TGX_ST_BAD_EVENT_NODE], P.ctl[bad_word]);
+    if (P.ctl[time_word] == 0) atomicAdd(&P.status[TGX_ST_KEY_COLLISION], 1);
   }
-  P.ctl[kCtlTimeOk] = 0;
-  P.ctl[kCtlBad] = 0;
+  P.ctl[time_word] = 0;
+  P.ctl[bad_word] = 0;
 }
 
 // ---- four-launch 1. count ----------------------------------------------------
@@ -130,7 +131,7 @@ __global__ __launch_bounds__(kThreads) void append_count(PlanParams P) {
   const int32_t u = entry_prologue(P, i, bad, time_ok);
   const int32_t t = node_ticket(P, u, L);
   if (i < P.n) P.ticket[i] = t;
-  report_diagnostics(P, bad, time_ok);
+  report_diagnostics(P, bad, time_ok, kCtlTimeOk, kCtlBad);
 }
 
 // ---- two-launch 1. plan -------------------------------------------------------
@@ -339,7 +340,7 @@ __global__ __launch_bounds__(kThreads) void append_commit(AppendParams P) {
   __shared__ int32_t rows[kCommitWaves][TGX_MAX_SLOTS];  // kept entry index by e
   __shared__ int32_t wsum[kCommitWaves];
   const int blk = static_cast<int>(blockIdx.x);
-  if (blk == 0 && threadIdx.x == 0) commit_diagnostics(P);
+  if (blk == 0 && threadIdx.x == 0) commit_diagnostics(P, kCtlTimeOk, kCtlBad);
   if (blk < P.ga) {
     commit_singletons<VEC>(P, blk);
     return;
@@ -450,10 +451,17 @@ __global__ __launch_bounds__(kThreads) void fast_commit(AppendParams P) {
   const int blk = static_cast<int>(blockIdx.x);
   const int wv = threadIdx.x / kWave;
   const int lane = threadIdx.x & (kWave - 1);
+  const int ph = P.ctl[kCtlPhaseCur] & 1;  // the cursor set of this batch's plan
+  if (blk == 0 && threadIdx.x == 0) {
+    // the other set belongs to a committed plan: clear it for the next plan
+    *reinterpret_cast<uint64_t*>(P.ctl + kCtlFCursor + 2 * (1 - ph)) = 0;
+    P.ctl[kCtlPhaseNext] = 1 - ph;
+    commit_diagnostics(P, kCtlFDiag + 2 * ph, kCtlFDiag + 2 * ph + 1);
+  }
   if (blk < P.ga) {
     commit_singletons<VEC>(P, blk);
   } else {
-    const uint64_t cur = *reinterpret_cast<const uint64_t*>(P.ctl + kCtlFCursor);
+    const uint64_t cur = *reinterpret_cast<const uint64_t*>(P.ctl + kCtlFCursor + 2 * ph);
     if (blk < P.ga + P.gb) {
       const int ngroups = field(cur, kFGroups);
       for (int gid = (blk - P.ga) * kCommitWaves + wv; gid < ngroups;
@@ -475,23 +483,22 @@ __global__ __launch_bounds__(kThreads) void fast_commit(AppendParams P) {
         fast_large<VEC>(P, P.large + gid, novf, bitmap, rows[0], wsum);
     }
   }
-  // the last workgroup to finish (every other one has read the cursors) reports
-  // the plan's diagnostics and clears the cursors for the next plan
-  __syncthreads();
-  if (threadIdx.x == 0 && atomicAdd(&P.ctl[kCtlFDone], 1) == static_cast<int>(gridDim.x) - 1) {
-    commit_diagnostics(P);
-    *reinterpret_cast<uint64_t*>(P.ctl + kCtlFCursor) = 0;
-    P.ctl[kCtlFDone] = 0;
-  }
 }
 
 // ---- discard: restore the scratch of a planned batch without committing it ----
-__global__ __launch_bounds__(kThreads) void append_discard(PlanParams P) {
+__global__ __launch_bounds__(kThreads) void append_discard(PlanParams P, int two_launch) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   if (i == 0) {
-    P.ctl[kCtlTimeOk] = 0;
-    P.ctl[kCtlBad] = 0;
-    *reinterpret_cast<uint64_t*>(P.ctl + kCtlFCursor) = 0;
+    if (two_launch) {
+      // the replacement plan takes the same set again (phase_next is unchanged)
+      const int ph = P.ctl[kCtlPhaseCur] & 1;
+      *reinterpret_cast<uint64_t*>(P.ctl + kCtlFCursor + 2 * ph) = 0;
+      P.ctl[kCtlFDiag + 2 * ph] = 0;
+      P.ctl[kCtlFDiag + 2 * ph + 1] = 0;
+    } else {
+      P.ctl[kCtlTimeOk] = 0;
+      P.ctl[kCtlBad] = 0;
+    }
   }
   if (i >= P.n) return;
   const int64_t u = entry_node(P.src, P.dst, i, P.b);
@@ -699,6 +706,7 @@ extern "C" int tgx_ring_discard(const tgx_ring* ring, const int64_t* src, const 
   int rc = plan_setup("tgx_ring_discard", ring, src, dst, &kNoTime, b, workspace, workspace_bytes, P);
   if (rc != TGX_OK || b == 0) return rc;
   const dim3 grid1(static_cast<unsigned>((P.n + kThreads - 1) / kThreads));
-  hipLaunchKernelGGL(append_discard, grid1, dim3(kThreads), 0, static_cast<hipStream_t>(stream_), P);
+  hipLaunchKernelGGL(append_discard, grid1, dim3(kThreads), 0, static_cast<hipStream_t>(stream_), P,
+                     plan_fused_ok(P) ? 1 : 0);
   return check_launch("append_discard");
 }

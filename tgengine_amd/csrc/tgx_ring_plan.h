@@ -21,13 +21,20 @@ constexpr int kPlanHashBits = 10;           // LDS hash of equal nodes, at most 
 constexpr int kPlanHash = 1 << kPlanHashBits;
 static_assert(kPlanHash >= 2 * kPlanMaxThreads, "hash table at most half full");
 
-// ctl words (ring scratch): four-launch cursors, shared diagnostics, two-launch cursors
+// ctl words (ring scratch).  Four-launch: cursors and diagnostics (words 0-4).
+// Two-launch: two cursor sets (uint64 at words 8 and 10: overflow | groups |
+// large counts) and two diagnostics pairs (time flag, bad count at 16 + 2p),
+// used by alternate plans.  A plan takes set p = phase_next and records it in
+// phase_cur; its commit reads set phase_cur, and its workgroup 0 clears the other
+// set (its plan is committed), reports and clears this plan's diagnostics and
+// sets phase_next to the other set, so nothing waits for the last workgroup.
 enum {
   kCtlCursor = 0, kCtlGroups = 1, kCtlTimeOk = 2, kCtlLarge = 3, kCtlBad = 4,
-  kCtlFCursor = 8,  // uint64 over words 8, 9: two-launch overflow | groups | large counts
-  kCtlFDone = 10
+  kCtlFCursor = 8,  // + 2p
+  kCtlPhaseNext = 12, kCtlPhaseCur = 13,
+  kCtlFDiag = 16    // + 2p: time flag, + 2p + 1: bad count
 };
-constexpr int kCtlWords = 16;
+constexpr int kCtlWords = 32;
 // fields of the two-launch cursor word (every count is at most n <= 2^15)
 constexpr int kFieldBits = 21;
 constexpr uint64_t kFieldMask = (uint64_t(1) << kFieldBits) - 1;
@@ -113,26 +120,32 @@ __device__ __forceinline__ int32_t node_ticket(const PlanParams& P, int32_t u, P
   return u >= 0 ? L.hbase[hs] + rank : -1;
 }
 
-__device__ __forceinline__ void report_diagnostics(const PlanParams& P, int bad, bool time_ok) {
+// out-of-range entries and the time flag into the words time_word / bad_word
+__device__ __forceinline__ void report_diagnostics(const PlanParams& P, int bad, bool time_ok,
+                                                   int time_word, int bad_word) {
   const uint64_t bm = __ballot(bad);
   const uint64_t tm = __ballot(time_ok);
   if ((threadIdx.x & (kWave - 1)) == 0) {
-    if (bm) atomicAdd(&P.ctl[kCtlBad], __popcll(bm));
-    if (tm) atomicOr(&P.ctl[kCtlTimeOk], 1);
+    if (bm) atomicAdd(&P.ctl[bad_word], __popcll(bm));
+    if (tm) atomicOr(&P.ctl[time_word], 1);
   }
 }
 
 // Two-launch plan of entries [block * blockDim.x, +blockDim.x) (blockDim.x a
 // multiple of kWave, at most kPlanMaxThreads; every thread of the workgroup
-// calls it).  Ticket t < kListCap stores the entry in lst[u][t]; later tickets
-// append (u, i) to the overflow array; the ticket-1 entry appends u to the
-// group list, the ticket-kListCap entry to the large-group list.  The three
-// wave counts are packed in one word: a workgroup prefix in LDS, then one
-// cursor atomic per workgroup.
+// calls it), into cursor set phase_next.  Ticket t < kListCap stores the entry
+// in lst[u][t]; later tickets append (u, i) to the overflow array; the ticket-1
+// entry appends u to the group list, the ticket-kListCap entry to the
+// large-group list.  The three wave counts are packed in one word: a workgroup
+// prefix in LDS, then one cursor atomic per workgroup.
 __device__ __forceinline__ void plan_block(const PlanParams& P, int64_t block, PlanLds& L) {
   const int64_t i = block * blockDim.x + threadIdx.x;
   const int wv = threadIdx.x / kWave;
   const int lane = threadIdx.x & (kWave - 1);
+  // nobody writes phase_next while a plan runs; every workgroup records the
+  // same phase for the commit
+  const int ph = P.ctl[kCtlPhaseNext] & 1;
+  if (threadIdx.x == 0) P.ctl[kCtlPhaseCur] = ph;
   int bad;
   bool time_ok;
   const int32_t u = entry_prologue(P, i, bad, time_ok);
@@ -155,7 +168,7 @@ __device__ __forceinline__ void plan_block(const PlanParams& P, int64_t block, P
       tot += c;
     }
     L.wofs[kPlanMaxWaves] =
-        tot != 0 ? atomicAdd(reinterpret_cast<unsigned long long*>(P.ctl + kCtlFCursor),
+        tot != 0 ? atomicAdd(reinterpret_cast<unsigned long long*>(P.ctl + kCtlFCursor + 2 * ph),
                              static_cast<unsigned long long>(tot))
                  : 0;
   }
@@ -166,7 +179,7 @@ __device__ __forceinline__ void plan_block(const PlanParams& P, int64_t block, P
     P.ovf[field(at, kFOvf) + __popcll(om & below)] = make_int2(u, static_cast<int32_t>(i));
   if (t == 1) P.groups[field(at, kFGroups) + __popcll(gm & below)] = u;
   if (t == kListCap) P.large[field(at, kFLarge) + __popcll(lm & below)] = u;
-  report_diagnostics(P, bad, time_ok);
+  report_diagnostics(P, bad, time_ok, kCtlFDiag + 2 * ph, kCtlFDiag + 2 * ph + 1);
 }
 
 // Host side (tgx_ring.hip).  plan_setup checks the arguments of a plan and fills
