@@ -142,9 +142,11 @@ def main():
     torch.cuda.set_device(device)
     # batches: W warm-up, K timed (value), R roofline window (kernel-dispatch events)
     avail = num_batches(cfg)
+    # a short stream (C1) keeps a few batches after the timed work for the CPU baseline
+    reserve = 0 if a.no_cpu else min(64, avail // 10)
     K = min(a.steps, avail)
-    R = min(a.roofline_steps, max(0, avail - K))
-    W = min(a.warmup, max(0, avail - K - R))
+    R = min(a.roofline_steps, max(0, avail - K - reserve))
+    W = min(a.warmup, max(0, avail - K - R - reserve))
     total = W + K + R
     t0 = time.time()
     dev, lens, bts = stage_stream(cfg, 0, total, torch, device)
