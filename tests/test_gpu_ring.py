@@ -226,10 +226,11 @@ def test_ring_zero_features_when_edge_feat_is_none():
 
 
 # ------------------------------------------------------------- planned updates
-# DataPipeline.prepare starts the ring update of its batch on a side stream
-# (TemporalGraph.plan_append); advance() commits the plan when it receives the
-# same src/dst/time tensors, otherwise discards it.  Every path must leave the
-# ring exactly as the oracle's update, with the node counters back at zero.
+# TemporalGraph.plan_append enqueues the first half of a batch's ring update
+# (DataPipeline.prepare runs the same plan inside its gather launch); advance()
+# commits the plan when it receives the same src/dst/time tensors, otherwise
+# discards it.  Every path must leave the ring exactly as the oracle's update,
+# with the node counters back at zero.
 
 def _stream_batches(rng, N, n_batches, b, hot=3):
     out = []
