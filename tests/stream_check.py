@@ -64,14 +64,14 @@ def _eq(name, got, exp, where):
         raise Mismatch(f"{where}: {name} differs at {len(bad)} positions, first {bad[:3].tolist()}")
 
 
-def compare_prepared(cfg, pb, bt, ring, w, where, with_te=True):
-    """Compare one PreparedBatch with the oracle on the same ring state."""
+def compare_prepared(cfg, pb, bt, ring, w, where, with_te=True, csr=None):
+    """Compare one PreparedBatch with the oracle on the same CSR and ring state."""
     b = len(bt["src"])
     K = cfg.k
     d = cfg.feat_dim
     fdt = np.uint16 if cfg.feat_dtype == "bf16" else np.float32
     nodes, qt = queries_of(bt)
-    nb = O.recent(nodes, qt, K, None, ring, d, fdt)
+    nb = O.recent(nodes, qt, K, csr, ring, d, fdt)
     groups = [pb.src_neighbors, pb.dst_neighbors, pb.neg_neighbors]
     ids = np.concatenate([g.neighbor_ids.cpu().numpy() for g in groups])
     tms = np.concatenate([g.timestamps.cpu().numpy() for g in groups])
