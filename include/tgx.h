@@ -182,8 +182,9 @@ typedef struct tgx_recent_args {
  * (write_pos + m) % B, m = 0.., and write_pos grows by min(c, B).
  * feat: [b, feat_dim] in ring->feat_dtype, or NULL for zero features.
  * eids (if the ring has them) receive eid_base + event index.
- * workspace: tgx_ring_append_workspace_size(b) bytes of device memory (no
- * initialisation needed).  Calls on one ring must be ordered (one stream). */
+ * workspace: tgx_ring_append_workspace_size(b) bytes of device memory, 16-byte
+ * aligned (no initialisation needed).  Calls on one ring must be ordered (one
+ * stream). */
 int tgx_ring_append(const tgx_ring* ring, const int64_t* src, const int64_t* dst,
                     const double* time, const void* feat, int64_t b, int64_t eid_base,
                     void* workspace, size_t workspace_bytes, int32_t* status, void* stream);

@@ -173,6 +173,12 @@ def test_ring_plan_commit_discard_argument_checks():
     assert "workspace" in _err()
     ring.slots = 65
     assert L.tgx_ring_commit(r, 8, 8, 8, None, 4, 0, ws, 1 << 16, None, None) == 3
+    ring.slots = 4
+    # the workspace is read as 16-byte vectors
+    base = ctypes.addressof(ws)
+    odd = base + (-base) % 16 + 4
+    assert L.tgx_ring_plan(r, 8, 8, 8, 4, odd, (1 << 16) - 64, None) == 1
+    assert "aligned" in _err()
 
 
 def test_size_queries():
@@ -182,8 +188,8 @@ def test_size_queries():
     assert L.tgx_ring_scratch_size(1001) == (9 * 1001 + 3 + 32) * 4
     n = 2 * 4000
     ws = L.tgx_ring_append_workspace_size(4000)
-    # tickets, 8-byte overflow pairs (or lists), groups, large groups
-    assert ws >= 4 * n + 8 * n + 4 * (n // 2 + 1) + 4 * (n // 65 + 1)
+    # tickets (or entry nodes), four-launch lists, groups, large groups
+    assert ws >= 4 * n + 4 * n + 4 * (n // 2 + 1) + 4 * (n // 9 + 1)
     assert L.tgx_ring_append_workspace_size(0) > 0
 
 

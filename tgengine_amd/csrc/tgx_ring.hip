@@ -17,16 +17,19 @@
 //
 // Batches of up to kFastMaxEntries entries: two launches.
 //   plan   : tickets; ticket t < kListCap stores the entry in the node's list
-//            lst[u][t] (ring scratch), later tickets append (u, i) to an
-//            overflow array; the ticket-1 entry appends the node to the group
-//            list, the ticket-kListCap entry to the large-group list.  The
-//            three cursors share one 64-bit word: one atomic per workgroup.
+//            lst[u][t] (ring scratch); the ticket-1 entry appends the node to
+//            the group list, the ticket-kListCap entry to the large-group
+//            list.  The two cursors share one 64-bit word: one atomic per
+//            workgroup.
 //   commit : singletons (c == 1) are written directly; a group of
 //            c <= kListCap is ranked by one wavefront from its node list; a
-//            larger group by a workgroup that marks its list and overflow
-//            entries in an LDS bitmap of the whole batch and takes the kept
-//            entries from the top.  Workgroup 0 reports the diagnostics and
-//            clears the other cursor set for the next plan (two sets alternate).
+//            larger group by a workgroup that reads the plan's int32 node of
+//            every entry from the top of the batch down, kTopChunk entries at a
+//            time, and ranks the node's entries until the kept ones are found.  Every role
+//            starts its loads before it knows whether it has work, so a role
+//            costs two or three memory round trips.  Workgroup 0 reports the
+//            diagnostics and clears the other cursor set for the next plan
+//            (two sets alternate).
 // Larger batches: four launches, whose lists are sized after counting.
 //   count  : tickets.
 //   groups : the ticket-0 entry of every node seen more than once reserves
@@ -45,6 +48,8 @@
 namespace tgx {
 namespace {
 
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
 constexpr int kThreads = 256;
 constexpr int kCommitWaves = kThreads / kWave;
 constexpr int kWinBits = 8192;                 // bitmap window (indices)
@@ -52,10 +57,8 @@ constexpr int kWinWords = kWinBits / 32;       // 256 words = 1 KB
 static_assert(kWinWords == kThreads, "one bitmap word per thread");
 constexpr int64_t kSmallGroupBlocks = 256;  // commit blocks for small groups (4 waves each)
 constexpr int64_t kLargeGroupBlocks = 64;   // four-launch commit blocks for large groups
-constexpr int kFastWords = kFastMaxEntries / 32;  // two-launch bitmap of the whole batch
-constexpr int kWordsPerThread = kFastWords / kThreads;
-static_assert(kWordsPerThread * kThreads == kFastWords, "bitmap words split evenly");
-constexpr int kScanUnroll = 32;             // overflow pairs in flight per thread
+constexpr int kTopRows = 8;                 // 16-byte loads (4 entry nodes each) in flight per thread
+constexpr int kTopChunk = 4 * kTopRows * kThreads;  // entries per top-down step
 constexpr int64_t kFastLargeBlocks = 128;   // two-launch commit blocks for large groups
 
 // (write_pos + off) % B for write_pos >= 0, 0 <= off < B
@@ -99,7 +102,6 @@ struct AppendParams : PlanParams {
   int64_t* wp;
   int64_t* eids;
   int32_t* nbase;   // [N] four-launch list base of multi-entry nodes (over lst)
-  int32_t* list;    // [n] four-launch lists (over ovf)
   int32_t* status;
   int tpe_log2;     // lanes per entry (singleton copy)
   int ga;           // blocks of the singleton role in commit
@@ -292,20 +294,28 @@ __device__ __forceinline__ void commit_singletons(const AppendParams& P, int blk
   const int64_t i = static_cast<int64_t>(blk) * epb + (threadIdx.x >> P.tpe_log2);
   const int l = threadIdx.x & (tpe - 1);
   if (i >= P.n) return;
+  // the entry's own data is read with its node, before the node is known to be
+  // a singleton, so the role costs two round trips
+  const int64_t e = i < P.b ? i : i - P.b;
   const int64_t u = entry_node(P.src, P.dst, i, P.b);
+  const V* srow = reinterpret_cast<const V*>(P.feat + e * P.row_bytes);
+  const V first = (P.feat != nullptr && l < nv) ? srow[l] : V{};
+  int32_t other = 0;
+  double tm = 0.0;
+  if (l == 0) {
+    other = static_cast<int32_t>(i < P.b ? P.dst[e] : P.src[e]);
+    tm = P.time[e];
+  }
   if (u < 0 || u >= P.N || P.cnt[u] != 1) return;
   const int64_t w = P.wp[u];
   const int64_t slot = u * P.B + ring_slot(w, 0, P.B);
-  const int64_t e = i < P.b ? i : i - P.b;
   V* drow = reinterpret_cast<V*>(P.feats + slot * P.row_bytes);
-  if (P.feat != nullptr) {
-    const V* srow = reinterpret_cast<const V*>(P.feat + e * P.row_bytes);
-    for (int c = l; c < nv; c += tpe) drow[c] = srow[c];
-  } else {
-    for (int c = l; c < nv; c += tpe) drow[c] = V{};
-  }
+  if (l < nv) drow[l] = first;
+  for (int c = l + tpe; c < nv; c += tpe) drow[c] = P.feat != nullptr ? srow[c] : V{};
   if (l == 0) {
-    write_entry_meta(P, i, slot);
+    P.ids[slot] = other;
+    P.times[slot] = tm;
+    if (P.eids != nullptr) P.eids[slot] = P.eid_base + e;
     P.wp[u] = w + 1;
     P.cnt[u] = 0;
   }
@@ -369,118 +379,175 @@ __global__ __launch_bounds__(kThreads) void append_commit(AppendParams P) {
 }
 
 // ---- two-launch 2. commit -------------------------------------------------------
-__device__ __forceinline__ void load_pairs(const AppendParams& P, int j0, int novf,
-                                           int2 (&pr)[kScanUnroll]) {
+// The plan's node of every entry, four per 16-byte load, top-down: row r of
+// thread t holds entries 4q .. 4q + 3 of q = hi4 / 4 - 1 - (r kThreads + t)
+// (hi4 a multiple of 4; the node array is padded to whole 256-byte lines, and
+// indices >= n are masked by the caller), so each row covers 4 kThreads
+// consecutive entries in descending order.
+__device__ __forceinline__ void load_top(const AppendParams& P, int64_t hi4,
+                                         int4 (&nd)[kTopRows]) {
 #pragma unroll
-  for (int r = 0; r < kScanUnroll; ++r) {
-    const int j = j0 + r * kThreads + static_cast<int>(threadIdx.x);
-    pr[r] = j < novf ? P.ovf[j] : make_int2(-1, 0);
+  for (int r = 0; r < kTopRows; ++r) {
+    const int64_t q = hi4 / 4 - 1 - (static_cast<int64_t>(r) * kThreads + threadIdx.x);
+    nd[r] = q >= 0 ? reinterpret_cast<const int4*>(P.ticket)[q] : make_int4(-1, -1, -1, -1);
   }
 }
 
-// One large group (c > kListCap) by the whole workgroup.  Its entries (the node
-// list and its overflow pairs) are marked in an LDS bitmap of the whole batch
-// (bit i for entry i); thread t owns words [kWordsPerThread t, +kWordsPerThread)
-// and takes the set bits of its words from the highest, so R[e] is the entry
-// with e later entries of the node.  The first overflow chunk is loaded before
-// the node's own values, so both round trips overlap.
+// LDS of the top-down ranking: per row r, bit k of every lane's match count in
+// a ballot per wavefront
+struct TopLds {
+  uint64_t cb[kTopRows][3][kCommitWaves];
+};
+static_assert(kTopRows * kCommitWaves <= kWave, "one lane per (row, wavefront) count");
+
+// One large group (c > kListCap) by the whole workgroup.  Its kept entries are
+// its last kept = min(c, B) in the batch: the plan's node array is read from the
+// top down, kTopChunk entries per step, and the entry with e later entries of
+// node u is ranked from the match counts (matches in earlier steps, earlier
+// rows, lower wavefronts, lower lanes, and this lane's higher entries; every
+// wavefront scans the (row, wavefront) counts itself).  The first step (nd) is loaded by the
+// caller before u is known.  Steps end once B entries are found (kept = B) or
+// the batch is exhausted (kept = c), so the node's counter is not read.
 template <int VEC>
-__device__ __forceinline__ void fast_large(const AppendParams& P, const int32_t* u_at, int novf,
-                                           uint32_t* bitmap, int32_t* R, int32_t* wsum) {
+__device__ __forceinline__ void fast_large(const AppendParams& P, int64_t u, int4 (&nd)[kTopRows],
+                                           int32_t* R, TopLds& T) {
   const int wv = threadIdx.x / kWave;
   const int lane = threadIdx.x & (kWave - 1);
   const int t = threadIdx.x;
-  int2 pr[kScanUnroll];
-  load_pairs(P, 0, novf, pr);
-  const int64_t u = *u_at;
-  const int c = P.cnt[u];
+  const uint64_t below = (uint64_t(1) << lane) - 1;
   const int64_t w = P.wp[u];
-  const int32_t first = t < kListCap ? P.lst[u * kListCap + t] : -1;
-  const int kept = c < P.B ? c : P.B;
+  const int32_t u32 = static_cast<int32_t>(u);
+  int carry = 0;
+  for (int64_t hi4 = (P.n + 3) & ~int64_t(3);;) {  // workgroup-uniform
+    // m4[r] bit s: entry 4q + 3 - s of row r is node u (s = 0 is the highest)
+    uint32_t m4[kTopRows];
 #pragma unroll
-  for (int q = 0; q < kWordsPerThread; ++q) bitmap[t * kWordsPerThread + q] = 0u;
-  __syncthreads();
-  if (first >= 0) atomicOr(&bitmap[first >> 5], 1u << (first & 31));
-  for (int j0 = 0;;) {
+    for (int r = 0; r < kTopRows; ++r) {
+      const int64_t top = hi4 - 4 * (static_cast<int64_t>(r) * kThreads + t) - 1;  // 4q + 3
+      uint32_t m = 0;
+      // entries n .. hi4 - 1 (at most 3) hold stale nodes; 4q < n always
+      m |= static_cast<uint32_t>(nd[r].w == u32 && top < P.n);
+      m |= static_cast<uint32_t>(nd[r].z == u32 && top - 1 < P.n) << 1;
+      m |= static_cast<uint32_t>(nd[r].y == u32 && top - 2 < P.n) << 2;
+      m |= static_cast<uint32_t>(nd[r].x == u32) << 3;
+      m4[r] = m;
+      const int cnt = __popc(m);
 #pragma unroll
-    for (int r = 0; r < kScanUnroll; ++r)
-      if (pr[r].x == u) atomicOr(&bitmap[pr[r].y >> 5], 1u << (pr[r].y & 31));
-    j0 += kScanUnroll * kThreads;
-    if (j0 >= novf) break;
-    load_pairs(P, j0, novf, pr);
-  }
-  __syncthreads();
-  // set bits in later words: own words, wave suffix scan, later waves' totals
-  int own = 0;
-#pragma unroll
-  for (int q = 0; q < kWordsPerThread; ++q) own += __popc(bitmap[t * kWordsPerThread + q]);
-  int suf = own;
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const int y = __shfl_down(suf, off, kWave);
-    if (lane + off < kWave) suf += y;
-  }
-  if (lane == 0) wsum[wv] = suf;
-  __syncthreads();
-  int k = suf - own;
-  for (int w2 = wv + 1; w2 < kCommitWaves; ++w2) k += wsum[w2];
-  for (int q = kWordsPerThread - 1; q >= 0 && k < kept; --q) {
-    uint32_t word = bitmap[t * kWordsPerThread + q];
-    while (word != 0u && k < kept) {
-      const int bit = 31 - __clz(static_cast<int>(word));
-      R[k++] = (t * kWordsPerThread + q) * 32 + bit;
-      word &= ~(1u << bit);
+      for (int k = 0; k < 3; ++k) {
+        const uint64_t bl = __ballot((cnt >> k) & 1);
+        if (lane == 0) T.cb[r][k][wv] = bl;
+      }
     }
+    __syncthreads();
+    // lane l < kTopRows kCommitWaves: the count of (row l / kCommitWaves,
+    // wavefront l % kCommitWaves); an exclusive scan in that order gives bases
+    int x = 0;
+    if (lane < kTopRows * kCommitWaves) {
+#pragma unroll
+      for (int k = 0; k < 3; ++k) x += __popcll(T.cb[lane / kCommitWaves][k][lane % kCommitWaves]) << k;
+    }
+    int incl = x;
+#pragma unroll
+    for (int off = 1; off < kTopRows * kCommitWaves; off <<= 1) {
+      const int y = __shfl_up(incl, off, kWave);
+      if (lane >= off) incl += y;
+    }
+    const int step_total = __shfl(incl, kTopRows * kCommitWaves - 1, kWave);
+#pragma unroll
+    for (int r = 0; r < kTopRows; ++r) {
+      const int base = carry + __shfl(incl - x, r * kCommitWaves + wv, kWave);
+      uint32_t m = m4[r];
+      if (m == 0u) continue;
+      int e = base;
+#pragma unroll
+      for (int k = 0; k < 3; ++k) e += __popcll(T.cb[r][k][wv] & below) << k;
+      const int64_t top = hi4 - 4 * (static_cast<int64_t>(r) * kThreads + t) - 1;
+      for (; m != 0u; m &= m - 1, ++e) {
+        const int s = __builtin_ctz(m);
+        if (e < P.B) R[e] = static_cast<int32_t>(top - s);
+      }
+    }
+    carry += step_total;
+    hi4 -= kTopChunk;
+    __syncthreads();  // T is rewritten by the next step; R is complete at the end
+    if (carry >= P.B || hi4 <= 0) break;
+    load_top(P, hi4, nd);
   }
-  __syncthreads();
+  const int kept = carry < P.B ? carry : P.B;
   write_kept<VEC>(P, R, u, kept, w, t, kThreads);
   if (t == 0) {
     P.wp[u] = w + kept;
     P.cnt[u] = 0;
   }
-  __syncthreads();  // the next group rewrites R and the bitmap
+  __syncthreads();  // the next group rewrites R
 }
 
 // blocks [0, ga): singletons; [ga, ga+gb): groups of c <= kListCap, one per
 // wavefront; [ga+gb, ...): larger groups, one per workgroup
 template <int VEC>
 __global__ __launch_bounds__(kThreads) void fast_commit(AppendParams P) {
-  __shared__ uint32_t bitmap[kFastWords];
   __shared__ int32_t rows[kCommitWaves][TGX_MAX_SLOTS];
-  __shared__ int32_t wsum[kCommitWaves];
+  __shared__ TopLds top;
   const int blk = static_cast<int>(blockIdx.x);
   const int wv = threadIdx.x / kWave;
   const int lane = threadIdx.x & (kWave - 1);
-  const int ph = P.ctl[kCtlPhaseCur] & 1;  // the cursor set of this batch's plan
+  // ctl words 8-15 in one round trip: both cursor sets, phase_next, phase_cur
+  // (this launch writes only the other set and phase_next, which it does not use)
+  const u32x4 c0 = *reinterpret_cast<const u32x4*>(P.ctl + kCtlFCursor);
+  const u32x4 c1 = *reinterpret_cast<const u32x4*>(P.ctl + kCtlFCursor + 4);
+  const int ph = static_cast<int>(c1[kCtlPhaseCur - kCtlFCursor - 4]) & 1;
+  const uint64_t cur = ph == 0 ? (static_cast<uint64_t>(c0[1]) << 32 | c0[0])
+                               : (static_cast<uint64_t>(c0[3]) << 32 | c0[2]);
   if (blk == 0 && threadIdx.x == 0) {
+    // both diagnostics pairs (words 16-19) in the same round trip as the cursors
+    const u32x4 dg = *reinterpret_cast<const u32x4*>(P.ctl + kCtlFDiag);
+    const int time_flag = static_cast<int>(ph == 0 ? dg[0] : dg[2]);
+    const int bad = static_cast<int>(ph == 0 ? dg[1] : dg[3]);
     // the other set belongs to a committed plan: clear it for the next plan
     *reinterpret_cast<uint64_t*>(P.ctl + kCtlFCursor + 2 * (1 - ph)) = 0;
     P.ctl[kCtlPhaseNext] = 1 - ph;
-    commit_diagnostics(P, kCtlFDiag + 2 * ph, kCtlFDiag + 2 * ph + 1);
+    if (P.status != nullptr) {
+      if (bad != 0) atomicAdd(&P.status[TGX_ST_BAD_EVENT_NODE], bad);
+      if (time_flag == 0) atomicAdd(&P.status[TGX_ST_KEY_COLLISION], 1);
+    }
+    P.ctl[kCtlFDiag + 2 * ph] = 0;
+    P.ctl[kCtlFDiag + 2 * ph + 1] = 0;
   }
   if (blk < P.ga) {
     commit_singletons<VEC>(P, blk);
+  } else if (blk < P.ga + P.gb) {
+    // the first group id of this wavefront is read with the cursor (in bounds of
+    // the n/2 + 1 list), so a group costs three round trips
+    const int ngroups = field(cur, kFGroups);
+    const int gstride = P.gb * kCommitWaves;
+    int gid = (blk - P.ga) * kCommitWaves + wv;
+    int64_t u = gid <= P.n / 2 ? P.groups[gid] : 0;
+    for (; gid < ngroups; gid += gstride) {  // wave-uniform
+      const int c = P.cnt[u];
+      const int64_t w = P.wp[u];
+      const int32_t idx = lane < kListCap ? P.lst[u * kListCap + lane] : -1;
+      const int64_t u_next = gid + gstride < ngroups ? P.groups[gid + gstride] : 0;
+      // a larger group has its own role; its counter reads c > kListCap, or 0
+      // once that role restored it
+      if (c >= 2 && c <= kListCap) commit_small<VEC>(P, u, c, lane < c ? idx : -1, w, rows[wv]);
+      u = u_next;
+    }
   } else {
-    const uint64_t cur = *reinterpret_cast<const uint64_t*>(P.ctl + kCtlFCursor + 2 * ph);
-    if (blk < P.ga + P.gb) {
-      const int ngroups = field(cur, kFGroups);
-      for (int gid = (blk - P.ga) * kCommitWaves + wv; gid < ngroups;
-           gid += P.gb * kCommitWaves) {  // wave-uniform
-        const int64_t u = P.groups[gid];
-        const int c = P.cnt[u];
-        const int64_t w = P.wp[u];
-        const int32_t idx = lane < kListCap ? P.lst[u * kListCap + lane] : -1;
-        // a larger group has its own role; its counter reads c > kListCap, or 0
-        // once that role restored it
-        if (c < 2 || c > kListCap) continue;
-        commit_small<VEC>(P, u, c, lane < c ? idx : -1, w, rows[wv]);
+    // the group's node and the top of the batch are read with the cursor
+    // (gid < n / (kListCap + 1) + 1, the large list's length)
+    const int nlarge = field(cur, kFLarge);
+    const int gstride = static_cast<int>(gridDim.x) - P.ga - P.gb;
+    const int64_t hi4 = (P.n + 3) & ~int64_t(3);
+    int gid = blk - P.ga - P.gb;
+    int64_t u = P.large[gid];
+    int4 nd[kTopRows];
+    load_top(P, hi4, nd);
+    for (; gid < nlarge; gid += gstride) {  // workgroup-uniform
+      fast_large<VEC>(P, u, nd, rows[0], top);
+      if (gid + gstride < nlarge) {
+        u = P.large[gid + gstride];
+        load_top(P, hi4, nd);
       }
-    } else {
-      const int nlarge = field(cur, kFLarge);
-      const int novf = field(cur, kFOvf);
-      const int gstride = static_cast<int>(gridDim.x) - P.ga - P.gb;
-      for (int gid = blk - P.ga - P.gb; gid < nlarge; gid += gstride)  // workgroup-uniform
-        fast_large<VEC>(P, P.large + gid, novf, bitmap, rows[0], wsum);
     }
   }
 }
@@ -515,8 +582,8 @@ using namespace tgx;
 extern "C" size_t tgx_ring_append_workspace_size(int64_t b) {
   if (b <= 0) return 256;
   const size_t n = static_cast<size_t>(2 * b);
-  // ticket | overflow pairs (four-launch: list) | groups | large
-  return align256(n * 4) + align256(n * 8) + align256((n / 2 + 1) * 4) +
+  // ticket | four-launch lists | groups | large
+  return align256(n * 4) + align256(n * 4) + align256((n / 2 + 1) * 4) +
          align256((n / (kListCap + 1) + 1) * 4);
 }
 
@@ -544,6 +611,8 @@ int plan_setup(const char* who, const tgx_ring* ring, const int64_t* src, const 
   const size_t need = tgx_ring_append_workspace_size(b);
   if (workspace == nullptr || workspace_bytes < need)
     return fail(TGX_ERR_ARG, "%s: workspace of %zu bytes needed, got %zu", who, need, workspace_bytes);
+  if (!aligned16(workspace))
+    return fail(TGX_ERR_ARG, "%s: workspace must be 16-byte aligned", who);
   P.src = src;
   P.dst = dst;
   P.time = time;
@@ -554,10 +623,10 @@ int plan_setup(const char* who, const tgx_ring* ring, const int64_t* src, const 
   P.lst = ring->scratch + ring->num_nodes;
   P.ctl = ring->scratch + ctl_offset(ring->num_nodes);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
-  const size_t o_ovf = align256(static_cast<size_t>(n) * 4);
-  const size_t o_groups = o_ovf + align256(static_cast<size_t>(n) * 8);
+  const size_t o_list = align256(static_cast<size_t>(n) * 4);
+  const size_t o_groups = o_list + align256(static_cast<size_t>(n) * 4);
   P.ticket = reinterpret_cast<int32_t*>(ws);
-  P.ovf = reinterpret_cast<int2*>(ws + o_ovf);
+  P.list = reinterpret_cast<int32_t*>(ws + o_list);
   P.groups = reinterpret_cast<int32_t*>(ws + o_groups);
   P.large = reinterpret_cast<int32_t*>(ws + o_groups + align256(static_cast<size_t>(n / 2 + 1) * 4));
   return TGX_OK;
@@ -573,7 +642,6 @@ int launch_plan(const PlanParams& P, hipStream_t stream) {
   AppendParams A{};
   static_cast<PlanParams&>(A) = P;
   A.nbase = P.lst;
-  A.list = reinterpret_cast<int32_t*>(P.ovf);
   hipLaunchKernelGGL(append_count, grid1, dim3(kThreads), 0, stream, static_cast<const PlanParams&>(A));
   int rc = check_launch("append_count");
   if (rc) return rc;
@@ -611,7 +679,6 @@ int setup_append(const char* who, const tgx_ring* ring, const int64_t* src, cons
   P.wp = ring->write_pos;
   P.eids = ring->eids;
   P.nbase = P.lst;
-  P.list = reinterpret_cast<int32_t*>(P.ovf);
   P.status = status;
 
   vec = 2;

@@ -22,9 +22,9 @@ constexpr int kPlanHash = 1 << kPlanHashBits;
 static_assert(kPlanHash >= 2 * kPlanMaxThreads, "hash table at most half full");
 
 // ctl words (ring scratch).  Four-launch: cursors and diagnostics (words 0-4).
-// Two-launch: two cursor sets (uint64 at words 8 and 10: overflow | groups |
-// large counts) and two diagnostics pairs (time flag, bad count at 16 + 2p),
-// used by alternate plans.  A plan takes set p = phase_next and records it in
+// Two-launch: two cursor sets (uint64 at words 8 and 10: groups | large counts)
+// and two diagnostics pairs (time flag, bad count at 16 + 2p), used by alternate
+// plans.  A plan takes set p = phase_next and records it in
 // phase_cur; its commit reads set phase_cur, and its workgroup 0 clears the other
 // set (its plan is committed), reports and clears this plan's diagnostics and
 // sets phase_next to the other set, so nothing waits for the last workgroup.
@@ -38,7 +38,7 @@ constexpr int kCtlWords = 32;
 // fields of the two-launch cursor word (every count is at most n <= 2^15)
 constexpr int kFieldBits = 21;
 constexpr uint64_t kFieldMask = (uint64_t(1) << kFieldBits) - 1;
-enum { kFOvf = 0, kFGroups = 1, kFLarge = 2 };
+enum { kFGroups = 0, kFLarge = 1 };
 __host__ __device__ constexpr int field(uint64_t x, int f) {
   return static_cast<int>((x >> (f * kFieldBits)) & kFieldMask);
 }
@@ -58,8 +58,8 @@ struct PlanParams {
   int32_t* cnt;    // [N] per-node counters (zero between calls)
   int32_t* lst;    // [N, kListCap] node lists
   int32_t* ctl;    // [kCtlWords]
-  int32_t* ticket; // [n] four-launch tickets
-  int2* ovf;       // [n] two-launch overflow (node, entry) pairs
+  int32_t* ticket; // [n] four-launch tickets; two-launch: node of every entry (-1: bad)
+  int32_t* list;   // [n] four-launch lists
   int32_t* groups; // [n/2 + 1] groups
   int32_t* large;  // [n/(kListCap+1) + 1] large groups
 };
@@ -134,10 +134,11 @@ __device__ __forceinline__ void report_diagnostics(const PlanParams& P, int bad,
 // Two-launch plan of entries [block * blockDim.x, +blockDim.x) (blockDim.x a
 // multiple of kWave, at most kPlanMaxThreads; every thread of the workgroup
 // calls it), into cursor set phase_next.  Ticket t < kListCap stores the entry
-// in lst[u][t]; later tickets append (u, i) to the overflow array; the ticket-1
-// entry appends u to the group list, the ticket-kListCap entry to the
-// large-group list.  The three wave counts are packed in one word: a workgroup
-// prefix in LDS, then one cursor atomic per workgroup.
+// in lst[u][t]; the ticket-1 entry appends u to the group list, the
+// ticket-kListCap entry to the large-group list.  Every entry's node goes to
+// ticket[i] as int32, where the commit of a large group finds the node's
+// entries.  The two wave counts are packed in one word: a workgroup prefix in
+// LDS, then one cursor atomic per workgroup.
 __device__ __forceinline__ void plan_block(const PlanParams& P, int64_t block, PlanLds& L) {
   const int64_t i = block * blockDim.x + threadIdx.x;
   const int wv = threadIdx.x / kWave;
@@ -150,13 +151,12 @@ __device__ __forceinline__ void plan_block(const PlanParams& P, int64_t block, P
   bool time_ok;
   const int32_t u = entry_prologue(P, i, bad, time_ok);
   const int32_t t = node_ticket(P, u, L);
+  if (i < P.n) P.ticket[i] = u;
   if (t >= 0 && t < kListCap) P.lst[static_cast<int64_t>(u) * kListCap + t] = static_cast<int32_t>(i);
-  const uint64_t om = __ballot(t >= kListCap);
   const uint64_t gm = __ballot(t == 1);
   const uint64_t lm = __ballot(t == kListCap);
   if (lane == 0)
-    L.wofs[wv] = static_cast<uint64_t>(__popcll(om)) |
-                 (static_cast<uint64_t>(__popcll(gm)) << (kFGroups * kFieldBits)) |
+    L.wofs[wv] = (static_cast<uint64_t>(__popcll(gm)) << (kFGroups * kFieldBits)) |
                  (static_cast<uint64_t>(__popcll(lm)) << (kFLarge * kFieldBits));
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -175,8 +175,6 @@ __device__ __forceinline__ void plan_block(const PlanParams& P, int64_t block, P
   __syncthreads();
   const uint64_t below = (uint64_t(1) << lane) - 1;
   const uint64_t at = L.wofs[kPlanMaxWaves] + L.wofs[wv];
-  if (t >= kListCap)
-    P.ovf[field(at, kFOvf) + __popcll(om & below)] = make_int2(u, static_cast<int32_t>(i));
   if (t == 1) P.groups[field(at, kFGroups) + __popcll(gm & below)] = u;
   if (t == kListCap) P.large[field(at, kFLarge) + __popcll(lm & below)] = u;
   report_diagnostics(P, bad, time_ok, kCtlFDiag + 2 * ph, kCtlFDiag + 2 * ph + 1);
