@@ -159,6 +159,31 @@ def test_ring_two_and_four_launch_size_boundary(b):
     _run(9, 20_000, 32, 8, True, _windows_gen(b, 2))
 
 
+def test_ring_odd_batch_masks_stale_entry_nodes():
+    """n = 2b with b odd: the commit reads the plan's entry-node array in 16-byte
+    groups from the top, so its first read covers two entries past the batch,
+    left there by the previous, larger batch.  Node 7 sits at exactly those two
+    positions (entries 1998 and 1999 of a 1001-event batch) and is a large group
+    of the next 999-event batches: with fewer entries than B (every entry kept)
+    and with more (only the top B)."""
+    def gen(rng):
+        src = rng.integers(100, 5000, 1001)
+        dst = rng.integers(100, 5000, 1001)
+        dst[997:999] = 7  # entries 1001 + 997 and 1001 + 998
+        src[::50] = 7
+        yield src, dst
+        for step in (40, 9):  # 25 entries of node 7 (< B), then 111 (> B)
+            src = rng.integers(100, 5000, 999)
+            dst = rng.integers(100, 5000, 999)
+            src[::step] = 7
+            yield src, dst
+            src = rng.integers(100, 5000, 1001)  # refill the stale positions
+            dst = rng.integers(100, 5000, 1001)
+            dst[997:999] = 7
+            yield src, dst
+    _run(11, 5000, 32, 8, False, gen)
+
+
 def test_ring_list_capacity_edges():
     """Groups of exactly 7, 8, 9 and 10 entries (a full node list, and the first
     overflow entries) next to singletons, for B below and above the group size."""
