@@ -111,6 +111,8 @@ struct Params {
   int off_cid, off_code, off_pcode, off_pdt, off_pid, off_pt, off_pe, off_tab;
   // work decomposition: m queries per wavefront in sub-groups of 2^lg_bp lanes
   int m, lg_bp;
+  // FastDiv multipliers of K, d_t / 4, d_t and nch
+  uint32_t fd_k, fd_q, fd_d, fd_c;
   int split;  // wavefronts per query (m == 1): each writes every split-th output chunk
   // fused ring plan: workgroups [0, plan_blocks) plan the caller's next batch
   PlanParams pl;
@@ -188,7 +190,12 @@ constexpr int kCopyDepth = 4;
 
 struct FastDiv {
   uint32_t n, m;
-  __device__ explicit FastDiv(uint32_t n_) : n(n_), m(n_ > 1 ? 0xffffffffu / n_ + 1u : 0u) {}
+  // the multiplier of divisor n (computed on the host: a division is tens of
+  // VALU instructions on the device)
+  __host__ __device__ static constexpr uint32_t magic(uint32_t n) {
+    return n > 1 ? 0xffffffffu / n + 1u : 0u;
+  }
+  __device__ FastDiv(uint32_t n_, uint32_t m_) : n(n_), m(m_) {}
   __device__ __forceinline__ uint32_t div(uint32_t x) const { return n > 1 ? __umulhi(x, m) : x; }
 };
 
@@ -272,7 +279,7 @@ __device__ __forceinline__ void encode_rows(const Params& P, int64_t r0, int np,
   if (P.te_vec4) {
     const int nq = d_t / 4;
     const int total = np * nq;
-    const FastDiv dq(nq);
+    const FastDiv dq(nq, P.fd_q);
     const f32x4* w4 = reinterpret_cast<const f32x4*>(s_w);
     const f32x4* b4 = reinterpret_cast<const f32x4*>(s_b);
     f32x4* o4 = reinterpret_cast<f32x4*>(P.o_te) + r0 * nq;
@@ -290,7 +297,7 @@ __device__ __forceinline__ void encode_rows(const Params& P, int64_t r0, int np,
     }
   } else {
     const int total = np * d_t;
-    const FastDiv dd(d_t);
+    const FastDiv dd(d_t, P.fd_d);
     float* out = P.o_te + r0 * d_t;
     for (int idx = start; idx < total; idx += stride) {
       const int gp = static_cast<int>(dd.div(idx));
@@ -600,7 +607,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) __attribute__((amdgpu_waves_per_
   if (q0 < 0) nvalid = 0;
   const int np = nvalid * K;
   const int64_t r0 = q0 * K;
-  const FastDiv dk(K);
+  const FastDiv dk(K, P.fd_k);
   const int ostart = part * kWave + lane;  // this wave's share of the output chunks
   const int ostride = split * kWave;
 
@@ -633,7 +640,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) __attribute__((amdgpu_waves_per_
   if (P.o_feats != nullptr && P.row_bytes > 0) {
     const int nch = P.nch;
     const int total = np * nch;
-    const FastDiv dv(nch);
+    const FastDiv dv(nch, P.fd_c);
     VT* of = reinterpret_cast<VT*>(P.o_feats) + r0 * nch;
     if constexpr (NREG > 0) {
       // ring rows come from the lanes that loaded them, CSR rows from memory;
@@ -999,6 +1006,10 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
   else if (P.row_bytes % 4 == 0 && (!fe || (al(P.r_feats, 3) && al(P.c_feats, 3) && al(P.o_feats, 3))))
     vec = 4;
   P.nch = static_cast<int>(P.row_bytes / vec);
+  P.fd_k = FastDiv::magic(static_cast<uint32_t>(P.K));
+  P.fd_q = FastDiv::magic(static_cast<uint32_t>(P.d_t / 4));
+  P.fd_d = FastDiv::magic(static_cast<uint32_t>(P.d_t));
+  P.fd_c = FastDiv::magic(static_cast<uint32_t>(P.nch));
   // rows of at most 4 16-byte chunks ride in registers with the ring slot
   int nreg = 0;
   if (vec == 16 && fe && P.B > 0) nreg = P.nch <= 2 ? 2 : (P.nch <= 4 ? 4 : 0);
