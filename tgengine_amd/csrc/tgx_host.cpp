@@ -31,6 +31,17 @@ int64_t ptr(const c10::optional<at::Tensor>& t) {
 // 1-D view of t (t itself when it already is 1-D)
 at::Tensor flat(const at::Tensor& t) { return t.dim() == 1 ? t : t.reshape({-1}); }
 
+// a contiguous `st` tensor of shape `sizes` at byte offset `byte_off` of base's
+// storage (a multiple of the element size), built directly like split_rows' blocks
+at::Tensor typed_block(const at::Tensor& base, at::ScalarType st, int64_t byte_off,
+                       at::IntArrayRef sizes) {
+  const caffe2::TypeMeta dt = c10::scalarTypeToTypeMeta(st);
+  auto impl = c10::make_intrusive<c10::TensorImpl>(c10::Storage(base.storage()), base.key_set(), dt);
+  impl->set_sizes_contiguous(sizes);
+  impl->set_storage_offset(byte_off / static_cast<int64_t>(dt.itemsize()));
+  return at::Tensor(std::move(impl));
+}
+
 // x split along dim 0 into consecutive blocks of sizes[g] rows: tensors built
 // directly on x's storage (no dispatcher round trip per block, about four times
 // cheaper than split_with_sizes; the blocks are plain tensors sharing x's
@@ -106,19 +117,30 @@ std::vector<std::vector<at::Tensor>> recent(
     Q += sizes[g];
   }
   if (num_groups < 0) num_groups = (Q + group - 1) / group;
-  auto o32 = at::TensorOptions().device(dev).dtype(at::kInt);
-  at::Tensor ids = at::empty({Q, k}, o32);
-  at::Tensor tms = at::empty({Q, k}, at::TensorOptions().device(dev).dtype(at::kDouble));
+  // The small outputs (times, edge ids, ids, co-occurrence, mask) share one
+  // allocation, laid out so every offset is a multiple of its element size; the
+  // feature rows and encodings, which dominate the bytes, get their own.
+  const int64_t QK = Q * k;
+  const int64_t L = co_mode == TGX_CO_FREQ ? k : k + 1;
+  const int64_t nco = co_mode != TGX_CO_NONE ? num_groups * L * 2 : 0;
+  const int64_t o_eids = QK * 8;
+  const int64_t o_ids = o_eids + (want_eids ? QK * 8 : 0);
+  const int64_t o_coa = o_ids + QK * 4;
+  const int64_t o_coc = o_coa + nco * 4;
+  const int64_t o_cop = o_coc + nco * 4;
+  const int64_t o_msk = o_cop + (co_mode != TGX_CO_NONE ? num_groups * 4 : 0);
+  at::Tensor small = at::empty({o_msk + QK}, at::TensorOptions().device(dev).dtype(at::kByte));
+  at::Tensor tms = typed_block(small, at::kDouble, 0, {Q, k});
+  at::Tensor ids = typed_block(small, at::kInt, o_ids, {Q, k});
+  at::Tensor msk = typed_block(small, at::kBool, o_msk, {Q, k});
   at::Tensor fts = at::empty({Q, k, feat_dim}, at::TensorOptions().device(dev).dtype(feat_dtype));
-  at::Tensor msk = at::empty({Q, k}, at::TensorOptions().device(dev).dtype(at::kBool));
   c10::optional<at::Tensor> eids, te, co_a, co_c, co_pair;
-  if (want_eids) eids = at::empty({Q, k}, at::TensorOptions().device(dev).dtype(at::kLong));
+  if (want_eids) eids = typed_block(small, at::kLong, o_eids, {Q, k});
   if (d_t > 0) te = at::empty({Q, k, d_t}, at::TensorOptions().device(dev).dtype(at::kFloat));
   if (co_mode != TGX_CO_NONE) {
-    const int64_t L = co_mode == TGX_CO_FREQ ? k : k + 1;
-    co_a = at::empty({num_groups, L, 2}, o32);
-    co_c = at::empty({num_groups, L, 2}, o32);
-    co_pair = at::empty({num_groups}, at::TensorOptions().device(dev).dtype(at::kFloat));
+    co_a = typed_block(small, at::kInt, o_coa, {num_groups, L, 2});
+    co_c = typed_block(small, at::kInt, o_coc, {num_groups, L, 2});
+    co_pair = typed_block(small, at::kFloat, o_cop, {num_groups});
   }
   tgx_recent_args a{};
   a.num_queries = Q;
