@@ -83,6 +83,24 @@ class DataPipeline:
             self._te[d_t] = t
         return t, None
 
+    def _event_plan(self, b: int, per_event: list) -> tuple:
+        """(plan, queries per event) of the event-major grouping [src p, dst p, its
+        negatives, neg_src p] of a batch of b events, cached per shape."""
+        key = (b, *per_event)
+        hit = self._plans.get(key)
+        if hit is not None:
+            return hit
+        offs, off = [], 0
+        for per in per_event:
+            offs.append((off, per))
+            off += b * per
+        G = sum(per_event)
+        if G > _lib.TGX_MAX_GROUP:
+            raise ValueError(f"{G} queries per event exceed the fused group limit {_lib.TGX_MAX_GROUP}")
+        hit = (self._plan(("ev", b, tuple(per_event)), b, offs), G)
+        self._plans[key] = hit
+        return hit
+
     def _plan(self, key, b: int, groups: list) -> Tensor:
         t = self._plans.get(key)
         if t is None:
@@ -232,15 +250,9 @@ class DataPipeline:
         k = spec.neighbors.k
         b = src.shape[0]
         if co_mode != _lib.TGX_CO_NONE:
-            offs, off = [], 0
-            for per in per_event:  # event-major groups: [src p, dst p, its negatives, neg_src p]
-                offs.append((off, per))
-                off += b * per
-            G = sum(per_event)
-            if G > _lib.TGX_MAX_GROUP:
-                raise ValueError(f"{G} queries per event exceed the fused group limit {_lib.TGX_MAX_GROUP}")
-            res = g._gather(qgroups, k, self._plan(("ev", b, tuple(per_event)), b, offs), G, b, d_t,
-                            te_w, te_b, _DT_MODES[spec.dt_mode], co_mode, spec.edge_ids, append)
+            plan, G = self._event_plan(b, per_event)
+            res = g._gather(qgroups, k, plan, G, b, d_t, te_w, te_b, _DT_MODES[spec.dt_mode],
+                            co_mode, spec.edge_ids, append)
         else:
             res = g._gather(qgroups, k, None, self.queries_per_workgroup, None, d_t, te_w, te_b,
                             _DT_MODES[spec.dt_mode], co_mode, spec.edge_ids, append)
