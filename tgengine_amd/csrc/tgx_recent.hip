@@ -403,7 +403,10 @@ __device__ __forceinline__ void co_occurrence_pair(const Params& P, int64_t g, i
 // stores would wait for their completion.  With at most one wave per SIMD slot
 // for the whole grid the gathers all run up front and the stores then stream.
 template <int VEC, int NREG>
-__global__ __launch_bounds__(kMaxWaves * kWave) __attribute__((amdgpu_waves_per_eu(8))) void recent_fused(Params P) {
+// (No waves-per-SIMD target: forcing 8 capped the scalar registers and spilled
+// them into the gather's own code; at the 7 the registers allow, C3's grid still
+// fits at once.)
+__global__ __launch_bounds__(kMaxWaves * kWave) void recent_fused(Params P) {
   using VT = typename Vec<VEC>::T;
   extern __shared__ __align__(16) uint8_t smem[];
   const int lane = threadIdx.x & (kWave - 1);
