@@ -402,11 +402,16 @@ __device__ __forceinline__ void co_occurrence_pair(const Params& P, int64_t g, i
 // gfx9 counts vector loads and stores in one in-order vmcnt, so a load behind
 // stores would wait for their completion.  With at most one wave per SIMD slot
 // for the whole grid the gathers all run up front and the stores then stream.
+// Waves-per-SIMD target: 8 for the large-row kernels, whose bandwidth needs every
+// resident wave (plan-group workgroups of 6 waves fit 5 per CU at 8, 4 at 7); none
+// for the small-row kernel, where forcing 8 capped the scalar registers and spilled
+// them into its own code, while the 7 the registers allow still hold its grid.
+template <int NREG>
+constexpr int kWavesPerEu = NREG > 0 ? 1 : 8;
+
 template <int VEC, int NREG>
-// (No waves-per-SIMD target: forcing 8 capped the scalar registers and spilled
-// them into the gather's own code; at the 7 the registers allow, C3's grid still
-// fits at once.)
-__global__ __launch_bounds__(kMaxWaves * kWave) void recent_fused(Params P) {
+__global__ __launch_bounds__(kMaxWaves * kWave) __attribute__((amdgpu_waves_per_eu(kWavesPerEu<NREG>)))
+void recent_fused(Params P) {
   using VT = typename Vec<VEC>::T;
   extern __shared__ __align__(16) uint8_t smem[];
   const int lane = threadIdx.x & (kWave - 1);
