@@ -228,9 +228,19 @@ class TemporalGraph:
                                    f"got {self.feat_dtype} for the ring and {edge_feat.dtype} for edge_feat")
         return _as(edge_feat, self.feat_dtype, self.device)
 
+    def _grown(self, old: Optional[Tensor], nbytes: int) -> Tensor:
+        """A workspace of at least nbytes.  Launches on several streams (the
+        prefetch stream's plan, the caller's commit) may still read the one it
+        replaces, so the device drains before that is released; workspaces only
+        grow, so this happens a few times per graph at most."""
+        if old is not None and old.numel() >= nbytes:
+            return old
+        if old is not None:
+            torch.cuda.synchronize(self.device)
+        return torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=self.device)
+
     def _workspace(self, nbytes: int) -> Tensor:
-        if self._ws is None or self._ws.numel() < nbytes:
-            self._ws = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=self.device)
+        self._ws = self._grown(self._ws, nbytes)
         return self._ws
 
     # ------------------------------------------------------------------ planned updates
@@ -246,9 +256,7 @@ class TemporalGraph:
                 and all(t.device == self.device and t.is_contiguous() for t in (src, dst, time)))
 
     def _plan_workspace(self, b: int) -> Tensor:
-        need = _ws_size(b)
-        if self._plan_ws is None or self._plan_ws.numel() < need:
-            self._plan_ws = torch.empty(max(need, 1 << 16), dtype=torch.uint8, device=self.device)
+        self._plan_ws = self._grown(self._plan_ws, _ws_size(b))
         return self._plan_ws
 
     def _order_after(self, stream: int) -> int:
