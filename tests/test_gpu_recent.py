@@ -7,6 +7,8 @@ mode, edge ids, negatives of shape (b, n), neg_src, 2-hop queries, and the
 restated known-answer tests of the reference suite (tests/test_core.py,
 tests/test_triton_kernel.py, tests/test_cuda_kernels.py, tests/test_negatives.py).
 """
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -67,6 +69,23 @@ def test_core_snapshot_restore():
     g.restore(snap)
     assert g.num_edges == 2
     assert torch.equal(g._ov_ids, ids0)
+
+
+def test_snapshot_restore_keeps_edge_ids():
+    g = TemporalGraph(5, buffer_size=4, edge_feat_dim=2, device="cuda", track_edge_ids=True)
+    g.freeze_csr()
+    g.advance(cu([0, 1]), cu([1, 2]), cu([1.0, 2.0], torch.float64), torch.randn(2, 2).cuda())
+    snap = g.snapshot()
+    eids0 = g._ov_eids.clone()
+    g.advance(cu([1]), cu([0]), cu([3.0], torch.float64), torch.randn(1, 2).cuda())
+    assert not torch.equal(g._ov_eids, eids0)
+    g.restore(snap)
+    assert torch.equal(g._ov_eids, eids0)
+    # a snapshot without edge ids (the reference's four ring arrays) cannot restore them
+    bare = dataclasses.replace(snap, overflow_eids=None)
+    with pytest.raises(ValueError):
+        g.restore(bare)
+    assert torch.equal(g._ov_eids, eids0) and g.num_edges == 2
 
 
 def test_async_ordering_ring_known_answer():

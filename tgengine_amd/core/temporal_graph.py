@@ -543,6 +543,9 @@ class TemporalGraph:
                         None if self._ov_eids is None else self._ov_eids.clone())
 
     def restore(self, snap: Snapshot) -> None:
+        if self._ov_eids is not None and snap.overflow_eids is None:
+            raise ValueError("restore: this graph tracks edge ids and the snapshot holds none; "
+                             "its ring edge ids would no longer match the restored slots")
         self._drop_plan()
         self._ov_ids.copy_(snap.overflow_ids)
         self._ov_times.copy_(snap.overflow_times)
