@@ -138,9 +138,13 @@ def test_async_pipeline_plans_on_its_prefetch_stream():
     bts = [gen_batch(cfg, i) for i in range(6)]
     raws = [S.to_raw(cfg, bt) for bt in bts]
     for i, (bt, rb) in enumerate(zip(bts, raws)):
-        neg.queue.append(rb.neg)
-        ap.start_prefetch(RawBatch(src=rb.src, dst=rb.dst, time=rb.time, edge_feat=rb.edge_feat))
+        # odd batches are prefetched twice without a get() between: the first
+        # prefetch is joined and dropped, its plan replaced by the second's
+        for _ in range(1 + i % 2):
+            neg.queue.append(rb.neg)
+            ap.start_prefetch(RawBatch(src=rb.src, dst=rb.dst, time=rb.time, edge_feat=rb.edge_feat))
         rb2, pb = ap.get()
+        assert not neg.queue
         S.compare_prepared(cfg, pb, bt, ring if i > 0 else None, w, f"async batch {i}")
         g.advance(rb2.src, rb2.dst, rb2.time, rb2.edge_feat)
         O.ring_advance(ring, bt["src"], bt["dst"], bt["time"], bt["feat"])

@@ -13,6 +13,7 @@ there before the caller's ``advance``).
 """
 from __future__ import annotations
 
+import dataclasses
 import threading
 from typing import Optional
 
@@ -43,7 +44,11 @@ class AsyncDataPipeline:
         return self._pipeline.graph
 
     def start_prefetch(self, raw_batch: RawBatch) -> None:
-        """Prepare ``raw_batch`` on the side stream; call after ``graph.advance`` of the previous batch."""
+        """Prepare ``raw_batch`` on the side stream; call after ``graph.advance`` of the previous batch.
+        A prefetch still running (never collected by ``get``) is joined and dropped first."""
+        if self._thread is not None:
+            self._thread.join()
+            self._thread = None
         self._prefetch_stream.wait_stream(torch.cuda.current_stream(self._graph.device))
         self._result = None
         self._exc = None
@@ -80,7 +85,31 @@ class AsyncDataPipeline:
         # the caller's stream, where advance() commits it
         self._graph._adopt_plan(caller)
         result, self._result = self._result, None
+        # the batch's tensors were allocated on the side stream and are used on
+        # the caller's from here on: without this, memory the caller frees could be
+        # reused by a later prefetch while the caller's queued work still reads it
+        _record_stream(result, caller, set())
         return result
 
     def prepare(self, raw_batch: RawBatch) -> PreparedBatch:
         return self._pipeline.prepare(raw_batch)
+
+
+def _record_stream(obj, stream, seen: set) -> None:
+    """record_stream(stream) on every device tensor inside obj (tensors, lists,
+    tuples, dicts and dataclass instances such as PreparedBatch / NeighborData)."""
+    if obj is None or id(obj) in seen:
+        return
+    seen.add(id(obj))
+    if isinstance(obj, torch.Tensor):
+        if obj.is_cuda:
+            obj.record_stream(stream)
+    elif isinstance(obj, (list, tuple)):
+        for x in obj:
+            _record_stream(x, stream, seen)
+    elif isinstance(obj, dict):
+        for x in obj.values():
+            _record_stream(x, stream, seen)
+    elif dataclasses.is_dataclass(obj) and not isinstance(obj, type):
+        for f in dataclasses.fields(obj):
+            _record_stream(getattr(obj, f.name), stream, seen)
