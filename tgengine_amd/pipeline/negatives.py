@@ -65,6 +65,9 @@ class HistoricalNegPool:
         s, d = self._ids(src), self._ids(dst)
         need = int(_lib.lib().tgx_negpool_update_workspace_size(n))
         if self._ws is None or self._ws.numel() < need:
+            if self._ws is not None:
+                # an update queued on another stream may still use the old one
+                torch.cuda.synchronize(self.device)
             self._ws = torch.empty(need, dtype=torch.uint8, device=self.device)
         _lib.check(_lib.lib().tgx_negpool_update(
             self._pool.data_ptr(), self._count.data_ptr(), self.num_nodes, self.pool_size,
