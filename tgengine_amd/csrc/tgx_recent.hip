@@ -186,7 +186,7 @@ constexpr int kMaxWaves = 8;
 constexpr int64_t kPackMinQueries = 8192;
 
 // output bytes of one query below which its waves are not split further
-constexpr int64_t kSplitBytes = 16384;
+constexpr int64_t kSplitBytes = 8192;
 
 // row chunks each lane loads before storing them (large-row copy)
 constexpr int kCopyDepth = 4;
@@ -988,7 +988,7 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
   P.off_tab = P.off_pe + round16(P.m * K * 8);
   P.wave_bytes = P.off_tab + round16(P.m * 24);
   // split: with one query per wave and fewer queries than wave slots, up to 8
-  // waves share each query's outputs; and up to 4 while each wave's share of a
+  // waves share each query's outputs; and up to 8 while each wave's share of a
   // query's output bytes stays at least kSplitBytes, so a grid of long copies
   // (large rows, large K) ends with a shorter tail of lone waves.  A workgroup
   // holds at most kMaxWaves waves (the kernel's launch bound): the plan group
@@ -999,7 +999,7 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
     while (split < 8 && a->num_queries * (split * 2) <= kPackMinQueries && gmin * split * 2 <= kMaxWaves)
       split *= 2;
     const int64_t qbytes = static_cast<int64_t>(K) * (P.row_bytes + 4 * a->d_t + 13);
-    while (split < 4 && qbytes / (split * 2) >= kSplitBytes && gmin * split * 2 <= kMaxWaves)
+    while (split < 8 && qbytes / (split * 2) >= kSplitBytes && gmin * split * 2 <= kMaxWaves)
       split *= 2;
   }
   P.split = split;
