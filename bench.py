@@ -56,60 +56,91 @@ def stage_stream(cfg, first: int, count: int, torch, device):
     return dev, lens, bts
 
 
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(cfg, g, pipe, first, seconds, torch, log, last):
     """Time the torch-CPU restatement of the reference path on batches first.. of the
-    stream, starting from the GPU ring state; its outputs must equal the GPU's."""
+    stream, starting from the GPU ring state; its outputs must equal the GPU's.
+
+    Two legs: the job's CPU share (OMP_NUM_THREADS where set, else the CPUs in
+    this process's affinity mask; torch threads set to that count) for
+    ``seconds``, then one thread for a third of that on the following batches.
+    os.cpu_count() is reported beside it: on a shared GPU box it counts the whole
+    host, not the CPUs this job was given."""
     from oracle.refpath_torch import RefPathCPU
-    from tgengine_amd import RawBatch
-    from tgengine_amd.synthetic import gen_batch
-    import stream_check
+    from tgengine_amd.synthetic import gen_batch, to_raw
     cpu = RefPathCPU(cfg.num_nodes, cfg.feat_dim, cfg.buffer_size)
     cpu.ids.copy_(g._ov_ids.cpu())
     cpu.times.copy_(g._ov_times.cpu())
     cpu.feats.copy_(g._ov_feats.float().cpu())
     cpu.wp.copy_(g._ov_write_pos.cpu())
-    threads = torch.get_num_threads()
-    spent = 0.0
-    queries = 0
-    batches = 0
-    i = first
-    while (spent < seconds or batches < 2) and i < last:
-        bt = gen_batch(cfg, i)
-        rb = stream_check.to_raw(cfg, bt)
-        pb = pipe.prepare(rb)
-        src = torch.from_numpy(bt["src"])
-        dst = torch.from_numpy(bt["dst"])
-        tt = torch.from_numpy(bt["time"])
-        neg = torch.from_numpy(bt["neg"])
-        f32 = torch.from_numpy(bt["feat"])
-        if cfg.feat_dtype == "bf16":
-            f32 = f32.view(torch.bfloat16).float()
-        t0 = time.perf_counter()
-        out = cpu.prepare(src, dst, neg, tt, cfg.k, co=cfg.co_occurrence)
-        cpu.advance(src, dst, tt, f32)
-        spent += time.perf_counter() - t0
-        # parity of the CPU restatement with the GPU on this full-size window
-        groups = [pb.src_neighbors, pb.dst_neighbors, pb.neg_neighbors]
-        gids = torch.cat([x.neighbor_ids.cpu() for x in groups])
-        gmask = torch.cat([x.mask.cpu() for x in groups])
-        gfeat = torch.cat([x.edge_feats.float().cpu() for x in groups])
-        gte = torch.cat([x.time_enc.cpu() for x in groups])
-        if not (torch.equal(gids, out["ids"]) and torch.equal(gmask, out["mask"])
-                and torch.equal(gfeat, out["feats"])):
-            raise RuntimeError(f"CPU baseline and GPU disagree at batch {i}")
-        te_err = float((gte.double() - out["te"].double()).abs().max()) if gte.numel() else 0.0
-        if te_err > 2e-6:
-            raise RuntimeError(f"time encodings differ by {te_err} at batch {i}")
-        g.advance(rb.src, rb.dst, rb.time, rb.edge_feat)
-        queries += len(bt["src"]) * cfg.queries_per_event
-        batches += 1
-        i += 1
-    log(f"cpu baseline: {batches} batches, {queries} queries in {spent:.2f}s on {threads} threads")
-    return {"value": queries / spent, "unit": "prepared queries/s", "cores": threads,
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    # the job's CPU share: OMP_NUM_THREADS where the box sets it (the GPU boxes
+    # give each GPU job 16 CPUs whatever the host counts), else the affinity mask
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    share = min(int(omp), affinity) if omp.isdigit() and int(omp) > 0 else affinity
+    prev_threads = torch.get_num_threads()
+    state = {"i": first}
+
+    def leg(threads, budget):
+        torch.set_num_threads(threads)
+        spent = 0.0
+        queries = batches = 0
+        start = state["i"]
+        while (spent < budget or batches < 2) and state["i"] < last:
+            i = state["i"]
+            bt = gen_batch(cfg, i)
+            rb = to_raw(cfg, bt)
+            pb = pipe.prepare(rb)
+            src = torch.from_numpy(bt["src"])
+            dst = torch.from_numpy(bt["dst"])
+            tt = torch.from_numpy(bt["time"])
+            neg = torch.from_numpy(bt["neg"])
+            f32 = torch.from_numpy(bt["feat"])
+            if cfg.feat_dtype == "bf16":
+                f32 = f32.view(torch.bfloat16).float()
+            t0 = time.perf_counter()
+            out = cpu.prepare(src, dst, neg, tt, cfg.k, co=cfg.co_occurrence)
+            cpu.advance(src, dst, tt, f32)
+            spent += time.perf_counter() - t0
+            # parity of the CPU restatement with the GPU on this full-size window
+            groups = [pb.src_neighbors, pb.dst_neighbors, pb.neg_neighbors]
+            gids = torch.cat([x.neighbor_ids.cpu() for x in groups])
+            gmask = torch.cat([x.mask.cpu() for x in groups])
+            gfeat = torch.cat([x.edge_feats.float().cpu() for x in groups])
+            gte = torch.cat([x.time_enc.cpu() for x in groups])
+            if not (torch.equal(gids, out["ids"]) and torch.equal(gmask, out["mask"])
+                    and torch.equal(gfeat, out["feats"])):
+                raise RuntimeError(f"CPU baseline and GPU disagree at batch {i}")
+            te_err = float((gte.double() - out["te"].double()).abs().max()) if gte.numel() else 0.0
+            if te_err > 2e-6:
+                raise RuntimeError(f"time encodings differ by {te_err} at batch {i}")
+            g.advance(rb.src, rb.dst, rb.time, rb.edge_feat)
+            queries += len(bt["src"]) * cfg.queries_per_event
+            batches += 1
+            state["i"] += 1
+        log(f"cpu baseline: {batches} batches, {queries} queries in {spent:.2f}s on {threads} threads")
+        return queries, spent, start, batches
+
+    q_n, s_n, b0, nb = leg(share, seconds)
+    q_1, s_1, b1, nb1 = leg(1, seconds / 3)
+    torch.set_num_threads(prev_threads)
+    return {"value": q_n / s_n, "unit": "prepared queries/s", "cores": share,
             "kind": "port",
-            "sample": (f"{cfg.name} batches {first}..{first + batches - 1} ({queries} queries, "
-                       f"prepare+advance) from the GPU ring state after batch {first - 1}; "
-                       f"outputs equal to the GPU's"), "batches": batches}
+            "sample": (f"{cfg.name} batches {b0}..{b0 + nb - 1} ({q_n} queries, prepare+advance) "
+                       f"from the GPU ring state after batch {b0 - 1}; outputs equal to the GPU's"),
+            "batches": nb, "threads": share, "os_cpu_count": os.cpu_count(),
+            "affinity_cpus": affinity, "cpu_model": cpu_model(),
+            "value_1thread": q_1 / s_1 if s_1 > 0 else None,
+            "sample_1thread": f"{cfg.name} batches {b1}..{b1 + nb1 - 1} ({q_1} queries) on 1 thread"}
 
 
 def main():
@@ -134,9 +165,7 @@ def main():
     log = (lambda *x: None) if a.quiet else (lambda *x: print(*x, file=sys.stderr, flush=True))
 
     import torch
-    sys.path.insert(0, str(ROOT / "tests"))
-    from tgengine_amd.synthetic import CONFIGS, num_batches
-    import stream_check
+    from tgengine_amd.synthetic import CONFIGS, make_graph, make_pipeline, num_batches
     cfg = CONFIGS[a.config]
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
@@ -156,8 +185,8 @@ def main():
         assert key_multiplier_ok(bt["time"], len(bt["src"]))
     del bts
 
-    g = stream_check.make_graph(cfg)
-    pipe = stream_check.make_pipeline(cfg, g)
+    g = make_graph(cfg)
+    pipe = make_pipeline(cfg, g)
     pipe.queries_per_workgroup = a.queries_per_workgroup
     from tgengine_amd import RawBatch
     offs = np.concatenate([[0], np.cumsum(lens)])
@@ -176,19 +205,22 @@ def main():
     torch.cuda.synchronize()
     log(f"warm-up {W} batches done")
 
-    # timed region: K steps, nothing but the hot path between the synchronisations
-    masks = []
+    # timed region: K steps, nothing but the hot path between the synchronisations;
+    # every step's outputs are dropped before the next, as in a training loop, so
+    # the caching allocator hands the same blocks back each step
     host_prep = host_adv = 0.0
+    total_q = 0
     torch.cuda.synchronize()
     t_start = time.perf_counter()
     for i in range(W, W + K):
         h0 = time.perf_counter()
         pb = pipe.prepare(raws[i])
         h1 = time.perf_counter()
-        masks.append((pb.src_neighbors.mask, pb.dst_neighbors.mask, pb.neg_neighbors.mask))
         g.advance(raws[i].src, raws[i].dst, raws[i].time, raws[i].edge_feat)
         host_adv += time.perf_counter() - h1
         host_prep += h1 - h0
+        total_q += lens[i] * cfg.queries_per_event
+    del pb
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_start
 
@@ -196,7 +228,10 @@ def main():
     # ring state the timed region left, captured once in a HIP graph and replayed
     # between two HIP events on the launch stream, so the kernels run back to back
     # with no host in the loop (a dispatch that records its own timing events runs
-    # measurably slower, and a Python launch loop cannot keep up with the kernel)
+    # measurably slower, and a Python launch loop cannot keep up with the kernel).
+    # Only the masks (the small output block) are kept; the bulk block of feature
+    # rows and encodings is released after each launch, so the graph's pool hands
+    # the same memory to the next launch, as the caching allocator does in the loop
     rmasks = []
     kern_ms = 0.0
     if R:
@@ -232,9 +267,7 @@ def main():
         prs = [lens[first + j] if cfg.co_occurrence else 0 for j in range(len(mask_list))]
         return qs, vs, [bytes_per_batch(cfg, qs[j], vs[j], prs[j]) for j in range(len(mask_list))]
 
-    Qs, Vs, _ = algo_bytes(masks, W)
     rQs, rVs, rbyts = algo_bytes(rmasks, W + K)
-    total_q = sum(Qs)
     value = total_q / wall
     avg_launch_s = kern_ms / 1e3 / n_launch
     achieved = sum(rbyts) / n_launch / avg_launch_s / 1e9 if rbyts else 0.0

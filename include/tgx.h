@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define TGX_ABI_VERSION 9
+#define TGX_ABI_VERSION 10
 
 /* status codes */
 #define TGX_OK 0
@@ -118,6 +118,11 @@ typedef struct tgx_query_group {
 } tgx_query_group;
 #define TGX_QG_NODES_I32 1
 
+/* work plans of tgx_recent_args.plan_mode */
+#define TGX_PLAN_TILES 0
+#define TGX_PLAN_EVENTS 1
+#define TGX_PLAN_LIST 2
+
 #define TGX_MAX_QUERY_GROUPS 4
 
 typedef struct tgx_recent_args {
@@ -127,10 +132,23 @@ typedef struct tgx_recent_args {
   const double* times;     /* [Q] query times */
   int64_t num_queries;
   int32_t k;               /* neighbours per query, 1..TGX_MAX_K */
-  /* work plan: group g handles queries plan[g*group + j], j < group (-1 = none).
-   * NULL plan: group g handles queries g*group .. g*group+group-1. */
+  /* work plan, by plan_mode:
+   *   TGX_PLAN_TILES (plan NULL): consecutive queries; `group` queries per
+   *     workgroup (a hint: a workgroup holds at most 8 wavefronts, so the launch
+   *     may give fewer queries to a workgroup when a query is shared by several
+   *     wavefronts); num_groups is ignored;
+   *   TGX_PLAN_EVENTS (plan NULL): event-major groups computed from the query
+   *     groups: group g = event g holds, for each query group in order,
+   *     its times_per queries of event g (the reference grouping [src, dst,
+   *     neg row-major, neg_src], pipeline/__init__.py:40-70, read as one
+   *     group per event); group = sum of times_per, num_groups = events;
+   *   TGX_PLAN_LIST (plan set): group g handles queries plan[g*group + j],
+   *     j < group (-1 = none).
+   * Co-occurrence needs TGX_PLAN_EVENTS or TGX_PLAN_LIST (its pairs are
+   * queries 0 and 1 of a group). */
   const int32_t* plan;
   int32_t group;           /* 1..8 */
+  int32_t plan_mode;       /* TGX_PLAN_*; TGX_PLAN_LIST iff plan != NULL */
   int64_t num_groups;
   /* outputs (row = query index); out_feats / out_eids / out_te may be NULL */
   int32_t* out_ids;        /* [Q,K] */
@@ -278,10 +296,24 @@ int tgx_negpool_sample(const int32_t* pool, const int64_t* count, int64_t num_no
 int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args* args,
                void* stream);
 
-/* Stand-alone co-occurrence over neighbour-id rows a, c int32 [P,K] (-1 = pad):
- * a_cnt/c_cnt int32 [P,K,2] (mode FREQ) and pair_count float [P] (may be NULL). */
-int tgx_co_occurrence(const int32_t* a_ids, const int32_t* c_ids, int64_t pairs, int32_t k,
-                      int32_t* a_cnt, int32_t* c_cnt, float* pair_count, void* stream);
+/* Launch shape tgx_recent would use for these arguments, without launching:
+ * shape[0] workgroups, [1] threads per workgroup, [2] dynamic LDS bytes,
+ * [3] queries per wavefront, [4] wavefronts per query, [5] queries per
+ * workgroup, [6] plan workgroups, [7] feature copy width in bytes.  Same
+ * argument checks and return codes as tgx_recent. */
+int tgx_recent_launch_shape(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args* args,
+                            int64_t shape[8]);
+
+/* Stand-alone co-occurrence over neighbour-id rows a, c int32 [P,K]:
+ * a_cnt/c_cnt int32 [P,K,2] (mode FREQ) and pair_count float [P] (may be NULL).
+ * a_mask / c_mask uint8 [P,K] (0/1) mark the valid positions; with a NULL mask
+ * a position is valid iff its id is not -1.  A count covers valid positions
+ * only, and an invalid position's counts are 0 (reference
+ * temporal_sample.cu:453-511, and the masked pair count of
+ * pipeline/__init__.py:206-219). */
+int tgx_co_occurrence(const int32_t* a_ids, const int32_t* c_ids, const uint8_t* a_mask,
+                      const uint8_t* c_mask, int64_t pairs, int32_t k, int32_t* a_cnt,
+                      int32_t* c_cnt, float* pair_count, void* stream);
 
 const char* tgx_last_error(void);
 int tgx_abi_version(void);

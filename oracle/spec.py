@@ -385,6 +385,26 @@ def co_occurrence_freq_brute(a, c):
     return a_cnt, c_cnt
 
 
+def co_occurrence_freq_masked(a, a_mask, c, c_mask):
+    """Per-position counts over the valid positions only (tgx_co_occurrence with
+    masks): a_cnt[p,i] = (#{j valid in a: a[j]==a[i]}, #{j valid in c: c[j]==a[i]})
+    at a valid position i, (0, 0) elsewhere; c_cnt likewise.  With masks
+    ``ids != -1`` this is co_occurrence_freq (temporal_sample.cu:453-511)."""
+    a = np.asarray(a, np.int64)
+    c = np.asarray(c, np.int64)
+    am = np.asarray(a_mask, bool)
+    cm = np.asarray(c_mask, bool)
+    aa = ((a[:, :, None] == a[:, None, :]) & am[:, None, :]).sum(-1)
+    ac = ((a[:, :, None] == c[:, None, :]) & cm[:, None, :]).sum(-1)
+    ca = ((c[:, :, None] == a[:, None, :]) & am[:, None, :]).sum(-1)
+    cc = ((c[:, :, None] == c[:, None, :]) & cm[:, None, :]).sum(-1)
+    a_cnt = np.stack([aa, ac], -1).astype(np.int32)
+    c_cnt = np.stack([ca, cc], -1).astype(np.int32)
+    a_cnt[~am] = 0
+    c_cnt[~cm] = 0
+    return a_cnt, c_cnt
+
+
 def co_pair_count(a_ids, a_mask, c_ids, c_mask) -> np.ndarray:
     """(P,) float32: #{i: a valid and some valid c[j]==a[i]} (pipeline/__init__.py:206-219)."""
     eq = a_ids[:, :, None] == c_ids[:, None, :]

@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(L, n), n
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
-    assert L.tgx_abi_version() == 9
+    assert L.tgx_abi_version() == _lib.TGX_ABI_VERSION == 10
     nm = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
                         text=True).stdout
     exported = set(re.findall(r"\bT (tgx_\w+)", nm))
@@ -47,7 +47,7 @@ int main(void) {
   S(tgx_query_group) F(tgx_query_group, count) F(tgx_query_group, times_per)
   F(tgx_query_group, flags) F(tgx_query_group, valid)
   S(tgx_recent_args) F(tgx_recent_args, k) F(tgx_recent_args, plan) F(tgx_recent_args, group)
-  F(tgx_recent_args, num_groups) F(tgx_recent_args, out_eids) F(tgx_recent_args, d_t)
+  F(tgx_recent_args, plan_mode) F(tgx_recent_args, num_groups) F(tgx_recent_args, out_eids) F(tgx_recent_args, d_t)
   F(tgx_recent_args, te_w) F(tgx_recent_args, dt_mode) F(tgx_recent_args, out_te)
   F(tgx_recent_args, co_mode) F(tgx_recent_args, co_a) F(tgx_recent_args, status)
   F(tgx_recent_args, num_query_groups) F(tgx_recent_args, query_groups)
@@ -122,9 +122,84 @@ def test_recent_argument_checks():
     a.timing_start = 8
     assert L.tgx_recent(ctypes.byref(ring), None, ctypes.byref(a), None) == 1 and "timing" in _err()
     a.timing_start = 0
-    a.plan = 0
-    a.num_groups = 1
-    assert L.tgx_recent(ctypes.byref(ring), None, ctypes.byref(a), None) == 1 and "without a plan" in _err()
+    a.plan_mode = 7
+    assert L.tgx_recent(ctypes.byref(ring), None, ctypes.byref(a), None) == 1 and "plan_mode" in _err()
+    a.plan_mode = _lib.TGX_PLAN_LIST  # a list plan needs its array
+    assert L.tgx_recent(ctypes.byref(ring), None, ctypes.byref(a), None) == 1 and "plan array" in _err()
+    a.plan_mode = _lib.TGX_PLAN_TILES
+
+
+def _shape(ring, csr, a):
+    out = (ctypes.c_int64 * 8)()
+    rc = _lib.lib().tgx_recent_launch_shape(ring, csr, ctypes.byref(a), out)
+    return rc, list(out)
+
+
+def test_co_occurrence_needs_a_plan_group():
+    """Co-occurrence pairs queries 0 and 1 of a plan group, so a tiled launch
+    (no plan array, no event-major plan) is refused instead of pairing queries
+    of the wrong workgroups and leaving output rows unwritten."""
+    L = _lib.lib()
+    ring = _lib.TgxRing(num_nodes=10, slots=4, feat_dim=2, feat_dtype=0, ids=8, times=8)
+    a = _lib.TgxRecentArgs(k=4, group=2, num_queries=6, num_groups=3, nodes=8, times=8,
+                           out_ids=8, out_times=8, out_mask=8, co_mode=_lib.TGX_CO_FREQ, co_a=8, co_c=8)
+    assert L.tgx_recent(ctypes.byref(ring), None, ctypes.byref(a), None) == 1
+    assert "TGX_PLAN_EVENTS" in _err()
+    # event-major groups need query groups whose per-event counts sum to `group`
+    a.plan_mode = _lib.TGX_PLAN_EVENTS
+    assert L.tgx_recent(ctypes.byref(ring), None, ctypes.byref(a), None) == 1 and "event-major" in _err()
+    a.num_query_groups = 2
+    for g in range(2):
+        a.query_groups[g].nodes = 8
+        a.query_groups[g].times = 8
+        a.query_groups[g].count = 3
+        a.query_groups[g].times_per = 1
+    rc, sh = _shape(ctypes.byref(ring), None, a)
+    assert rc == 0, _err()
+    assert sh[0] == 3 and sh[5] == 2 and sh[1] == 64 * 2 * sh[4]  # one event (2 queries) per workgroup
+    a.query_groups[1].count = 2  # not one query per event
+    assert L.tgx_recent(ctypes.byref(ring), None, ctypes.byref(a), None) == 1 and "times_per" in _err()
+
+
+def test_launch_shapes_stay_within_the_kernel_bounds():
+    """Every tiled launch fits the kernel's 512-thread bound and the LDS, for
+    every query count on both sides of the split rule, K and group: a tiny
+    batch (one query, K=3, no ring) once asked for four query slots of eight
+    split wavefronts, a 2048-thread block that the runtime refused."""
+    csr = _lib.TgxCsr(num_nodes=10, num_entries=5, feat_dim=4, feat_dtype=0, offsets=8, ids=8,
+                      times=8, feats=8)
+    ring = _lib.TgxRing(num_nodes=10, slots=32, feat_dim=4, feat_dtype=0, ids=8, times=8, feats=16)
+    for Q in (1, 2, 3, 511, 512, 513, 1024, 2049, 4096, 4097, 8192, 8193, 20000):
+        for k in (1, 3, 20, 64, 256):
+            for group in (1, 2, 4, 8):
+                for store in ((None, ctypes.byref(csr)), (ctypes.byref(ring), None)):
+                    a = _lib.TgxRecentArgs(k=k, group=group, num_queries=Q, nodes=8, times=8,
+                                           out_ids=8, out_times=8, out_mask=8, out_feats=16)
+                    rc, sh = _shape(store[0], store[1], a)
+                    assert rc == 0, _err()
+                    blocks, threads, lds, m, split, qpb = sh[:6]
+                    assert 64 <= threads <= 512 and threads % 64 == 0
+                    assert lds <= 160 * 1024
+                    assert threads // 64 == (qpb // m) * split
+                    assert blocks * qpb >= Q  # every query has a slot
+                    assert qpb // m <= group
+    a = _lib.TgxRecentArgs(k=3, group=4, num_queries=1, nodes=8, times=8, out_ids=8, out_times=8,
+                           out_mask=8, out_feats=16)
+    rc, sh = _shape(None, ctypes.byref(csr), a)
+    assert rc == 0 and sh[1] == 512 and sh[4] == 8 and sh[0] == 1  # one query over 8 waves
+
+
+def test_fastdiv_range_is_checked():
+    """Feature chunks are divided by the row's chunk count with a multiply-high
+    that is exact for dividends below 2^32 / chunks: wider rows are refused."""
+    ring = _lib.TgxRing(num_nodes=10, slots=4, feat_dim=30001, feat_dtype=_lib.TGX_BF16, ids=8,
+                        times=8, feats=2)
+    a = _lib.TgxRecentArgs(k=32, group=1, num_queries=5, nodes=8, times=8, out_ids=8, out_times=8,
+                           out_mask=8, out_feats=2)
+    assert _lib.lib().tgx_recent(ctypes.byref(ring), None, ctypes.byref(a), None) == 3
+    assert "index range" in _err()
+    a.k = 4  # 4 * 30001^2 < 2^32
+    assert _shape(ctypes.byref(ring), None, a)[0] == 0
 
 
 def test_ring_append_argument_checks():
@@ -235,20 +310,20 @@ def test_negpool_argument_checks():
 
 def test_co_occurrence_argument_checks():
     L = _lib.lib()
-    assert L.tgx_co_occurrence(8, 8, -1, 4, 8, 8, None, None) == 1
-    assert L.tgx_co_occurrence(8, 8, 4, 5000, 8, 8, None, None) == 3
-    assert L.tgx_co_occurrence(None, None, 0, 4, None, None, None, None) == 0
-    assert L.tgx_co_occurrence(None, None, 4, 4, None, None, None, None) == 1
+    assert L.tgx_co_occurrence(8, 8, None, None, -1, 4, 8, 8, None, None) == 1
+    assert L.tgx_co_occurrence(8, 8, None, None, 4, 5000, 8, 8, None, None) == 3
+    assert L.tgx_co_occurrence(None, None, None, None, 0, 4, None, None, None, None) == 0
+    assert L.tgx_co_occurrence(None, None, None, None, 4, 4, None, None, None, None) == 1
 
 
 def test_last_error_is_per_thread():
     L = _lib.lib()
-    L.tgx_co_occurrence(8, 8, -1, 4, 8, 8, None, None)
+    L.tgx_co_occurrence(8, 8, None, None, -1, 4, 8, 8, None, None)
     main_msg = _err()
     seen = []
 
     def other():
-        L.tgx_co_occurrence(8, 8, 4, 5000, 8, 8, None, None)
+        L.tgx_co_occurrence(8, 8, None, None, 4, 5000, 8, 8, None, None)
         seen.append(_lib.lib().tgx_last_error().decode())
 
     th = threading.Thread(target=other)

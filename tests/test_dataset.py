@@ -118,7 +118,7 @@ def test_known_answer_small(tmp_path):
     assert ds.edge_feat.shape == (10, PAD_FEAT_DIM)
     assert (ds.edge_feat[:, :2] == 1).all() and (ds.edge_feat[:, 2:] == 0).all()
     assert ds.node_feat is None and ds.node_feat_dim == 0
-    assert "train :       7 events" in ds.summary()
+    assert "train events [0, 7) = 7" in ds.summary()
 
     dt = load_dataset("tiny", str(tmp_path), split_strategy="time")
     # span 9: boundaries 1 + 9 * 0.7 = 7.3 and 1 + 9 * 0.85 = 8.65, as "event" here

@@ -318,6 +318,37 @@ def test_standalone_co_occurrence_rows():
     assert np.array_equal(got, O.co_pair_count(a, a != -1, c, c != -1))
 
 
+def test_standalone_co_occurrence_uses_the_masks():
+    # masked positions hold ordinary ids (not -1): the reference pair count reads
+    # the masks (pipeline/__init__.py:206-219), so these must not count
+    import ctypes
+    from tgengine_amd.core import _lib
+    rng = np.random.default_rng(16)
+    P, K = 41, 37
+    a = rng.integers(-1, 7, (P, K)).astype(np.int32)
+    c = rng.integers(-1, 7, (P, K)).astype(np.int32)
+    am = rng.random((P, K)) < 0.7
+    cm = rng.random((P, K)) < 0.6
+    from tgengine_amd.core import NeighborData
+    z = torch.zeros(P, K, dtype=torch.float64).cuda()
+    got = DataPipeline._co_occur_from_neighbors(NeighborData(cu(a), z, z, cu(am)),
+                                                NeighborData(cu(c), z, z, cu(cm))).cpu().numpy()
+    assert np.array_equal(got, O.co_pair_count(a, am, c, cm))
+    # per-position counts through the C ABI, with and without masks
+    ga, gc = cu(a), cu(c)
+    gam, gcm = cu(am.astype(np.uint8)), cu(cm.astype(np.uint8))
+    for masks, (ea, ec) in (((gam.data_ptr(), gcm.data_ptr()), O.co_occurrence_freq_masked(a, am, c, cm)),
+                            ((None, None), O.co_occurrence_freq(a, c))):
+        a_cnt = torch.empty((P, K, 2), dtype=torch.int32, device="cuda")
+        c_cnt = torch.empty((P, K, 2), dtype=torch.int32, device="cuda")
+        pair = torch.empty(P, dtype=torch.float32, device="cuda")
+        rc = _lib.lib().tgx_co_occurrence(ga.data_ptr(), gc.data_ptr(), masks[0], masks[1], P, K,
+                                          a_cnt.data_ptr(), c_cnt.data_ptr(), pair.data_ptr(),
+                                          torch.cuda.current_stream().cuda_stream)
+        _lib.check(rc, "tgx_co_occurrence")
+        assert np.array_equal(a_cnt.cpu().numpy(), ea) and np.array_equal(c_cnt.cpu().numpy(), ec)
+
+
 def test_pipeline_negatives_2d_and_neg_src():
     rng, g, csr, ring, tmax = _build(16, 25, 8, 6, 6, False, True, eids=True)
     spec = GatherSpec(neighbors=NeighborSpec(k=6), time_encoding=8, edge_ids=True)

@@ -224,6 +224,30 @@ def test_co_occurrence_freq_matches_bruteforce(seed):
     assert np.array_equal(pc, ((a != -1) & (x1[..., 1] > 0)).sum(1).astype(np.float32))
 
 
+@pytest.mark.parametrize("seed", [0, 1])
+def test_co_occurrence_freq_masked(seed):
+    rng = np.random.default_rng(seed)
+    a = rng.integers(-1, 6, (7, 9))
+    c = rng.integers(-1, 6, (7, 9))
+    # masks ids != -1 reduce to the reference's id rule
+    x, y = O.co_occurrence_freq_masked(a, a != -1, c, c != -1)
+    x2, y2 = O.co_occurrence_freq(a, c)
+    assert np.array_equal(x, x2) and np.array_equal(y, y2)
+    # arbitrary masks: brute force over the valid positions only
+    am = rng.random((7, 9)) < 0.6
+    cm = rng.random((7, 9)) < 0.6
+    x, y = O.co_occurrence_freq_masked(a, am, c, cm)
+    for p in range(7):
+        for i in range(9):
+            ex = (sum(am[p, j] and a[p, j] == a[p, i] for j in range(9)),
+                  sum(cm[p, j] and c[p, j] == a[p, i] for j in range(9))) if am[p, i] else (0, 0)
+            ey = (sum(am[p, j] and a[p, j] == c[p, i] for j in range(9)),
+                  sum(cm[p, j] and c[p, j] == c[p, i] for j in range(9))) if cm[p, i] else (0, 0)
+            assert tuple(x[p, i]) == ex and tuple(y[p, i]) == ey
+    # the pair count is #{valid i: a_cnt[i, 1] > 0} under the same masks
+    assert np.array_equal(O.co_pair_count(a, am, c, cm), (am & (x[..., 1] > 0)).sum(1).astype(np.float32))
+
+
 def test_co_pair_known_answers():
     """tests/test_core.py:59-76 (2), tests/test_cuda_kernels.py:225-263 (0 and 5)."""
     assert O.co_pair_count(np.array([[2, 3]]), np.array([[True, True]]),

@@ -21,6 +21,10 @@ TGX_DT_TGN = 1
 TGX_CO_NONE = 0
 TGX_CO_FREQ = 1
 TGX_CO_DYGFORMER = 2
+TGX_PLAN_TILES = 0
+TGX_PLAN_EVENTS = 1
+TGX_PLAN_LIST = 2
+TGX_ABI_VERSION = 10
 TGX_STATUS_WORDS = 8
 TGX_ST_BAD_EVENT_NODE = 0
 TGX_ST_KEY_COLLISION = 1
@@ -55,7 +59,7 @@ class TgxQueryGroup(ctypes.Structure):
 
 class TgxRecentArgs(ctypes.Structure):
     _fields_ = [("nodes", c_vp), ("times", c_vp), ("num_queries", c_i64), ("k", c_i32),
-                ("plan", c_vp), ("group", c_i32), ("num_groups", c_i64),
+                ("plan", c_vp), ("group", c_i32), ("plan_mode", c_i32), ("num_groups", c_i64),
                 ("out_ids", c_vp), ("out_times", c_vp), ("out_feats", c_vp), ("out_mask", c_vp),
                 ("out_eids", c_vp),
                 ("d_t", c_i32), ("te_w", c_vp), ("te_b", c_vp), ("dt_mode", c_i32), ("out_te", c_vp),
@@ -90,7 +94,9 @@ SIGNATURES = {
     "tgx_ring_scratch_size": (ctypes.c_size_t, [c_i64]),
     "tgx_recent": (c_i32, [ctypes.POINTER(TgxRing), ctypes.POINTER(TgxCsr),
                            ctypes.POINTER(TgxRecentArgs), c_vp]),
-    "tgx_co_occurrence": (c_i32, [c_vp, c_vp, c_i64, c_i32, c_vp, c_vp, c_vp, c_vp]),
+    "tgx_recent_launch_shape": (c_i32, [ctypes.POINTER(TgxRing), ctypes.POINTER(TgxCsr),
+                                        ctypes.POINTER(TgxRecentArgs), ctypes.POINTER(c_i64)]),
+    "tgx_co_occurrence": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i32, c_vp, c_vp, c_vp, c_vp]),
     "tgx_csr_build": (c_i32, [ctypes.POINTER(TgxCsrBuildArgs), c_vp]),
     "tgx_csr_build_workspace_size": (ctypes.c_size_t, [c_i64]),
     "tgx_negpool_update_workspace_size": (ctypes.c_size_t, [c_i64]),
@@ -127,7 +133,7 @@ def lib() -> ctypes.CDLL:
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
-        if handle.tgx_abi_version() != 9:
+        if handle.tgx_abi_version() != TGX_ABI_VERSION:
             raise RuntimeError("libtgx ABI version mismatch")
         _lib = handle
         return _lib

@@ -87,18 +87,20 @@ class TemporalDataset:
         return self.num_edges - self.val_end
 
     def summary(self) -> str:
-        """Human-readable split summary (reference :107-121)."""
-        lines = [
-            f"Dataset: {self.num_nodes} nodes, {self.num_edges} edges, d_edge={self.edge_feat_dim}",
-            f"Split ({self.split_strategy}-based):",
-            f"  train : {self.train_size:>7,} events  (t ≤ {self.val_time:.2f})",
-            f"  val   : {self.val_size:>7,} events  ({self.val_time:.2f} < t ≤ {self.test_time:.2f})",
-            f"  test  : {self.test_size:>7,} events  (t > {self.test_time:.2f})",
-        ]
+        """One line per split: event index range, size and time bounds."""
+        out = [f"{self.num_nodes} nodes / {self.num_edges} events / edge features {self.edge_feat_dim}"
+               f" / {self.split_strategy} split"]
+        bounds = (("train", 0, self.train_end, f"time <= {self.val_time:.4g}"),
+                  ("val", self.train_end, self.val_end,
+                   f"{self.val_time:.4g} < time <= {self.test_time:.4g}"),
+                  ("test", self.val_end, self.num_edges, f"time > {self.test_time:.4g}"))
+        for name, lo, hi, cond in bounds:
+            out.append(f"{name:>5} events [{lo}, {hi}) = {hi - lo}, {cond}")
         if self.inductive_edges is not None:
-            pct = 100 * len(self.inductive_edges["src"]) / max(self.num_nodes, 1)
-            lines.append(f"  inductive nodes hidden from train: ~{pct:.1f}%")
-        return "\n".join(lines)
+            n = len(self.inductive_edges["src"])
+            out.append(f"{'new':>5} nodes withheld from training: {n} "
+                       f"({n / max(self.num_nodes, 1):.1%} of all nodes)")
+        return "\n".join(out)
 
     def split_range(self, split: str) -> tuple[int, int]:
         if split == "train":
@@ -218,16 +220,14 @@ def hidden_test_nodes(src: np.ndarray, dst: np.ndarray, time_vals: np.ndarray,
 def _print_split_summary(name: str, strategy: str, train_end: int, val_size: int, test_size: int,
                          val_time: float, test_time: float, num_nodes: int,
                          n_inductive: int) -> None:
-    """Split report printed at load (reference dataset.py:214-235)."""
+    """Load-time report: dataset size, then the three split sizes and cut times."""
     total = train_end + val_size + test_size
-    print(f"Dataset: {name} | {total:,} edges | {num_nodes:,} nodes")
-    print(f"Split ({strategy}-based):")
-    print(f"  train : {train_end:>7,} events  (t ≤ {val_time:.2f})")
-    print(f"  val   : {val_size:>7,} events  ({val_time:.2f} < t ≤ {test_time:.2f})")
-    print(f"  test  : {test_size:>7,} events  (t > {test_time:.2f})")
+    parts = [f"{name}: {total} events, {num_nodes} nodes, {strategy} split",
+             f"train={train_end} val={val_size} test={test_size}",
+             f"cuts at t={val_time:.4g} and t={test_time:.4g}"]
     if n_inductive > 0:
-        pct = 100 * n_inductive / max(num_nodes, 1)
-        print(f"  Inductive nodes hidden from train: {n_inductive} ({pct:.1f}%)")
+        parts.append(f"{n_inductive} new nodes withheld ({n_inductive / max(num_nodes, 1):.1%})")
+    print("; ".join(parts))
 
 
 def load_dyglib(dataset_name: str, base: Path, val_ratio: float = 0.15, test_ratio: float = 0.15,

@@ -25,7 +25,6 @@ import threading
 from dataclasses import dataclass
 from typing import Optional
 
-import numpy as np
 import torch
 from torch import Tensor
 
@@ -169,6 +168,9 @@ class TemporalGraph:
         self._plan_lock = threading.Lock()
         self._ring_struct: Optional[_lib.TgxRing] = None
         self._csr_struct: Optional[_lib.TgxCsr] = None
+        # bumped whenever the ring or CSR arrays (and so their C structs) change:
+        # launch contexts cached by a DataPipeline are rebuilt when it moves
+        self._gen = 0
         # optional object whose events() returns a (start, stop) pair of raw
         # hipEvent_t handles (or (0, 0)); each tgx_recent launch records the
         # kernel's own start and end on them
@@ -190,6 +192,7 @@ class TemporalGraph:
         nscr = int(_lib.lib().tgx_ring_scratch_size(N)) // 4
         self._ov_scratch = torch.zeros(nscr, dtype=torch.int32, device=dev)
         self._ring_struct = None
+        self._gen += 1
 
     def _ring(self) -> Optional[_lib.TgxRing]:
         if self._ov_ids is None:
@@ -398,11 +401,13 @@ class TemporalGraph:
         self._frozen = True
         self._build = []
         self._csr_struct = None
+        self._gen += 1
 
     # ------------------------------------------------------------------ queries
     def _query(self, nodes: Optional[Tensor], times: Optional[Tensor], k: int, *,
                groups: Optional[list] = None, plan: Optional[Tensor] = None,
-               group: int = 1, num_groups: Optional[int] = None, d_t: int = 0,
+               plan_mode: int = _lib.TGX_PLAN_TILES, group: int = 4,
+               num_groups: Optional[int] = None, d_t: int = 0,
                te_w: Optional[Tensor] = None, te_b: Optional[Tensor] = None,
                dt_mode: int = _lib.TGX_DT_DYGFORMER, co_mode: int = _lib.TGX_CO_NONE,
                want_eids: bool = False, append: Optional[tuple] = None) -> dict:
@@ -411,7 +416,7 @@ class TemporalGraph:
         Queries come either as ``nodes``/``times`` or as ``groups``: a list of
         (nodes, times, times_per[, valid]) read in place and concatenated in order
         (int64 or int32 nodes; a False in ``valid`` makes that query padding only).  Returns
-        lists of per-group views under "ids", "times", "feats", "mask" (bool), and
+        lists of per-group tensors under "ids", "times", "feats", "mask" (bool), and
         "eids" / "te" when asked for, plus "co_a", "co_c", "co_pair" with co-occurrence.
         ``append``: (src, dst, time) of the batch the caller advances next; when it
         can be planned (see plan_append) the same launch also plans its ring update.
@@ -427,23 +432,25 @@ class TemporalGraph:
             groups = [(nodes, times, 1)]
         if len(groups) > _lib.TGX_MAX_QUERY_GROUPS:
             raise ValueError(f"at most {_lib.TGX_MAX_QUERY_GROUPS} query groups")
-        res = self._gather(groups, k, plan, group, num_groups, d_t, te_w, te_b, dt_mode, co_mode,
-                           want_eids, append)
-        out = {"ids": res[0], "times": res[1], "feats": res[2], "mask": res[3]}
-        if want_eids:
-            out["eids"] = res[4]
+        planned, res = self._gather(groups, k, plan, plan_mode, group, num_groups, d_t, te_w, te_b,
+                                    dt_mode, co_mode, want_eids, append)
+        nf = 4 + (d_t > 0) + bool(want_eids)
+        ng = len(groups)
+        out = {"ids": res[0:ng * nf:nf], "times": res[1:ng * nf:nf], "feats": res[2:ng * nf:nf],
+               "mask": res[3:ng * nf:nf]}
         if d_t > 0:
-            out["te"] = res[5]
+            out["te"] = res[4:ng * nf:nf]
+        if want_eids:
+            out["eids"] = res[nf - 1:ng * nf:nf]
         if co_mode != _lib.TGX_CO_NONE:
-            out["co_a"], out["co_c"], out["co_pair"] = res[6]
+            out["co_a"], out["co_c"], out["co_pair"] = res[ng * nf:ng * nf + 3]
         return out
 
-    def _gather(self, groups, k, plan, group, num_groups, d_t, te_w, te_b, dt_mode, co_mode,
-                want_eids, append) -> list:
-        """One tgx_recent launch over checked query groups; the extension's result
-        list (per-group views: ids, times, feats, mask, eids, te; co-occurrence;
-        whether the ``append`` batch was planned).  When ``append`` is given and the
-        ring exists, the launch also plans that batch (see plan_append)."""
+    def _gather(self, groups, k, plan, plan_mode, group, num_groups, d_t, te_w, te_b, dt_mode,
+                co_mode, want_eids, append) -> tuple:
+        """One tgx_recent launch over checked query groups: the extension's
+        (planned, tensors) pair.  When ``append`` is given and the ring exists,
+        the launch also plans that batch (see plan_append)."""
         if not self._frozen:
             self.freeze_csr()
         ring = self._ring()
@@ -453,22 +460,24 @@ class TemporalGraph:
             ev0, ev1 = self.kernel_timer.events()
         stream = _stream_handle(self.device)
         if append is None or ring is None:
-            return self._launch_recent(ring, csr, groups, k, plan, group, num_groups, d_t, te_w,
-                                       te_b, dt_mode, co_mode, want_eids, ev0, ev1, None, None, stream)
+            return self._launch_recent(ring, csr, groups, k, plan, plan_mode, group, num_groups, d_t,
+                                       te_w, te_b, dt_mode, co_mode, want_eids, ev0, ev1, None, None,
+                                       stream)
         # the extension plans the batch when its tensors allow it (int64 / float64
         # contiguous 1-D device tensors of one non-zero length)
         with self._plan_lock:
             if self._plan is not None:  # an earlier plan nobody advanced: drop it first
                 self._discard_plan()
             ws = self._plan_workspace(int(append[0].shape[0]))
-            res = self._launch_recent(ring, csr, groups, k, plan, group, num_groups, d_t, te_w,
-                                      te_b, dt_mode, co_mode, want_eids, ev0, ev1, append, ws, stream)
-            if res[7]:
+            res = self._launch_recent(ring, csr, groups, k, plan, plan_mode, group, num_groups, d_t,
+                                      te_w, te_b, dt_mode, co_mode, want_eids, ev0, ev1, append, ws,
+                                      stream)
+            if res[0]:
                 self._plan = _Plan(append[0], append[1], append[2], stream)
         return res
 
-    def _launch_recent(self, ring, csr, groups, k, plan, group, num_groups, d_t, te_w, te_b,
-                       dt_mode, co_mode, want_eids, ev0, ev1, append, ws, stream):
+    def _launch_recent(self, ring, csr, groups, k, plan, plan_mode, group, num_groups, d_t, te_w,
+                       te_b, dt_mode, co_mode, want_eids, ev0, ev1, append, ws, stream):
         a_src, a_dst, a_time = append if append is not None else (None, None, None)
         gn, gt, gp, gv = [], [], [], []
         for grp in groups:
@@ -482,10 +491,37 @@ class TemporalGraph:
         return _host().recent(
             ctypes.addressof(ring) if ring is not None else 0,
             ctypes.addressof(csr) if csr is not None else 0,
-            gn, gt, gp, gv, k, self.edge_feat_dim, self.feat_dtype, plan, group,
+            gn, gt, gp, gv, k, self.edge_feat_dim, self.feat_dtype, plan, int(plan_mode), int(group),
             -1 if num_groups is None else int(num_groups), int(d_t), te_w, te_b, int(dt_mode),
             int(co_mode), bool(want_eids), self._status, stream, ev0, ev1,
             a_src, a_dst, a_time, ws)
+
+    def _prepare(self, prep, src: Tensor, dst: Tensor, time: Tensor, neg: Optional[Tensor],
+                 neg_src: Optional[Tensor], plan_updates: bool) -> tuple:
+        """One DataPipeline 1-hop launch through its configured extension context
+        ``prep``: (planned, tensors).  With ``plan_updates`` and a ring, the launch
+        also plans the ring update of this batch for the advance() that follows."""
+        if not self._frozen:
+            self.freeze_csr()
+        stream = _stream_handle(self.device)
+        if not plan_updates or self._ov_ids is None:
+            return prep.run(src, dst, time, neg, neg_src, stream, None)
+        with self._plan_lock:
+            if self._plan is not None:  # an earlier plan nobody advanced: drop it first
+                self._discard_plan()
+            ws = self._plan_workspace(int(src.shape[0]))
+            res = prep.run(src, dst, time, neg, neg_src, stream, ws)
+            if res[0]:
+                self._plan = _Plan(src, dst, time, stream)
+        return res
+
+    def _structs(self) -> tuple:
+        """Addresses of the ring and CSR C structs (0 when absent); stable until
+        ``_gen`` changes."""
+        ring = self._ring()
+        csr = self._csr()
+        return (ctypes.addressof(ring) if ring is not None else 0,
+                ctypes.addressof(csr) if csr is not None else 0)
 
     def recent(self, nodes: Tensor, times: Tensor, k: int) -> NeighborData:
         """Most recent k neighbours before each query time (reference :183-280)."""
@@ -515,10 +551,11 @@ class TemporalGraph:
         B = int(src.shape[0])
         if B == 0:
             return torch.zeros(0, dtype=torch.float32, device=self.device)
-        nodes = torch.cat([src.to(self.device, torch.int64), dst.to(self.device, torch.int64)])
-        qt = torch.cat([times, times]).to(self.device, torch.float64)
-        plan = pair_plan(B, self.device)
-        o = self._query(nodes, qt, k, plan=plan, group=2, num_groups=B,
+        qt = times.to(self.device, torch.float64)
+        # event-major pairs: group p = (src p, dst p)
+        o = self._query(None, None, k, groups=[(src.to(self.device, torch.int64), qt, 1),
+                                               (dst.to(self.device, torch.int64), qt, 1)],
+                        plan_mode=_lib.TGX_PLAN_EVENTS, group=2, num_groups=B,
                         co_mode=_lib.TGX_CO_FREQ)
         return o["co_pair"]
 
@@ -533,6 +570,7 @@ class TemporalGraph:
         self._ov_scratch = None
         self._ring_struct = None
         self._csr_struct = None
+        self._gen += 1
         self._num_edges = 0
 
     def snapshot(self) -> Snapshot:
@@ -583,17 +621,3 @@ class TemporalGraph:
                           edge_feat[s:e] if edge_feat is not None else None)
         graph.freeze_csr()
         return graph
-
-
-_PLAN_CACHE: dict = {}
-
-
-def pair_plan(B: int, device: torch.device) -> Tensor:
-    """Plan pairing query p with query B+p in group p (int32, device)."""
-    key = ("pair", B, str(device))
-    t = _PLAN_CACHE.get(key)
-    if t is None:
-        a = np.arange(B, dtype=np.int32)
-        t = torch.from_numpy(np.stack([a, a + B], 1).reshape(-1).copy()).to(device)
-        _PLAN_CACHE[key] = t
-    return t

@@ -2,9 +2,17 @@
 //
 // One call per TemporalGraph.recent / DataPipeline.prepare / advance: it checks
 // the inputs, allocates the outputs from the caching allocator, fills the C-ABI
-// argument block, launches through libtgx and returns the per-group views.  This
-// keeps the per-batch host cost to a few microseconds; all device work is in
-// libtgx (include/tgx.h), which never sees a torch type.
+// argument block, launches through libtgx and returns the per-group tensors.
+// All device work is in libtgx (include/tgx.h), which never sees a torch type.
+//
+// The outputs of one launch live in two allocations (two caching-allocator
+// round trips per prepare): a small block with ids, times, masks, edge ids and
+// co-occurrence counts, and a bulk block with the feature rows and time
+// encodings.  The per-group tensors are typed blocks of those byte buffers,
+// built directly as TensorImpls: they share the buffer's storage and are plain
+// tensors, not autograd views of each other.  Keeping one tensor alive keeps
+// its whole block alive, so a caller that keeps only masks or ids does not pin
+// the feature rows and encodings.
 #include <torch/extension.h>
 
 #include <stdexcept>
@@ -12,6 +20,8 @@
 #include <vector>
 
 #include "tgx.h"
+
+namespace py = pybind11;
 
 namespace {
 
@@ -24,47 +34,60 @@ at::Tensor as_dev(const at::Tensor& t, at::ScalarType dt, const at::Device& dev)
   return t.to(dev, dt).contiguous();
 }
 
-int64_t ptr(const c10::optional<at::Tensor>& t) {
-  return t.has_value() ? reinterpret_cast<int64_t>(t->data_ptr()) : 0;
-}
-
 // 1-D view of t (t itself when it already is 1-D)
 at::Tensor flat(const at::Tensor& t) { return t.dim() == 1 ? t : t.reshape({-1}); }
 
 // a contiguous `st` tensor of shape `sizes` at byte offset `byte_off` of base's
-// storage (a multiple of the element size), built directly like split_rows' blocks
-at::Tensor typed_block(const at::Tensor& base, at::ScalarType st, int64_t byte_off,
+// storage (a multiple of the element size)
+at::Tensor typed_block(const at::Tensor& base, const caffe2::TypeMeta dt, int64_t byte_off,
                        at::IntArrayRef sizes) {
-  const caffe2::TypeMeta dt = c10::scalarTypeToTypeMeta(st);
   auto impl = c10::make_intrusive<c10::TensorImpl>(c10::Storage(base.storage()), base.key_set(), dt);
   impl->set_sizes_contiguous(sizes);
   impl->set_storage_offset(byte_off / static_cast<int64_t>(dt.itemsize()));
   return at::Tensor(std::move(impl));
 }
 
-// x split along dim 0 into consecutive blocks of sizes[g] rows: tensors built
-// directly on x's storage (no dispatcher round trip per block, about four times
-// cheaper than split_with_sizes; the blocks are plain tensors sharing x's
-// memory, not autograd views of x)
-std::vector<at::Tensor> split_rows(const at::Tensor& x, const std::vector<int64_t>& sizes) {
-  if (sizes.size() == 1) return {x};
-  std::vector<at::Tensor> out;
-  out.reserve(sizes.size());
-  const c10::Storage& st = x.storage();
-  const c10::DispatchKeySet ks = x.key_set();
-  const caffe2::TypeMeta dt = x.dtype();
-  std::vector<int64_t> sz(x.sizes().begin(), x.sizes().end());
-  const at::IntArrayRef strides = x.strides();
-  int64_t off = x.storage_offset();
-  for (int64_t s : sizes) {
-    sz[0] = s;
-    auto impl = c10::make_intrusive<c10::TensorImpl>(c10::Storage(st), ks, dt);
-    impl->set_sizes_and_strides(sz, strides, off);
-    out.emplace_back(std::move(impl));
-    off += s * strides[0];
+int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
+
+// Byte layout of the outputs of one tgx_recent launch over Q queries: the bulk
+// block (feature rows, encodings) and the small block (times, edge ids, ids,
+// co-occurrence, masks), every field 256-byte aligned within its block.
+struct Layout {
+  int64_t feats = 0, te = 0, bulk = 0;
+  int64_t times = 0, eids = 0, ids = 0, coa = 0, coc = 0, cop = 0, mask = 0, small = 0;
+  Layout(int64_t Q, int64_t k, int64_t row_bytes, int64_t d_t, bool want_eids, int64_t co_rows,
+         int64_t co_len) {
+    const int64_t QK = Q * k;
+    int64_t o = 0;
+    feats = o;
+    o = align256(o + QK * row_bytes);
+    te = o;
+    o = align256(o + QK * d_t * 4);
+    bulk = o;
+    o = 0;
+    times = o;
+    o = align256(o + QK * 8);
+    eids = o;
+    o = align256(o + (want_eids ? QK * 8 : 0));
+    ids = o;
+    o = align256(o + QK * 4);
+    coa = o;
+    o = align256(o + co_rows * co_len * 2 * 4);
+    coc = o;
+    o = align256(o + co_rows * co_len * 2 * 4);
+    cop = o;
+    o = align256(o + co_rows * 4);
+    mask = o;
+    o = align256(o + QK);
+    small = o;
   }
-  return out;
-}
+};
+
+const caffe2::TypeMeta kI32 = caffe2::TypeMeta::Make<int32_t>();
+const caffe2::TypeMeta kI64 = caffe2::TypeMeta::Make<int64_t>();
+const caffe2::TypeMeta kF64 = caffe2::TypeMeta::Make<double>();
+const caffe2::TypeMeta kF32 = caffe2::TypeMeta::Make<float>();
+const caffe2::TypeMeta kBool = caffe2::TypeMeta::Make<bool>();
 
 // the ring plan of a batch can run in the gather launch: int64 / int64 /
 // float64 contiguous 1-D tensors of one non-zero length on the launch's device
@@ -77,22 +100,79 @@ bool plannable(const at::Tensor& s, const at::Tensor& d, const at::Tensor& t, co
   return b > 0 && ok(s, at::kLong) && ok(d, at::kLong) && ok(t, at::kDouble);
 }
 
-// Queries arrive as groups (nodes, times, times_per) read in place by the kernel.
-// append_src/dst/time + append_ws (all or none): the caller's next ring batch,
-// planned by the same launch when plannable() allows.
-// Returns [ids, times, feats, mask(bool), eids|None-placeholder, te|placeholder,
-//          co_a, co_c, co_pair, planned] as lists of per-group views (co_*
-// unsplit); planned holds one tensor when the batch was planned, else nothing.
-std::vector<std::vector<at::Tensor>> recent(
-    int64_t ring_addr, int64_t csr_addr, const std::vector<at::Tensor>& gnodes,
-    const std::vector<at::Tensor>& gtimes, const std::vector<int64_t>& gper,
-    const std::vector<c10::optional<at::Tensor>>& gvalid, int64_t k,
-    int64_t feat_dim, at::ScalarType feat_dtype, const c10::optional<at::Tensor>& plan,
-    int64_t group, int64_t num_groups, int64_t d_t, const c10::optional<at::Tensor>& te_w,
-    const c10::optional<at::Tensor>& te_b, int64_t dt_mode, int64_t co_mode, bool want_eids,
-    const at::Tensor& status, int64_t stream, int64_t ev0, int64_t ev1,
-    const c10::optional<at::Tensor>& append_src, const c10::optional<at::Tensor>& append_dst,
-    const c10::optional<at::Tensor>& append_time, const c10::optional<at::Tensor>& append_ws) {
+// Output tensors of one launch: allocation, layout and the argument block's
+// output pointers; per-group tensors are built on demand.
+struct Out {
+  at::Tensor bulk, small;
+  Layout lay;
+  int64_t k, row_bytes, d_t, feat_dim;
+  caffe2::TypeMeta fdt;
+  bool eids, co;
+  int64_t co_rows, co_len;
+  Out(const at::Device& dev, int64_t Q, int64_t k_, int64_t feat_dim_, at::ScalarType feat_dtype,
+      int64_t d_t_, bool want_eids, int64_t co_mode, int64_t co_rows_)
+      : lay(Q, k_, feat_dim_ * c10::elementSize(feat_dtype), d_t_, want_eids,
+            co_mode != TGX_CO_NONE ? co_rows_ : 0, co_mode == TGX_CO_FREQ ? k_ : k_ + 1),
+        k(k_), row_bytes(feat_dim_ * c10::elementSize(feat_dtype)), d_t(d_t_), feat_dim(feat_dim_),
+        fdt(c10::scalarTypeToTypeMeta(feat_dtype)), eids(want_eids), co(co_mode != TGX_CO_NONE),
+        co_rows(co_mode != TGX_CO_NONE ? co_rows_ : 0),
+        co_len(co_mode == TGX_CO_FREQ ? k_ : k_ + 1) {
+    const auto opt = at::TensorOptions().device(dev).dtype(at::kByte);
+    bulk = at::empty({lay.bulk}, opt);
+    small = at::empty({lay.small}, opt);
+  }
+  uint8_t* pb(int64_t off) const { return static_cast<uint8_t*>(bulk.data_ptr()) + off; }
+  uint8_t* ps(int64_t off) const { return static_cast<uint8_t*>(small.data_ptr()) + off; }
+  void fill(tgx_recent_args& a) const {
+    a.out_ids = reinterpret_cast<int32_t*>(ps(lay.ids));
+    a.out_times = reinterpret_cast<double*>(ps(lay.times));
+    a.out_feats = pb(lay.feats);
+    a.out_mask = ps(lay.mask);
+    a.out_eids = eids ? reinterpret_cast<int64_t*>(ps(lay.eids)) : nullptr;
+    a.out_te = d_t > 0 ? reinterpret_cast<float*>(pb(lay.te)) : nullptr;
+    if (co) {
+      a.co_a = reinterpret_cast<int32_t*>(ps(lay.coa));
+      a.co_c = reinterpret_cast<int32_t*>(ps(lay.coc));
+      a.co_pair = reinterpret_cast<float*>(ps(lay.cop));
+    }
+  }
+  // rows [r0, r0 + n) of every per-query output, appended to v:
+  // ids, times, feats, mask, [te], [eids]
+  void group(std::vector<at::Tensor>& v, int64_t r0, int64_t n) const {
+    const int64_t rk = r0 * k;
+    v.push_back(typed_block(small, kI32, lay.ids + rk * 4, {n, k}));
+    v.push_back(typed_block(small, kF64, lay.times + rk * 8, {n, k}));
+    v.push_back(typed_block(bulk, fdt, lay.feats + rk * row_bytes, {n, k, feat_dim}));
+    v.push_back(typed_block(small, kBool, lay.mask + rk, {n, k}));
+    if (d_t > 0) v.push_back(typed_block(bulk, kF32, lay.te + rk * d_t * 4, {n, k, d_t}));
+    if (eids) v.push_back(typed_block(small, kI64, lay.eids + rk * 8, {n, k}));
+  }
+  void co_out(std::vector<at::Tensor>& v) const {
+    v.push_back(typed_block(small, kI32, lay.coa, {co_rows, co_len, 2}));
+    v.push_back(typed_block(small, kI32, lay.coc, {co_rows, co_len, 2}));
+    v.push_back(typed_block(small, kF32, lay.cop, {co_rows}));
+  }
+};
+
+// Generic launch (TemporalGraph.recent, recent_2hop, co_neighbors, the timing
+// launches of DataPipeline.launch).  Queries arrive as groups (nodes, times,
+// times_per[, valid]) read in place by the kernel.  append_src/dst/time +
+// append_ws (all or none): the caller's next ring batch, planned by the same
+// launch when plannable() allows.
+// Returns (planned, tensors): per group ids, times, feats, mask, [te], [eids],
+// then co_a, co_c, co_pair with co-occurrence.
+py::tuple recent(int64_t ring_addr, int64_t csr_addr, const std::vector<at::Tensor>& gnodes,
+                 const std::vector<at::Tensor>& gtimes, const std::vector<int64_t>& gper,
+                 const std::vector<c10::optional<at::Tensor>>& gvalid, int64_t k,
+                 int64_t feat_dim, at::ScalarType feat_dtype, const c10::optional<at::Tensor>& plan,
+                 int64_t plan_mode, int64_t group, int64_t num_groups, int64_t d_t,
+                 const c10::optional<at::Tensor>& te_w, const c10::optional<at::Tensor>& te_b,
+                 int64_t dt_mode, int64_t co_mode, bool want_eids, const at::Tensor& status,
+                 int64_t stream, int64_t ev0, int64_t ev1,
+                 const c10::optional<at::Tensor>& append_src,
+                 const c10::optional<at::Tensor>& append_dst,
+                 const c10::optional<at::Tensor>& append_time,
+                 const c10::optional<at::Tensor>& append_ws) {
   const size_t ng = gnodes.size();
   if (ng == 0 || ng > TGX_MAX_QUERY_GROUPS || gtimes.size() != ng || gper.size() != ng ||
       (!gvalid.empty() && gvalid.size() != ng))
@@ -116,52 +196,20 @@ std::vector<std::vector<at::Tensor>> recent(
     sizes[g] = n[g].numel();
     Q += sizes[g];
   }
-  if (num_groups < 0) num_groups = (Q + group - 1) / group;
-  // The small outputs (times, edge ids, ids, co-occurrence, mask) share one
-  // allocation, laid out so every offset is a multiple of its element size; the
-  // feature rows and encodings, which dominate the bytes, get their own.
-  const int64_t QK = Q * k;
-  const int64_t L = co_mode == TGX_CO_FREQ ? k : k + 1;
-  const int64_t nco = co_mode != TGX_CO_NONE ? num_groups * L * 2 : 0;
-  const int64_t o_eids = QK * 8;
-  const int64_t o_ids = o_eids + (want_eids ? QK * 8 : 0);
-  const int64_t o_coa = o_ids + QK * 4;
-  const int64_t o_coc = o_coa + nco * 4;
-  const int64_t o_cop = o_coc + nco * 4;
-  const int64_t o_msk = o_cop + (co_mode != TGX_CO_NONE ? num_groups * 4 : 0);
-  at::Tensor small = at::empty({o_msk + QK}, at::TensorOptions().device(dev).dtype(at::kByte));
-  at::Tensor tms = typed_block(small, at::kDouble, 0, {Q, k});
-  at::Tensor ids = typed_block(small, at::kInt, o_ids, {Q, k});
-  at::Tensor msk = typed_block(small, at::kBool, o_msk, {Q, k});
-  at::Tensor fts = at::empty({Q, k, feat_dim}, at::TensorOptions().device(dev).dtype(feat_dtype));
-  c10::optional<at::Tensor> eids, te, co_a, co_c, co_pair;
-  if (want_eids) eids = typed_block(small, at::kLong, o_eids, {Q, k});
-  if (d_t > 0) te = at::empty({Q, k, d_t}, at::TensorOptions().device(dev).dtype(at::kFloat));
-  if (co_mode != TGX_CO_NONE) {
-    co_a = typed_block(small, at::kInt, o_coa, {num_groups, L, 2});
-    co_c = typed_block(small, at::kInt, o_coc, {num_groups, L, 2});
-    co_pair = typed_block(small, at::kFloat, o_cop, {num_groups});
-  }
+  const Out out(dev, Q, k, feat_dim, feat_dtype, d_t, want_eids, co_mode, num_groups < 0 ? 0 : num_groups);
   tgx_recent_args a{};
   a.num_queries = Q;
   a.k = static_cast<int32_t>(k);
   a.plan = plan.has_value() ? plan->data_ptr<int32_t>() : nullptr;
+  a.plan_mode = plan.has_value() ? TGX_PLAN_LIST : static_cast<int32_t>(plan_mode);
   a.group = static_cast<int32_t>(group);
-  a.num_groups = num_groups;
-  a.out_ids = ids.data_ptr<int32_t>();
-  a.out_times = tms.data_ptr<double>();
-  a.out_feats = fts.data_ptr();
-  a.out_mask = reinterpret_cast<uint8_t*>(msk.data_ptr<bool>());
-  a.out_eids = eids.has_value() ? eids->data_ptr<int64_t>() : nullptr;
+  a.num_groups = num_groups < 0 ? 0 : num_groups;
+  out.fill(a);
   a.d_t = static_cast<int32_t>(d_t);
   a.te_w = te_w.has_value() ? te_w->data_ptr<float>() : nullptr;
   a.te_b = te_b.has_value() ? te_b->data_ptr<float>() : nullptr;
   a.dt_mode = static_cast<int32_t>(dt_mode);
-  a.out_te = te.has_value() ? te->data_ptr<float>() : nullptr;
   a.co_mode = static_cast<int32_t>(co_mode);
-  a.co_a = co_a.has_value() ? co_a->data_ptr<int32_t>() : nullptr;
-  a.co_c = co_c.has_value() ? co_c->data_ptr<int32_t>() : nullptr;
-  a.co_pair = co_pair.has_value() ? co_pair->data_ptr<float>() : nullptr;
   a.status = status.data_ptr<int32_t>();
   a.num_query_groups = static_cast<int32_t>(ng);
   for (size_t g = 0; g < ng; ++g) {
@@ -193,21 +241,135 @@ std::vector<std::vector<at::Tensor>> recent(
                      reinterpret_cast<const tgx_csr*>(csr_addr), &a,
                      reinterpret_cast<void*>(stream)),
           "tgx_recent");
-  std::vector<std::vector<at::Tensor>> out;
-  out.reserve(8);
-  auto split = [&](const at::Tensor& x) { return split_rows(x, sizes); };
-  out.push_back(split(ids));
-  out.push_back(split(tms));
-  out.push_back(split(fts));
-  out.push_back(split(msk));
-  out.push_back(eids.has_value() ? split(*eids) : std::vector<at::Tensor>{});
-  out.push_back(te.has_value() ? split(*te) : std::vector<at::Tensor>{});
-  if (co_mode != TGX_CO_NONE) out.push_back({*co_a, *co_c, *co_pair});
-  else out.push_back({});
-  if (planned) out.push_back({*append_src});
-  else out.push_back({});
-  return out;
+  std::vector<at::Tensor> res;
+  res.reserve(ng * 6 + 3);
+  int64_t r0 = 0;
+  for (size_t g = 0; g < ng; ++g) {
+    out.group(res, r0, sizes[g]);
+    r0 += sizes[g];
+  }
+  if (out.co) out.co_out(res);
+  return py::make_tuple(planned, std::move(res));
 }
+
+// The 1-hop prepare of one DataPipeline on one graph, configured once: the
+// query groups [src, dst, neg (row-major), neg_src] that the spec asks for,
+// k, the feature layout, the time encoding and the co-occurrence mode.
+// run() takes one batch and returns (planned, tensors) as recent() does, with
+// the groups present in this batch in that order.
+class Prepare {
+ public:
+  Prepare(int64_t ring_addr, int64_t csr_addr, int64_t groups_mask, int64_t k, int64_t feat_dim,
+          at::ScalarType feat_dtype, int64_t d_t, const c10::optional<at::Tensor>& te_w,
+          const c10::optional<at::Tensor>& te_b, int64_t dt_mode, int64_t co_mode, bool want_eids,
+          int64_t qpw, const at::Tensor& status)
+      : ring_(ring_addr), csr_(csr_addr), mask_(groups_mask), k_(k), feat_dim_(feat_dim),
+        feat_dtype_(feat_dtype), d_t_(d_t), te_w_(te_w), te_b_(te_b), dt_mode_(dt_mode),
+        co_mode_(co_mode), want_eids_(want_eids), qpw_(qpw), status_(status),
+        dev_(status.device()) {
+    if (k < 1 || k > TGX_MAX_K) throw std::invalid_argument("Prepare: k outside [1, TGX_MAX_K]");
+    if (co_mode != TGX_CO_NONE && (groups_mask & 3) != 3)
+      throw std::invalid_argument("Prepare: co-occurrence needs the src and dst groups");
+  }
+
+  py::tuple run(const at::Tensor& src, const at::Tensor& dst, const at::Tensor& time,
+                const c10::optional<at::Tensor>& neg, const c10::optional<at::Tensor>& neg_src,
+                int64_t stream, const c10::optional<at::Tensor>& append_ws) const {
+    const int64_t b = src.size(0);
+    if (dst.size(0) != b || time.size(0) != b)
+      throw std::invalid_argument("prepare: src, dst and time must have the same length");
+    at::Tensor tt = as_dev(flat(time), at::kDouble, dev_);
+    at::Tensor gn[TGX_MAX_QUERY_GROUPS];
+    int32_t per[TGX_MAX_QUERY_GROUPS];
+    int ng = 0;
+    if (mask_ & 1) {
+      gn[ng] = as_dev(flat(src), at::kLong, dev_);
+      per[ng++] = 1;
+    }
+    if (mask_ & 2) {
+      gn[ng] = as_dev(flat(dst), at::kLong, dev_);
+      per[ng++] = 1;
+    }
+    if ((mask_ & 4) && neg.has_value()) {
+      // a (b, n) block is read row-major: n queries per event
+      const int64_t p = neg->dim() > 1 ? neg->size(1) : 1;
+      if (neg->numel() != b * p) throw std::invalid_argument("prepare: neg must hold b x n nodes");
+      gn[ng] = as_dev(flat(*neg), at::kLong, dev_);
+      per[ng++] = static_cast<int32_t>(p);
+    }
+    if ((mask_ & 8) && neg_src.has_value()) {
+      if (neg_src->numel() != b) throw std::invalid_argument("prepare: neg_src must hold b nodes");
+      gn[ng] = as_dev(flat(*neg_src), at::kLong, dev_);
+      per[ng++] = 1;
+    }
+    int64_t Q = 0;
+    int G = 0;
+    for (int g = 0; g < ng; ++g) {
+      Q += b * per[g];
+      G += per[g];
+    }
+    // event-major groups when the pair must meet in one workgroup
+    const bool events = co_mode_ != TGX_CO_NONE;
+    if (events && G > TGX_MAX_GROUP)
+      throw std::invalid_argument("prepare: " + std::to_string(G) +
+                                  " queries per event exceed the fused group limit");
+    const Out out(dev_, Q, k_, feat_dim_, feat_dtype_, d_t_, want_eids_, co_mode_, b);
+    tgx_recent_args a{};
+    a.num_queries = Q;
+    a.k = static_cast<int32_t>(k_);
+    a.plan_mode = events ? TGX_PLAN_EVENTS : TGX_PLAN_TILES;
+    a.group = events ? G : static_cast<int32_t>(qpw_);
+    a.num_groups = events ? b : 0;
+    out.fill(a);
+    a.d_t = static_cast<int32_t>(d_t_);
+    a.te_w = te_w_.has_value() ? te_w_->data_ptr<float>() : nullptr;
+    a.te_b = te_b_.has_value() ? te_b_->data_ptr<float>() : nullptr;
+    a.dt_mode = static_cast<int32_t>(dt_mode_);
+    a.co_mode = static_cast<int32_t>(co_mode_);
+    a.status = status_.data_ptr<int32_t>();
+    a.num_query_groups = ng;
+    const double* tp = tt.data_ptr<double>();
+    for (int g = 0; g < ng; ++g) {
+      a.query_groups[g].nodes = gn[g].data_ptr();
+      a.query_groups[g].times = tp;
+      a.query_groups[g].count = b * per[g];
+      a.query_groups[g].times_per = per[g];
+    }
+    const bool planned = append_ws.has_value() && ring_ != 0 && plannable(src, dst, time, dev_);
+    if (planned) {
+      a.append_src = src.data_ptr<int64_t>();
+      a.append_dst = dst.data_ptr<int64_t>();
+      a.append_time = time.data_ptr<double>();
+      a.append_b = b;
+      a.append_workspace = append_ws->data_ptr();
+      a.append_workspace_bytes = static_cast<size_t>(append_ws->numel());
+    }
+    if (Q > 0 || a.append_b > 0)
+      check(tgx_recent(reinterpret_cast<const tgx_ring*>(ring_),
+                       reinterpret_cast<const tgx_csr*>(csr_), &a, reinterpret_cast<void*>(stream)),
+            "tgx_recent");
+    std::vector<at::Tensor> res;
+    res.reserve(ng * 6 + 3);
+    int64_t r0 = 0;
+    for (int g = 0; g < ng; ++g) {
+      out.group(res, r0, b * per[g]);
+      r0 += b * per[g];
+    }
+    if (out.co) out.co_out(res);
+    return py::make_tuple(planned, std::move(res));
+  }
+
+ private:
+  int64_t ring_, csr_, mask_, k_, feat_dim_;
+  at::ScalarType feat_dtype_;
+  int64_t d_t_;
+  c10::optional<at::Tensor> te_w_, te_b_;
+  int64_t dt_mode_, co_mode_;
+  bool want_eids_;
+  int64_t qpw_;
+  at::Tensor status_;
+  at::Device dev_;
+};
 
 void ring_append(int64_t ring_addr, const at::Tensor& src, const at::Tensor& dst,
                  const at::Tensor& time, const c10::optional<at::Tensor>& feat,
@@ -261,7 +423,12 @@ void ring_discard(int64_t ring_addr, const at::Tensor& src, const at::Tensor& ds
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
-  m.def("recent", &recent, "allocate outputs, launch tgx_recent, return per-group views");
+  m.def("recent", &recent, "allocate outputs, launch tgx_recent, return (planned, tensors)");
+  py::class_<Prepare>(m, "Prepare")
+      .def(py::init<int64_t, int64_t, int64_t, int64_t, int64_t, at::ScalarType, int64_t,
+                    const c10::optional<at::Tensor>&, const c10::optional<at::Tensor>&, int64_t,
+                    int64_t, bool, int64_t, const at::Tensor&>())
+      .def("run", &Prepare::run, "one 1-hop prepare launch: (planned, tensors)");
   m.def("ring_append", &ring_append, "launch tgx_ring_append on one batch");
   m.def("ring_plan", &ring_plan, "launch tgx_ring_plan (first half of an append)");
   m.def("ring_commit", &ring_commit, "launch tgx_ring_commit (second half of an append)");

@@ -41,9 +41,7 @@
 
 #include <cstdio>
 #include <cstdlib>
-#include <map>
 #include <mutex>
-#include <tuple>
 
 #include "tgx_cos.h"
 #include "tgx_ring_plan.h"
@@ -117,6 +115,13 @@ struct Params {
   // fused ring plan: workgroups [0, plan_blocks) plan the caller's next batch
   PlanParams pl;
   int plan_blocks;
+  int plan_mode;  // TGX_PLAN_*
+  // event-major plan over b events: query slot j of event g is
+  // b * before_j + g * per_j + index_j, with 12 bits per slot in ev_code
+  // (before_j: queries per event of the earlier query groups, per_j: of this
+  // group, index_j: the slot's index among them)
+  uint64_t ev_code[2];
+  int64_t ev_b;
 };
 
 template <int VEC>
@@ -219,8 +224,18 @@ __device__ __forceinline__ int64_t wave_lower_bound(const double* __restrict__ t
   return lo + __popcll(__ballot(pr));
 }
 
+// Query j of plan group g (-1: none).  Event-major groups: group g is event g,
+// and its j-th query is, for each query group in order, one of that group's
+// times_per queries of event g; every query group holds b x times_per queries,
+// so the query is b * before + g * per + index with the slot's three small
+// constants decoded from ev_code by shifts.
 __device__ __forceinline__ int64_t query_of(const Params& P, int64_t g, int j) {
   if (j >= P.G) return -1;
+  if (P.plan_mode == TGX_PLAN_EVENTS) {
+    const uint64_t w = j < 5 ? P.ev_code[0] >> (12 * j) : P.ev_code[1] >> (12 * (j - 5));
+    const int before = static_cast<int>(w & 15u), per = static_cast<int>((w >> 4) & 15u);
+    return P.ev_b * before + g * per + static_cast<int>((w >> 8) & 15u);
+  }
   const int64_t slot = g * P.G + j;
   const int64_t q = P.plan != nullptr ? static_cast<int64_t>(P.plan[slot]) : slot;
   return (q >= 0 && q < P.Q) ? q : -1;
@@ -459,7 +474,7 @@ void recent_fused(Params P) {
   const int qs = wv / split;
   const int part = wv - qs * split;
   int64_t q;
-  if (P.plan != nullptr) {
+  if (P.plan_mode != TGX_PLAN_TILES) {
     q = query_of(P, g, qs);
   } else {
     const int64_t t = g * (blockDim.x / kWave / split) + qs;
@@ -745,85 +760,93 @@ void recent_fused(Params P) {
   }
 }
 
-// stand-alone co-occurrence (FREQ) over id rows: one wavefront per pair
+// stand-alone co-occurrence (FREQ) over id rows: one wavefront per pair.  A
+// position is valid by its mask byte, or without masks when its id is not -1;
+// counts cover valid positions only (an id of -2^31 marks an invalid one in LDS:
+// valid ids are compared only against valid ids)
 __global__ __launch_bounds__(64) void co_occurrence_rows(const int32_t* __restrict__ a_ids,
                                                          const int32_t* __restrict__ c_ids,
+                                                         const uint8_t* __restrict__ a_mask,
+                                                         const uint8_t* __restrict__ c_mask,
                                                          int64_t pairs, int K,
                                                          int32_t* __restrict__ a_cnt,
                                                          int32_t* __restrict__ c_cnt,
                                                          float* __restrict__ pair_count) {
   extern __shared__ int32_t rows[];
-  int32_t* A = rows;
-  int32_t* Cc = rows + K;
+  int32_t* A = rows;             // [K] ids
+  int32_t* Cc = rows + K;        // [K] ids
+  int32_t* Av = rows + 2 * K;    // [K] validity
+  int32_t* Cv = rows + 3 * K;
   const int64_t g = blockIdx.x;
   const int lane = threadIdx.x;
   for (int i = lane; i < K; i += kWave) {
-    A[i] = a_ids[g * K + i];
-    Cc[i] = c_ids[g * K + i];
+    const int32_t x = a_ids[g * K + i];
+    const int32_t y = c_ids[g * K + i];
+    A[i] = x;
+    Cc[i] = y;
+    Av[i] = a_mask != nullptr ? (a_mask[g * K + i] != 0) : (x != -1);
+    Cv[i] = c_mask != nullptr ? (c_mask[g * K + i] != 0) : (y != -1);
   }
   __syncthreads();
   int pc = 0;
   for (int i0 = 0; i0 < K; i0 += kWave) {
     const int i = i0 + lane;
     int aa = 0, ac = 0, ca = 0, cc = 0;
-    int32_t x = -1, y = -1;
+    bool xv = false;
     if (i < K) {
-      x = A[i];
-      y = Cc[i];
+      const int32_t x = A[i], y = Cc[i];
+      xv = Av[i] != 0;
+      const bool yv = Cv[i] != 0;
       for (int j = 0; j < K; ++j) {
         const int32_t aj = A[j], cj = Cc[j];
-        aa += aj == x;
-        ac += cj == x;
-        ca += aj == y;
-        cc += cj == y;
+        const bool ajv = Av[j] != 0, cjv = Cv[j] != 0;
+        aa += ajv && aj == x;
+        ac += cjv && cj == x;
+        ca += ajv && aj == y;
+        cc += cjv && cj == y;
       }
-      if (x == -1) aa = ac = 0;
-      if (y == -1) ca = cc = 0;
+      if (!xv) aa = ac = 0;
+      if (!yv) ca = cc = 0;
       a_cnt[(g * K + i) * 2 + 0] = aa;
       a_cnt[(g * K + i) * 2 + 1] = ac;
       c_cnt[(g * K + i) * 2 + 0] = ca;
       c_cnt[(g * K + i) * 2 + 1] = cc;
     }
-    pc += __popcll(__ballot(i < K && x != -1 && ac > 0));
+    pc += __popcll(__ballot(i < K && xv && ac > 0));
   }
   if (lane == 0 && pair_count != nullptr) pair_count[g] = static_cast<float>(pc);
 }
 
 int round16(int x) { return (x + 15) & ~15; }
 
-// Workgroups of `kern` (threads, lds bytes) resident on the current device at
-// once: CUs x occupancy, cached per (device, kernel, threads, lds).
-int resident_groups(const void* kern, int threads, size_t lds, int* out) {
-  static std::mutex mu;
-  static std::map<std::tuple<int, const void*, int, size_t>, int> cache;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return fail(TGX_ERR_HIP, "tgx_recent: hipGetDevice failed");
-  const auto key = std::make_tuple(dev, kern, threads, lds);
-  std::lock_guard<std::mutex> lock(mu);
-  auto it = cache.find(key);
-  if (it != cache.end()) {
-    *out = it->second;
-    return TGX_OK;
-  }
-  (void)hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-  int cus = 0, per_cu = 0;
-  hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, lds);
-  if (e != hipSuccess) return fail(TGX_ERR_HIP, "tgx_recent: occupancy query: %s", hipGetErrorString(e));
-  const int n = (cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1);
-  cache.emplace(key, n);
-  *out = n;
-  return TGX_OK;
-}
-
 }  // namespace
 }  // namespace tgx
 
 using namespace tgx;
 
-extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args* a,
-                          void* stream_) {
-  hipStream_t stream = static_cast<hipStream_t>(stream_);
+namespace tgx {
+namespace {
+
+// Launch configuration of one tgx_recent call: kernel parameters, grid and the
+// fused plan (see tgx_recent_launch_shape for the reported fields).
+struct Launch {
+  Params P;
+  PlanParams pl;
+  bool want_plan = false;
+  bool fuse_plan = false;
+  bool empty = false;  // no queries: only the plan (if any) runs
+  int64_t blocks = 0;
+  int threads = 0;
+  size_t lds = 0;
+  int qslots = 0;
+  int vec = 2;
+  int nreg = 0;
+};
+
+int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args* a, Launch& L) {
+  L = Launch{};
+  Params& P = L.P;
+  P = Params{};
   if (a == nullptr) return fail(TGX_ERR_ARG, "tgx_recent: args is NULL");
   if (a->num_queries < 0 || a->num_groups < 0)
     return fail(TGX_ERR_ARG, "tgx_recent: negative query/group count");
@@ -833,26 +856,31 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
     return fail(TGX_ERR_LIMIT, "tgx_recent: group=%d outside [1, %d]", a->group, TGX_MAX_GROUP);
   if (a->num_groups >= (int64_t(1) << 31))
     return fail(TGX_ERR_LIMIT, "tgx_recent: too many groups");
+  const int mode = a->plan != nullptr ? TGX_PLAN_LIST : a->plan_mode;
+  if (mode != TGX_PLAN_TILES && mode != TGX_PLAN_EVENTS && mode != TGX_PLAN_LIST)
+    return fail(TGX_ERR_ARG, "tgx_recent: unknown plan_mode %d", a->plan_mode);
+  if (mode == TGX_PLAN_LIST && a->plan == nullptr)
+    return fail(TGX_ERR_ARG, "tgx_recent: TGX_PLAN_LIST needs a plan array");
   // the caller's next ring batch, planned in this launch (or on its own)
-  PlanParams pl{};
-  const bool want_plan = a->append_b != 0;
-  if (want_plan) {
+  L.want_plan = a->append_b != 0;
+  if (L.want_plan) {
     if (ring == nullptr) return fail(TGX_ERR_ARG, "tgx_recent: an append plan needs the ring");
     const int rc = plan_setup("tgx_recent", ring, a->append_src, a->append_dst, a->append_time,
-                              a->append_b, a->append_workspace, a->append_workspace_bytes, pl);
+                              a->append_b, a->append_workspace, a->append_workspace_bytes, L.pl);
     if (rc != TGX_OK) return rc;
   }
-  if (a->num_queries == 0 || a->num_groups == 0) return want_plan ? launch_plan(pl, stream) : TGX_OK;
+  const int64_t ngroups_eff = mode == TGX_PLAN_TILES ? 1 : a->num_groups;
+  if (a->num_queries == 0 || ngroups_eff == 0) {
+    L.empty = true;
+    return TGX_OK;
+  }
   if (a->num_query_groups < 0 || a->num_query_groups > TGX_MAX_QUERY_GROUPS)
     return fail(TGX_ERR_LIMIT, "tgx_recent: %d query groups outside [0, %d]", a->num_query_groups,
                 TGX_MAX_QUERY_GROUPS);
   if ((a->num_query_groups == 0 && (a->nodes == nullptr || a->times == nullptr)) ||
       a->out_ids == nullptr || a->out_times == nullptr || a->out_mask == nullptr)
     return fail(TGX_ERR_ARG, "tgx_recent: nodes/times/out_ids/out_times/out_mask must not be NULL");
-  if (a->plan == nullptr && a->num_groups * a->group < a->num_queries)
-    return fail(TGX_ERR_ARG, "tgx_recent: num_groups*group < num_queries without a plan");
 
-  Params P{};
   int feat_dim = -1, dtype = -1;
   if (ring != nullptr) {
     if (ring->slots < 1 || ring->slots > TGX_MAX_SLOTS)
@@ -908,6 +936,7 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
   P.ngroups = a->num_query_groups;
   {
     int64_t off = 0;
+    int per_event = 0;
     for (int g = 0; g < a->num_query_groups; ++g) {
       const tgx_query_group& qg = a->query_groups[g];
       if (qg.count < 0 || qg.times_per < 1 || (qg.count > 0 && (qg.nodes == nullptr || qg.times == nullptr)) ||
@@ -920,15 +949,39 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
       P.gdiv[g] = qg.times_per;
       P.goff[g] = off;
       off += qg.count;
+      per_event += qg.times_per;
+      if (mode == TGX_PLAN_EVENTS && qg.count != a->num_groups * qg.times_per)
+        return fail(TGX_ERR_ARG, "tgx_recent: event-major plan: query group %d holds %lld queries, "
+                    "not num_groups x times_per = %lld", g, (long long)qg.count,
+                    (long long)(a->num_groups * qg.times_per));
     }
-    P.goff[a->num_query_groups] = off;
+    for (int g = a->num_query_groups; g <= TGX_MAX_QUERY_GROUPS; ++g) P.goff[g] = off;
     if (a->num_query_groups > 0 && off != a->num_queries)
       return fail(TGX_ERR_ARG, "tgx_recent: query groups hold %lld queries, num_queries is %lld",
                   (long long)off, (long long)a->num_queries);
+    if (mode == TGX_PLAN_EVENTS && (a->num_query_groups == 0 || per_event != a->group))
+      return fail(TGX_ERR_ARG, "tgx_recent: event-major plan needs query groups whose times_per "
+                  "sum to group (%d)", a->group);
+    if (mode == TGX_PLAN_EVENTS) {
+      // every query group holds exactly num_groups x times_per queries (checked
+      // above), so slot j of event g < num_groups is always a query
+      int j = 0, before = 0;
+      P.ev_code[0] = P.ev_code[1] = 0;
+      P.ev_b = a->num_groups;
+      for (int g = 0; g < a->num_query_groups; ++g) {
+        const int per = a->query_groups[g].times_per;
+        for (int i = 0; i < per; ++i, ++j) {
+          const uint64_t c = static_cast<uint64_t>(before | (per << 4) | (i << 8));
+          P.ev_code[j < 5 ? 0 : 1] |= c << (12 * (j < 5 ? j : j - 5));
+        }
+        before += per;
+      }
+    }
   }
   P.Q = a->num_queries;
   P.K = a->k;
   P.plan = a->plan;
+  P.plan_mode = mode;
   P.G = a->group;
   P.o_ids = a->out_ids;
   P.o_times = a->out_times;
@@ -951,6 +1004,9 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
     return fail(TGX_ERR_ARG, "tgx_recent: unknown co_mode %d", a->co_mode);
   if (a->co_mode != TGX_CO_NONE && (a->group < 2 || a->co_a == nullptr || a->co_c == nullptr))
     return fail(TGX_ERR_ARG, "tgx_recent: co-occurrence needs group >= 2 and co_a/co_c");
+  if (a->co_mode != TGX_CO_NONE && mode == TGX_PLAN_TILES)
+    return fail(TGX_ERR_ARG, "tgx_recent: co-occurrence pairs queries 0 and 1 of a plan group: it "
+                "needs TGX_PLAN_EVENTS or a plan array");
   P.co_mode = a->co_mode;
   P.co_a = a->co_a;
   P.co_c = a->co_c;
@@ -965,12 +1021,12 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
   // Queries per wave.  Packing m = 64 / Bp queries into sub-groups of Bp >= B
   // lanes (Bp at least 16, the wave's LDS within 12 KB) pays off only when the
   // rows ride in registers and the batch has more queries than the device has
-  // wave slots (one round of waves instead of two); otherwise, and with a plan,
-  // one query per wave keeps the most waves in flight.
+  // wave slots (one round of waves instead of two); otherwise, and with plan
+  // groups, one query per wave keeps the most waves in flight.
   const bool small_rows = P.B > 0 && a->out_feats != nullptr && P.row_bytes > 0 &&
                           P.row_bytes <= 64 && P.row_bytes % 16 == 0;
   int lg = 6;
-  if (a->plan == nullptr && small_rows && a->num_queries > kPackMinQueries) {
+  if (mode == TGX_PLAN_TILES && small_rows && a->num_queries > kPackMinQueries) {
     lg = 4;
     while ((1 << lg) < P.B) ++lg;
     while (lg < 6 && wave_lds(kWave >> lg) > 12 * 1024) ++lg;
@@ -991,24 +1047,26 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
   // waves share each query's outputs; and up to 8 while each wave's share of a
   // query's output bytes stays at least kSplitBytes, so a grid of long copies
   // (large rows, large K) ends with a shorter tail of lone waves.  A workgroup
-  // holds at most kMaxWaves waves (the kernel's launch bound): the plan group
-  // times split, else 8 / split query slots.
+  // holds at most kMaxWaves waves (the kernel's launch bound): its query slots
+  // (the plan group, or `group` consecutive tiles) times split.
+  const int qwant = mode != TGX_PLAN_TILES ? a->group : 1;
   int split = 1;
-  const int gmin = a->plan != nullptr ? a->group : 1;
   if (P.m == 1) {
-    while (split < 8 && a->num_queries * (split * 2) <= kPackMinQueries && gmin * split * 2 <= kMaxWaves)
+    while (split < 8 && a->num_queries * (split * 2) <= kPackMinQueries && qwant * split * 2 <= kMaxWaves)
       split *= 2;
     const int64_t qbytes = static_cast<int64_t>(K) * (P.row_bytes + 4 * a->d_t + 13);
-    while (split < 8 && qbytes / (split * 2) >= kSplitBytes && gmin * split * 2 <= kMaxWaves)
+    while (split < 8 && qbytes / (split * 2) >= kSplitBytes && qwant * split * 2 <= kMaxWaves)
       split *= 2;
   }
   P.split = split;
-  const int qslots = a->plan != nullptr ? a->group : (split > 1 ? kMaxWaves / split : 4);
+  // tiles: `group` query slots per workgroup, fewer when split waves fill it
+  int qslots = a->group;
+  if (mode == TGX_PLAN_TILES && qslots * split > kMaxWaves) qslots = kMaxWaves / split;
   const int waves = qslots * split;
   if (waves < 1 || waves > kMaxWaves)
     return fail(TGX_ERR_LIMIT, "tgx_recent: %d wavefronts per workgroup outside [1, %d]", waves, kMaxWaves);
   int64_t nblocks = a->num_groups;
-  if (a->plan == nullptr) {
+  if (mode == TGX_PLAN_TILES) {
     const int64_t ntiles = (a->num_queries + P.m - 1) / P.m;
     nblocks = (ntiles + qslots - 1) / qslots;
   }
@@ -1023,6 +1081,13 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
   else if (P.row_bytes % 4 == 0 && (!fe || (al(P.r_feats, 3) && al(P.c_feats, 3) && al(P.o_feats, 3))))
     vec = 4;
   P.nch = static_cast<int>(P.row_bytes / vec);
+  // FastDiv(n) is exact for x * n < 2^32; its largest dividends: K * nch
+  // feature chunks (divided by nch), m*K*d_t encodings (by d_t or d_t / 4) and
+  // m*K positions (by K)
+  if (static_cast<uint64_t>(K) * static_cast<uint64_t>(P.nch) * static_cast<uint64_t>(P.nch) >=
+      (uint64_t(1) << 32))
+    return fail(TGX_ERR_LIMIT, "tgx_recent: k=%d with %lld-byte rows (%d chunks of %d bytes) exceeds "
+                "the kernel's index range", K, (long long)P.row_bytes, P.nch, vec);
   P.fd_k = FastDiv::magic(static_cast<uint32_t>(P.K));
   P.fd_q = FastDiv::magic(static_cast<uint32_t>(P.d_t / 4));
   P.fd_d = FastDiv::magic(static_cast<uint32_t>(P.d_t));
@@ -1031,18 +1096,34 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
   int nreg = 0;
   if (vec == 16 && fe && P.B > 0) nreg = P.nch <= 2 ? 2 : (P.nch <= 4 ? 4 : 0);
 
+  // fused plan: one plan workgroup per blockDim entries, dispatched first
+  L.fuse_plan = L.want_plan && plan_fused_ok(L.pl);
+  P.pl = L.pl;
+  P.plan_blocks = L.fuse_plan ? static_cast<int>((L.pl.n + kWave * waves - 1) / (kWave * waves)) : 0;
+  L.lds = L.fuse_plan ? std::max(lds, sizeof(PlanLds)) : lds;
+  L.blocks = nblocks + P.plan_blocks;
+  if (L.blocks >= (int64_t(1) << 31)) return fail(TGX_ERR_LIMIT, "tgx_recent: grid too large");
+  L.threads = kWave * waves;
+  L.qslots = qslots;
+  L.vec = vec;
+  L.nreg = nreg;
+  return TGX_OK;
+}
+
+}  // namespace
+}  // namespace tgx
+
+extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args* a,
+                          void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  Launch L;
+  int rc = setup_recent(ring, csr, a, L);
+  if (rc != TGX_OK) return rc;
+  if (L.empty) return L.want_plan ? launch_plan(L.pl, stream) : TGX_OK;
   hipEvent_t ev0 = static_cast<hipEvent_t>(a->timing_start);
   hipEvent_t ev1 = static_cast<hipEvent_t>(a->timing_stop);
   if ((ev0 == nullptr) != (ev1 == nullptr))
     return fail(TGX_ERR_ARG, "tgx_recent: timing_start and timing_stop must both be set or both NULL");
-
-  // fused plan: one plan workgroup per blockDim entries, dispatched first
-  const bool fuse_plan = want_plan && plan_fused_ok(pl);
-  P.pl = pl;
-  P.plan_blocks = fuse_plan ? static_cast<int>((pl.n + kWave * waves - 1) / (kWave * waves)) : 0;
-  const size_t lds_launch = fuse_plan ? std::max(lds, sizeof(PlanLds)) : lds;
-  const dim3 grid(static_cast<unsigned>(nblocks + P.plan_blocks));
-  const dim3 block(kWave * waves);
   static std::once_flag attr_once;
   std::call_once(attr_once, [] {
     const void* fns[] = {reinterpret_cast<const void*>(recent_fused<16, 0>),
@@ -1054,32 +1135,52 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
       (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     (void)hipGetLastError();
   });
+  const dim3 grid(static_cast<unsigned>(L.blocks));
+  const dim3 block(static_cast<unsigned>(L.threads));
   auto launch = [&](auto kernel) {
     if (ev0 != nullptr)
-      hipExtLaunchKernelGGL(kernel, grid, block, lds_launch, stream, ev0, ev1, 0, P);
+      hipExtLaunchKernelGGL(kernel, grid, block, L.lds, stream, ev0, ev1, 0, L.P);
     else
-      hipLaunchKernelGGL(kernel, grid, block, lds_launch, stream, P);
+      hipLaunchKernelGGL(kernel, grid, block, L.lds, stream, L.P);
   };
-  if (vec == 16) {
-    if (nreg == 2)
+  if (L.vec == 16) {
+    if (L.nreg == 2)
       launch(recent_fused<16, 2>);
-    else if (nreg == 4)
+    else if (L.nreg == 4)
       launch(recent_fused<16, 4>);
     else
       launch(recent_fused<16, 0>);
-  } else if (vec == 4) {
+  } else if (L.vec == 4) {
     launch(recent_fused<4, 0>);
   } else {
     launch(recent_fused<2, 0>);
   }
-  const int rc = check_launch("recent_fused");
-  if (rc != TGX_OK || !want_plan || fuse_plan) return rc;
-  return launch_plan(pl, stream);  // batches beyond the fused plan's size
+  rc = check_launch("recent_fused");
+  if (rc != TGX_OK || !L.want_plan || L.fuse_plan) return rc;
+  return launch_plan(L.pl, stream);  // batches beyond the fused plan's size
 }
 
-extern "C" int tgx_co_occurrence(const int32_t* a_ids, const int32_t* c_ids, int64_t pairs,
-                                 int32_t k, int32_t* a_cnt, int32_t* c_cnt, float* pair_count,
-                                 void* stream_) {
+extern "C" int tgx_recent_launch_shape(const tgx_ring* ring, const tgx_csr* csr,
+                                       const tgx_recent_args* a, int64_t shape[8]) {
+  if (shape == nullptr) return fail(TGX_ERR_ARG, "tgx_recent_launch_shape: shape is NULL");
+  for (int i = 0; i < 8; ++i) shape[i] = 0;
+  Launch L;
+  const int rc = setup_recent(ring, csr, a, L);
+  if (rc != TGX_OK || L.empty) return rc;
+  shape[0] = L.blocks;
+  shape[1] = L.threads;
+  shape[2] = static_cast<int64_t>(L.lds);
+  shape[3] = L.P.m;
+  shape[4] = L.P.split;
+  shape[5] = static_cast<int64_t>(L.qslots) * L.P.m;
+  shape[6] = L.P.plan_blocks;
+  shape[7] = L.vec;
+  return TGX_OK;
+}
+
+extern "C" int tgx_co_occurrence(const int32_t* a_ids, const int32_t* c_ids, const uint8_t* a_mask,
+                                 const uint8_t* c_mask, int64_t pairs, int32_t k, int32_t* a_cnt,
+                                 int32_t* c_cnt, float* pair_count, void* stream_) {
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   if (pairs < 0 || k < 0) return fail(TGX_ERR_ARG, "tgx_co_occurrence: negative size");
   if (k > 4096) return fail(TGX_ERR_LIMIT, "tgx_co_occurrence: k=%d above 4096", k);
@@ -1088,7 +1189,7 @@ extern "C" int tgx_co_occurrence(const int32_t* a_ids, const int32_t* c_ids, int
   if (a_ids == nullptr || c_ids == nullptr || a_cnt == nullptr || c_cnt == nullptr)
     return fail(TGX_ERR_ARG, "tgx_co_occurrence: NULL pointer");
   hipLaunchKernelGGL(co_occurrence_rows, dim3(static_cast<unsigned>(pairs)), dim3(kWave),
-                     2 * k * sizeof(int32_t), stream, a_ids, c_ids, pairs, k, a_cnt, c_cnt,
-                     pair_count);
+                     4 * k * sizeof(int32_t), stream, a_ids, c_ids, a_mask, c_mask, pairs, k, a_cnt,
+                     c_cnt, pair_count);
   return check_launch("co_occurrence_rows");
 }

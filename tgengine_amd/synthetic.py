@@ -26,7 +26,7 @@ from typing import Optional
 import numpy as np
 
 __all__ = ["StreamConfig", "CONFIGS", "gen_batch", "num_batches", "f32_to_bf16_bits",
-           "bf16_bits_to_f32"]
+           "bf16_bits_to_f32", "make_graph", "make_pipeline", "to_raw"]
 
 
 @dataclass(frozen=True)
@@ -204,3 +204,37 @@ def key_multiplier_ok(time: np.ndarray, b: int) -> bool:
     """True when the reference ring sort key is a lexicographic (node, index) key."""
     M = int(float(np.max(time))) + 2
     return M > 2 * b - 1
+
+
+def make_graph(cfg: StreamConfig, device="cuda", track_edge_ids: bool = False):
+    """An empty TemporalGraph laid out for ``cfg`` (ring of cfg.buffer_size slots,
+    the config's feature width and storage dtype)."""
+    import torch
+    from tgengine_amd import TemporalGraph
+    return TemporalGraph(cfg.num_nodes, edge_feat_dim=cfg.feat_dim, device=device,
+                         buffer_size=cfg.buffer_size,
+                         feat_dtype=torch.bfloat16 if cfg.feat_dtype == "bf16" else torch.float32,
+                         track_edge_ids=track_edge_ids)
+
+
+def make_pipeline(cfg: StreamConfig, graph, d_t: int = 100):
+    """The config's DataPipeline: K most recent neighbours of src/dst/neg, a d_t
+    cosine time encoding and, for the co-occurrence configs, per-position counts."""
+    from tgengine_amd import DataPipeline, GatherSpec, NeighborSpec
+    spec = GatherSpec(neighbors=NeighborSpec(k=cfg.k), co_occurrence=cfg.co_occurrence,
+                      time_encoding=d_t)
+    return DataPipeline(spec, graph)
+
+
+def to_raw(cfg: StreamConfig, bt: dict, device="cuda"):
+    """A generated batch as a RawBatch of device tensors (bf16 rows as bf16)."""
+    import torch
+    from tgengine_amd import RawBatch
+    feat = torch.from_numpy(bt["feat"])
+    if cfg.feat_dtype == "bf16":
+        feat = feat.view(torch.bfloat16)
+    return RawBatch(src=torch.from_numpy(bt["src"]).to(device),
+                    dst=torch.from_numpy(bt["dst"]).to(device),
+                    time=torch.from_numpy(bt["time"]).to(device),
+                    edge_feat=feat.to(device),
+                    neg=torch.from_numpy(bt["neg"]).to(device))
