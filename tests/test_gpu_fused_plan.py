@@ -153,6 +153,68 @@ def test_async_pipeline_plans_on_its_prefetch_stream():
     _check_status(g)
 
 
+# spin length of the bounded delay kernels (GPU clock cycles; a few ms)
+SPIN = 20_000_000
+
+
+class _SlowNegatives(_GivenNegatives):
+    """Hands out given negatives after a bounded spin kernel on the current
+    stream, which inside the prefetch thread is the prefetch stream."""
+
+    def sample(self, src, dst, time, graph, edge_indices):
+        torch.cuda._sleep(SPIN)
+        return self.queue.pop(0)
+
+
+def test_async_pipeline_orders_its_streams_under_delays():
+    """The prefetch protocol (reference pipeline/async_pipeline.py:85-139) with
+    bounded delay kernels that make each ordering step necessary:
+
+    * a spin on the caller's stream right before advance(i): the commit of batch
+      i is queued behind it, so prepare(i+1) on the prefetch stream reads the
+      ring before batch i lands unless start_prefetch makes the prefetch stream
+      wait for the caller's stream (AsyncDataPipeline.start_prefetch) -- the
+      neighbours of batch i+1 would then miss batch i's events;
+    * a spin on the prefetch stream before prepare(i+1): its outputs are written
+      late, so the caller's copies (``.cpu()`` on the caller's stream) and the
+      caller's advance(i+1), whose commit reads the plan written on the prefetch
+      stream, see unwritten memory unless get() makes the caller's stream wait
+      for the prefetch stream.
+    The plan handed over by get() (TemporalGraph._adopt_plan) only spares
+    advance() a second wait on the prefetch stream: without it advance() orders
+    itself after the plan's stream on its own (_order_after), so no delay can
+    expose its absence; it is checked here by the plan living on the caller's
+    stream after get()."""
+    cfg = C1
+    g = S.make_graph(cfg)
+    neg = _SlowNegatives()
+    spec = S.make_pipeline(cfg, g).spec
+    ap = AsyncDataPipeline(spec, g, neg)
+    ring = O.Ring.empty(cfg.num_nodes, cfg.buffer_size, cfg.feat_dim, np.float32)
+    w = O.time_weights(100)
+    bts = [gen_batch(cfg, i) for i in range(8)]
+    raws = [S.to_raw(cfg, bt) for bt in bts]
+    caller = torch.cuda.current_stream()
+    neg.queue.append(raws[0].neg)
+    ap.start_prefetch(RawBatch(src=raws[0].src, dst=raws[0].dst, time=raws[0].time,
+                               edge_feat=raws[0].edge_feat))
+    for i, bt in enumerate(bts):
+        rb2, pb = ap.get()
+        if g._plan is not None:
+            assert g._plan.stream == caller.cuda_stream  # handed over to the caller's stream
+        S.compare_prepared(cfg, pb, bt, ring if i > 0 else None, w, f"delayed async batch {i}")
+        torch.cuda._sleep(SPIN)  # the commit of batch i is queued behind this spin
+        g.advance(rb2.src, rb2.dst, rb2.time, rb2.edge_feat)
+        O.ring_advance(ring, bt["src"], bt["dst"], bt["time"], bt["feat"])
+        if i + 1 < len(bts):
+            nxt = raws[i + 1]
+            neg.queue.append(nxt.neg)
+            ap.start_prefetch(RawBatch(src=nxt.src, dst=nxt.dst, time=nxt.time, edge_feat=nxt.edge_feat))
+    torch.cuda.synchronize()
+    _check_ring(g, ring, bts[-1], "delayed async ring")
+    _check_status(g)
+
+
 def test_many_batch_sizes_stay_exact_without_per_shape_state():
     # 70 distinct batch sizes, then a size seen before: the event-major grouping
     # is computed in the kernel, so nothing is cached per batch shape
