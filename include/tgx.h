@@ -209,6 +209,22 @@ int tgx_ring_append(const tgx_ring* ring, const int64_t* src, const int64_t* dst
 size_t tgx_ring_append_workspace_size(int64_t b);
 size_t tgx_ring_scratch_size(int64_t num_nodes);
 
+/* tgx_ring_append with no workspace argument and no allocation: the workspace is
+ * a file-scope device array of tgx_ring_append_static_max_bytes() bytes (2 MiB;
+ * each GPU the library runs on holds its own copy until the process ends),
+ * enough for batches with tgx_ring_append_workspace_size(b) <= that (about
+ * 100,000 events); larger batches return TGX_ERR_LIMIT.  It calls no hipMalloc
+ * or hipFree.  Every call on one GPU shares that GPU's array, so calls that
+ * overlap on one GPU (other streams, other threads) race; calls ordered on one
+ * stream are safe.  The ring's scratch is the caller's, as for tgx_ring_append.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc). */
+int tgx_ring_append_static(const tgx_ring* ring, const int64_t* src, const int64_t* dst,
+                           const double* time, const void* feat, int64_t b, int64_t eid_base,
+                           int32_t* status, void* stream);
+size_t tgx_ring_append_static_max_bytes(void);
+
 /* tgx_ring_append in two halves, so the first can run while other work still
  * reads the ring (the same split of _append_overflow, temporal_graph.py:351-387):
  *   tgx_ring_plan   : per-node counts and the entry lists of the batch, in the

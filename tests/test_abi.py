@@ -256,6 +256,25 @@ def test_ring_plan_commit_discard_argument_checks():
     assert "aligned" in _err()
 
 
+def test_static_append_limits():
+    """tgx_ring_append_static refuses batches beyond its static workspace before
+    touching the device, and an empty batch is a no-op."""
+    L = _lib.lib()
+    cap = L.tgx_ring_append_static_max_bytes()
+    assert cap == 2 << 20
+    ring = _lib.TgxRing(num_nodes=10, slots=4, feat_dim=2, feat_dtype=0, ids=8, times=8, feats=8,
+                        write_pos=8, scratch=8)
+    big = 1
+    while L.tgx_ring_append_workspace_size(big) <= cap:
+        big *= 2
+    assert big > 100_000  # about 100,000 events fit
+    assert L.tgx_ring_append_static(ctypes.byref(ring), 8, 8, 8, None, big, 0, None, None) == 3
+    assert "static workspace" in _err()
+    assert L.tgx_ring_append_static(ctypes.byref(ring), 8, 8, 8, None, -1, 0, None, None) == 1
+    assert L.tgx_ring_append_static(ctypes.byref(ring), 8, 8, 8, None, 0, 0, None, None) == 0
+    assert L.tgx_ring_append_static(None, 8, 8, 8, None, 0, 0, None, None) == 1
+
+
 def test_size_queries():
     L = _lib.lib()
     # per-node counter + 8-entry node list, and 32 control words (16-byte aligned)

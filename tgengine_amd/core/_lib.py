@@ -91,6 +91,9 @@ SIGNATURES = {
     "tgx_ring_discard": (c_i32, [ctypes.POINTER(TgxRing), c_vp, c_vp, c_i64, c_vp, ctypes.c_size_t,
                                  c_vp]),
     "tgx_ring_append_workspace_size": (ctypes.c_size_t, [c_i64]),
+    "tgx_ring_append_static": (c_i32, [ctypes.POINTER(TgxRing), c_vp, c_vp, c_vp, c_vp, c_i64, c_i64,
+                                       c_vp, c_vp]),
+    "tgx_ring_append_static_max_bytes": (ctypes.c_size_t, []),
     "tgx_ring_scratch_size": (ctypes.c_size_t, [c_i64]),
     "tgx_recent": (c_i32, [ctypes.POINTER(TgxRing), ctypes.POINTER(TgxCsr),
                            ctypes.POINTER(TgxRecentArgs), c_vp]),

@@ -44,6 +44,7 @@
 #include "tgx_ring_plan.h"
 
 #include <algorithm>
+#include <mutex>
 
 namespace tgx {
 namespace {
@@ -776,4 +777,59 @@ extern "C" int tgx_ring_discard(const tgx_ring* ring, const int64_t* src, const 
   hipLaunchKernelGGL(append_discard, grid1, dim3(kThreads), 0, static_cast<hipStream_t>(stream_), P,
                      plan_fused_ok(P) ? 1 : 0);
   return check_launch("append_discard");
+}
+
+// ---- tgx_ring_append_static: the workspace in a file-scope device array ----
+namespace tgx {
+namespace {
+
+constexpr size_t kStaticWorkspaceBytes = size_t(2) << 20;  // 2 MiB per GPU
+constexpr int kMaxDevices = 64;
+
+// The static workspace.  Its name is a host-side stand-in: kernels get the
+// device address that hipGetSymbolAddress returns for the current device.
+__device__ __align__(256) uint8_t scratch[kStaticWorkspaceBytes];
+
+std::mutex g_static_mu;
+void* g_static_ptr[kMaxDevices] = {};
+
+// device address of `scratch` on the current device, resolved once per device
+int static_workspace(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(TGX_ERR_HIP, "tgx_ring_append_static: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(TGX_ERR_LIMIT, "tgx_ring_append_static: device %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_static_mu);
+  if (g_static_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(TGX_ERR_HIP, "tgx_ring_append_static: hipGetSymbolAddress: %s", hipGetErrorString(e));
+    g_static_ptr[dev] = p;
+  }
+  *out = g_static_ptr[dev];
+  return TGX_OK;
+}
+
+}  // namespace
+}  // namespace tgx
+
+extern "C" size_t tgx_ring_append_static_max_bytes(void) { return kStaticWorkspaceBytes; }
+
+extern "C" int tgx_ring_append_static(const tgx_ring* ring, const int64_t* src, const int64_t* dst,
+                                      const double* time, const void* feat, int64_t b,
+                                      int64_t eid_base, int32_t* status, void* stream) {
+  if (b < 0) return fail(TGX_ERR_ARG, "tgx_ring_append_static: negative batch size %lld", (long long)b);
+  if (b == 0) return ring == nullptr ? fail(TGX_ERR_ARG, "tgx_ring_append_static: ring is NULL") : TGX_OK;
+  if (b >= (int64_t(1) << 29) || tgx_ring_append_workspace_size(b) > kStaticWorkspaceBytes)
+    return fail(TGX_ERR_LIMIT, "tgx_ring_append_static: %lld events need %zu workspace bytes, the "
+                "static workspace holds %zu", (long long)b,
+                b < (int64_t(1) << 29) ? tgx_ring_append_workspace_size(b) : size_t(0),
+                kStaticWorkspaceBytes);
+  void* ws = nullptr;
+  const int rc = static_workspace(&ws);
+  if (rc != TGX_OK) return rc;
+  return tgx_ring_append(ring, src, dst, time, feat, b, eid_base, ws, kStaticWorkspaceBytes, status,
+                         stream);
 }
