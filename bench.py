@@ -56,6 +56,37 @@ def stage_stream(cfg, first: int, count: int, torch, device):
     return dev, lens, bts
 
 
+def measure_ceilings(torch, device, launch_bytes: int, log) -> dict:
+    """HBM ceilings of plain device kernels: a copy (reads + writes the size) and a
+    store-only fill, at 1 GiB and at the gather launch's byte count, each the best of
+    5 event-timed repetitions after a warm-up."""
+    out = {}
+    for name, nbytes in (("1GiB", 1 << 30), ("launch", max(launch_bytes, 1 << 20))):
+        n = nbytes // 4
+        src = torch.ones(n, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        for kind, fn, moved in (("copy", lambda: dst.copy_(src), 2 * n * 4),
+                                ("store", lambda: dst.fill_(2.0), n * 4)):
+            fn()
+            torch.cuda.synchronize()
+            best = None
+            for _ in range(5):
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+                fn()
+                e1.record()
+                torch.cuda.synchronize()
+                ms = e0.elapsed_time(e1)
+                best = ms if best is None else min(best, ms)
+            out[f"{kind}_{name}"] = {"bytes": moved, "us": best * 1e3, "GB/s": moved / (best * 1e-3) / 1e9}
+            log(f"ceiling {kind} {name}: {moved / 1e6:.1f} MB in {best * 1e3:.1f} us = "
+                f"{moved / (best * 1e-3) / 1e9:.0f} GB/s")
+        del src, dst
+        torch.cuda.synchronize()
+    return out
+
+
 def cpu_model() -> str:
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -157,6 +188,9 @@ def main():
                     help="batches after the timed region whose prepare kernels are timed back to back")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after timing, run a plain device copy of this size (PMC byte calibration)")
+    ap.add_argument("--ceilings", action="store_true",
+                    help="after timing, measure the device's copy and store ceilings (torch copy_ / "
+                         "fill_ of 1 GiB and of the gather's write size) and report them")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only: the fused pipeline path has no multi-GPU mode "
@@ -284,6 +318,10 @@ def main():
         torch.cuda.synchronize()
         del src_buf, dst_buf
 
+    ceilings = None
+    if a.ceilings:
+        ceilings = measure_ceilings(torch, device, int(sum(rbyts) / n_launch) if rbyts else 1 << 27, log)
+
     traffic = None
     pmc = ROOT / "profiles" / f"{cfg.name}_recent_fused_pmc.json"
     if pmc.exists():
@@ -317,6 +355,8 @@ def main():
                                f"batches {W + K}..{total - 1}"},
         "cpu_baseline": cpu,
     }
+    if ceilings is not None:
+        line["ceilings"] = ceilings
     print(json.dumps(line), flush=True)
 
 
