@@ -201,25 +201,62 @@ __device__ __forceinline__ void write_entry_meta(const AppendParams& P, int64_t 
   if (P.eids != nullptr) P.eids[slot] = P.eid_base + e;
 }
 
+// row chunks each thread loads before storing them when it copies kept rows
+constexpr int kKeptDepth = 4;
+
 // copy the kept rows R[0..kept) of node u (row r -> slot (w + kept - 1 - r) % B);
-// threads t = first, first + stride, ... of the caller share the work
+// threads t = first, first + stride, ... of the caller share the work.  Loads
+// and stores share one in-order vmcnt, so every load of a round (the thread's
+// first row's id and time, kKeptDepth row chunks) is issued before its stores:
+// a row of many chunks costs one round trip per kKeptDepth chunks, not per chunk.
 template <int VEC>
 __device__ __forceinline__ void write_kept(const AppendParams& P, const int32_t* R, int64_t u,
                                            int kept, int64_t w, int first, int stride) {
   using V = typename VecT<VEC>::T;
   const int nv = static_cast<int>(P.row_bytes / VEC);
-  for (int r = first; r < kept; r += stride)
-    write_entry_meta(P, R[r], u * P.B + ring_slot(w, kept - 1 - r, P.B));
   const int total = kept * nv;
-  for (int f = first; f < total; f += stride) {
-    const int r = f / nv;
-    const int cch = f - r * nv;
-    const int64_t i = R[r];
-    const int64_t e = i < P.b ? i : i - P.b;
-    const int64_t slot = u * P.B + ring_slot(w, kept - 1 - r, P.B);
-    V* drow = reinterpret_cast<V*>(P.feats + slot * P.row_bytes);
-    drow[cch] = P.feat != nullptr ? reinterpret_cast<const V*>(P.feat + e * P.row_bytes)[cch] : V{};
+  // the thread's first row: id, time, edge id (loaded with the first chunks)
+  int32_t m_id = 0;
+  double m_t = 0.0;
+  int64_t m_slot = -1, m_e = 0;
+  if (first < kept) {
+    const int64_t i = R[first];
+    m_e = i < P.b ? i : i - P.b;
+    m_id = static_cast<int32_t>(i < P.b ? P.dst[m_e] : P.src[m_e]);
+    m_t = P.time[m_e];
+    m_slot = u * P.B + ring_slot(w, kept - 1 - first, P.B);
   }
+  for (int f0 = first; f0 < total || m_slot >= 0; f0 += kKeptDepth * stride) {
+    V v[kKeptDepth];
+    V* dp[kKeptDepth];
+#pragma unroll
+    for (int k = 0; k < kKeptDepth; ++k) {
+      const int f = f0 + k * stride;
+      dp[k] = nullptr;
+      v[k] = V{};
+      if (f < total) {
+        const int r = f / nv;
+        const int cch = f - r * nv;
+        const int64_t i = R[r];
+        const int64_t e = i < P.b ? i : i - P.b;
+        const int64_t slot = u * P.B + ring_slot(w, kept - 1 - r, P.B);
+        dp[k] = reinterpret_cast<V*>(P.feats + slot * P.row_bytes) + cch;
+        if (P.feat != nullptr) v[k] = reinterpret_cast<const V*>(P.feat + e * P.row_bytes)[cch];
+      }
+    }
+    if (m_slot >= 0) {
+      P.ids[m_slot] = m_id;
+      P.times[m_slot] = m_t;
+      if (P.eids != nullptr) P.eids[m_slot] = P.eid_base + m_e;
+      m_slot = -1;
+    }
+#pragma unroll
+    for (int k = 0; k < kKeptDepth; ++k)
+      if (dp[k] != nullptr) *dp[k] = v[k];
+  }
+  // rows beyond the first of this thread (only when kept > stride)
+  for (int r = first + stride; r < kept; r += stride)
+    write_entry_meta(P, R[r], u * P.B + ring_slot(w, kept - 1 - r, P.B));
 }
 
 // one large group (c > 64) by the whole workgroup
@@ -286,6 +323,9 @@ __device__ __forceinline__ void commit_large(const AppendParams& P, int64_t gid,
 
 // singletons (c == 1), written directly: tpe lanes per entry, blocks [0, ga).
 // A group's counter reads c >= 2 or 0 (once its role restored it), never 1.
+// Each lane holds up to kKeptDepth chunks of the row (tpe <= 16 lanes per entry,
+// so 16-byte chunks cover rows up to 1 KB in one round); longer rows continue
+// in rounds of kKeptDepth loads, then stores.
 template <int VEC>
 __device__ __forceinline__ void commit_singletons(const AppendParams& P, int blk) {
   using V = typename VecT<VEC>::T;
@@ -300,19 +340,42 @@ __device__ __forceinline__ void commit_singletons(const AppendParams& P, int blk
   const int64_t e = i < P.b ? i : i - P.b;
   const int64_t u = entry_node(P.src, P.dst, i, P.b);
   const V* srow = reinterpret_cast<const V*>(P.feat + e * P.row_bytes);
-  const V first = (P.feat != nullptr && l < nv) ? srow[l] : V{};
+  V v[kKeptDepth];
+#pragma unroll
+  for (int k = 0; k < kKeptDepth; ++k) {
+    const int c = l + k * tpe;
+    v[k] = (P.feat != nullptr && c < nv) ? srow[c] : V{};
+  }
   int32_t other = 0;
   double tm = 0.0;
   if (l == 0) {
     other = static_cast<int32_t>(i < P.b ? P.dst[e] : P.src[e]);
     tm = P.time[e];
   }
-  if (u < 0 || u >= P.N || P.cnt[u] != 1) return;
+  if (u < 0 || u >= P.N) return;
+  // the counter and the write position in one round trip
+  const int32_t cn = P.cnt[u];
   const int64_t w = P.wp[u];
+  if (cn != 1) return;
   const int64_t slot = u * P.B + ring_slot(w, 0, P.B);
   V* drow = reinterpret_cast<V*>(P.feats + slot * P.row_bytes);
-  if (l < nv) drow[l] = first;
-  for (int c = l + tpe; c < nv; c += tpe) drow[c] = P.feat != nullptr ? srow[c] : V{};
+#pragma unroll
+  for (int k = 0; k < kKeptDepth; ++k) {
+    const int c = l + k * tpe;
+    if (c < nv) drow[c] = v[k];
+  }
+  for (int c0 = l + kKeptDepth * tpe; c0 < nv; c0 += kKeptDepth * tpe) {
+#pragma unroll
+    for (int k = 0; k < kKeptDepth; ++k) {
+      const int c = c0 + k * tpe;
+      v[k] = (P.feat != nullptr && c < nv) ? srow[c] : V{};
+    }
+#pragma unroll
+    for (int k = 0; k < kKeptDepth; ++k) {
+      const int c = c0 + k * tpe;
+      if (c < nv) drow[c] = v[k];
+    }
+  }
   if (l == 0) {
     P.ids[slot] = other;
     P.times[slot] = tm;
@@ -690,7 +753,8 @@ int setup_append(const char* who, const tgx_ring* ring, const int64_t* src, cons
     vec = 4;
   const int64_t nchunks = P.row_bytes / vec;
   int tpe_log2 = 0;
-  while ((int64_t(1) << tpe_log2) < nchunks && tpe_log2 < 6) ++tpe_log2;
+  // lanes per singleton entry: one chunk each up to 16 lanes, then several per lane
+  while ((int64_t(1) << tpe_log2) < nchunks && tpe_log2 < 4) ++tpe_log2;
   P.tpe_log2 = tpe_log2;
   const int64_t epb = kThreads >> tpe_log2;
   P.ga = static_cast<int>((n + epb - 1) / epb);
