@@ -27,7 +27,7 @@
 //            every entry from the top of the batch down, kTopChunk entries at a
 //            time, and ranks the node's entries until the kept ones are found.  Every role
 //            starts its loads before it knows whether it has work, so a role
-//            costs two or three memory round trips.  Workgroup 0 reports the
+//            costs two or three memory round trips.  The first small-group workgroup reports the
 //            diagnostics and clears the other cursor set for the next plan
 //            (two sets alternate).
 // Larger batches: four launches, whose lists are sized after counting.
@@ -457,34 +457,41 @@ __device__ __forceinline__ void load_top(const AppendParams& P, int64_t hi4,
   }
 }
 
-// LDS of the top-down ranking: per row r, bit k of every lane's match count in
-// a ballot per wavefront
+// LDS of the top-down ranking: the match count of every (row, wavefront)
 struct TopLds {
-  uint64_t cb[kTopRows][3][kCommitWaves];
+  int32_t tot[kTopRows][kCommitWaves];
 };
 static_assert(kTopRows * kCommitWaves <= kWave, "one lane per (row, wavefront) count");
+
+// set bits of the wave mask b below this lane
+__device__ __forceinline__ int lanes_below(uint64_t b) {
+  return static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(b >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(b), 0u)));
+}
 
 // One large group (c > kListCap) by the whole workgroup.  Its kept entries are
 // its last kept = min(c, B) in the batch: the plan's node array is read from the
 // top down, kTopChunk entries per step, and the entry with e later entries of
 // node u is ranked from the match counts (matches in earlier steps, earlier
-// rows, lower wavefronts, lower lanes, and this lane's higher entries; every
-// wavefront scans the (row, wavefront) counts itself).  The first step (nd) is loaded by the
-// caller before u is known.  Steps end once B entries are found (kept = B) or
-// the batch is exhausted (kept = c), so the node's counter is not read.
+// rows, lower wavefronts, lower lanes, and this lane's higher entries).  Within
+// a wavefront, three ballots of the bits of every lane's count give the
+// matches of the lower lanes (mbcnt) and the wavefront's total, so only the
+// (row, wavefront) totals pass through LDS.  The first step (nd) is loaded by
+// the caller before u is known.  Steps end once B entries are found (kept = B)
+// or the batch is exhausted (kept = c), so the node's counter is not read.
 template <int VEC>
 __device__ __forceinline__ void fast_large(const AppendParams& P, int64_t u, int4 (&nd)[kTopRows],
                                            int32_t* R, TopLds& T) {
   const int wv = threadIdx.x / kWave;
   const int lane = threadIdx.x & (kWave - 1);
   const int t = threadIdx.x;
-  const uint64_t below = (uint64_t(1) << lane) - 1;
-  const int64_t w = P.wp[u];
   const int32_t u32 = static_cast<int32_t>(u);
   int carry = 0;
   for (int64_t hi4 = (P.n + 3) & ~int64_t(3);;) {  // workgroup-uniform
-    // m4[r] bit s: entry 4q + 3 - s of row r is node u (s = 0 is the highest)
+    // m4[r] bit s: entry 4q + 3 - s of row r is node u (s = 0 is the highest);
+    // below[r]: matches of the lower lanes of this wavefront in row r
     uint32_t m4[kTopRows];
+    int below[kTopRows];
 #pragma unroll
     for (int r = 0; r < kTopRows; ++r) {
       const int64_t top = hi4 - 4 * (static_cast<int64_t>(r) * kThreads + t) - 1;  // 4q + 3
@@ -496,20 +503,20 @@ __device__ __forceinline__ void fast_large(const AppendParams& P, int64_t u, int
       m |= static_cast<uint32_t>(nd[r].x == u32) << 3;
       m4[r] = m;
       const int cnt = __popc(m);
+      int bl = 0, tot = 0;
 #pragma unroll
       for (int k = 0; k < 3; ++k) {
-        const uint64_t bl = __ballot((cnt >> k) & 1);
-        if (lane == 0) T.cb[r][k][wv] = bl;
+        const uint64_t b = __ballot((cnt >> k) & 1);
+        bl += lanes_below(b) << k;
+        tot += __popcll(b) << k;
       }
+      below[r] = bl;
+      if (lane == 0) T.tot[r][wv] = tot;
     }
     __syncthreads();
     // lane l < kTopRows kCommitWaves: the count of (row l / kCommitWaves,
     // wavefront l % kCommitWaves); an exclusive scan in that order gives bases
-    int x = 0;
-    if (lane < kTopRows * kCommitWaves) {
-#pragma unroll
-      for (int k = 0; k < 3; ++k) x += __popcll(T.cb[lane / kCommitWaves][k][lane % kCommitWaves]) << k;
-    }
+    const int x = lane < kTopRows * kCommitWaves ? T.tot[lane / kCommitWaves][lane % kCommitWaves] : 0;
     int incl = x;
 #pragma unroll
     for (int off = 1; off < kTopRows * kCommitWaves; off <<= 1) {
@@ -519,17 +526,11 @@ __device__ __forceinline__ void fast_large(const AppendParams& P, int64_t u, int
     const int step_total = __shfl(incl, kTopRows * kCommitWaves - 1, kWave);
 #pragma unroll
     for (int r = 0; r < kTopRows; ++r) {
-      const int base = carry + __shfl(incl - x, r * kCommitWaves + wv, kWave);
+      int e = carry + __shfl(incl - x, r * kCommitWaves + wv, kWave) + below[r];
       uint32_t m = m4[r];
-      if (m == 0u) continue;
-      int e = base;
-#pragma unroll
-      for (int k = 0; k < 3; ++k) e += __popcll(T.cb[r][k][wv] & below) << k;
       const int64_t top = hi4 - 4 * (static_cast<int64_t>(r) * kThreads + t) - 1;
-      for (; m != 0u; m &= m - 1, ++e) {
-        const int s = __builtin_ctz(m);
-        if (e < P.B) R[e] = static_cast<int32_t>(top - s);
-      }
+      // only ranks below B are kept
+      for (; m != 0u && e < P.B; m &= m - 1, ++e) R[e] = static_cast<int32_t>(top - __builtin_ctz(m));
     }
     carry += step_total;
     hi4 -= kTopChunk;
@@ -538,6 +539,10 @@ __device__ __forceinline__ void fast_large(const AppendParams& P, int64_t u, int
     load_top(P, hi4, nd);
   }
   const int kept = carry < P.B ? carry : P.B;
+  // the write position is loaded here, not with the node: the step loop's
+  // first wait would otherwise wait for it too (one round trip more); here it
+  // shares the round trip of the kept rows' loads
+  const int64_t w = P.wp[u];
   write_kept<VEC>(P, R, u, kept, w, t, kThreads);
   if (t == 0) {
     P.wp[u] = w + kept;
@@ -546,8 +551,37 @@ __device__ __forceinline__ void fast_large(const AppendParams& P, int64_t u, int
   __syncthreads();  // the next group rewrites R
 }
 
+// the plan's cursor word (groups | large counts) of ctl words 8-15 (c0, c1:
+// both cursor sets, phase_next, phase_cur)
+static_assert(kCtlPhaseCur - kCtlFCursor - 4 == 1, "phase_cur is word 1 of c1");
+__device__ __forceinline__ uint64_t plan_cursor(u32x4 c0, u32x4 c1) {
+  const uint32_t ph = c1.y & 1u;
+  return ph == 0 ? (static_cast<uint64_t>(c0.y) << 32 | c0.x) : (static_cast<uint64_t>(c0.w) << 32 | c0.z);
+}
+
+// the first small-group workgroup of a commit (gb >= 1 always), once the
+// cursor words are in: report the plan's diagnostics, clear them, clear the
+// other cursor set (its plan is committed) and hand it to the next plan
+__device__ __forceinline__ void fast_diagnostics(const AppendParams& P, uint32_t phase_cur) {
+  const int ph = static_cast<int>(phase_cur & 1u);
+  const u32x4 dg = *reinterpret_cast<const u32x4*>(P.ctl + kCtlFDiag);
+  const int time_flag = static_cast<int>(ph == 0 ? dg[0] : dg[2]);
+  const int bad = static_cast<int>(ph == 0 ? dg[1] : dg[3]);
+  *reinterpret_cast<uint64_t*>(P.ctl + kCtlFCursor + 2 * (1 - ph)) = 0;
+  P.ctl[kCtlPhaseNext] = 1 - ph;
+  if (P.status != nullptr) {
+    if (bad != 0) atomicAdd(&P.status[TGX_ST_BAD_EVENT_NODE], bad);
+    if (time_flag == 0) atomicAdd(&P.status[TGX_ST_KEY_COLLISION], 1);
+  }
+  P.ctl[kCtlFDiag + 2 * ph] = 0;
+  P.ctl[kCtlFDiag + 2 * ph + 1] = 0;
+}
+
 // blocks [0, ga): singletons; [ga, ga+gb): groups of c <= kListCap, one per
-// wavefront; [ga+gb, ...): larger groups, one per workgroup
+// wavefront; [ga+gb, ...): larger groups, one per workgroup.  The ctl words
+// (cursors, phase) are loaded first, and every role issues its own first loads
+// before it uses them, so they cost one round trip together: loads and their
+// wait counter are in order, and a wait for a younger load is a wait for all.
 template <int VEC>
 __global__ __launch_bounds__(kThreads) void fast_commit(AppendParams P) {
   __shared__ int32_t rows[kCommitWaves][TGX_MAX_SLOTS];
@@ -559,33 +593,16 @@ __global__ __launch_bounds__(kThreads) void fast_commit(AppendParams P) {
   // (this launch writes only the other set and phase_next, which it does not use)
   const u32x4 c0 = *reinterpret_cast<const u32x4*>(P.ctl + kCtlFCursor);
   const u32x4 c1 = *reinterpret_cast<const u32x4*>(P.ctl + kCtlFCursor + 4);
-  const int ph = static_cast<int>(c1[kCtlPhaseCur - kCtlFCursor - 4]) & 1;
-  const uint64_t cur = ph == 0 ? (static_cast<uint64_t>(c0[1]) << 32 | c0[0])
-                               : (static_cast<uint64_t>(c0[3]) << 32 | c0[2]);
-  if (blk == 0 && threadIdx.x == 0) {
-    // both diagnostics pairs (words 16-19) in the same round trip as the cursors
-    const u32x4 dg = *reinterpret_cast<const u32x4*>(P.ctl + kCtlFDiag);
-    const int time_flag = static_cast<int>(ph == 0 ? dg[0] : dg[2]);
-    const int bad = static_cast<int>(ph == 0 ? dg[1] : dg[3]);
-    // the other set belongs to a committed plan: clear it for the next plan
-    *reinterpret_cast<uint64_t*>(P.ctl + kCtlFCursor + 2 * (1 - ph)) = 0;
-    P.ctl[kCtlPhaseNext] = 1 - ph;
-    if (P.status != nullptr) {
-      if (bad != 0) atomicAdd(&P.status[TGX_ST_BAD_EVENT_NODE], bad);
-      if (time_flag == 0) atomicAdd(&P.status[TGX_ST_KEY_COLLISION], 1);
-    }
-    P.ctl[kCtlFDiag + 2 * ph] = 0;
-    P.ctl[kCtlFDiag + 2 * ph + 1] = 0;
-  }
   if (blk < P.ga) {
     commit_singletons<VEC>(P, blk);
   } else if (blk < P.ga + P.gb) {
     // the first group id of this wavefront is read with the cursor (in bounds of
     // the n/2 + 1 list), so a group costs three round trips
-    const int ngroups = field(cur, kFGroups);
     const int gstride = P.gb * kCommitWaves;
     int gid = (blk - P.ga) * kCommitWaves + wv;
     int64_t u = gid <= P.n / 2 ? P.groups[gid] : 0;
+    const int ngroups = field(plan_cursor(c0, c1), kFGroups);
+    if (blk == P.ga && threadIdx.x == 0) fast_diagnostics(P, c1.y);
     for (; gid < ngroups; gid += gstride) {  // wave-uniform
       const int c = P.cnt[u];
       const int64_t w = P.wp[u];
@@ -599,13 +616,13 @@ __global__ __launch_bounds__(kThreads) void fast_commit(AppendParams P) {
   } else {
     // the group's node and the top of the batch are read with the cursor
     // (gid < n / (kListCap + 1) + 1, the large list's length)
-    const int nlarge = field(cur, kFLarge);
     const int gstride = static_cast<int>(gridDim.x) - P.ga - P.gb;
     const int64_t hi4 = (P.n + 3) & ~int64_t(3);
     int gid = blk - P.ga - P.gb;
     int64_t u = P.large[gid];
     int4 nd[kTopRows];
     load_top(P, hi4, nd);
+    const int nlarge = field(plan_cursor(c0, c1), kFLarge);
     for (; gid < nlarge; gid += gstride) {  // workgroup-uniform
       fast_large<VEC>(P, u, nd, rows[0], top);
       if (gid + gstride < nlarge) {
