@@ -486,21 +486,21 @@ __device__ __forceinline__ void fast_large(const AppendParams& P, int64_t u, int
   const int lane = threadIdx.x & (kWave - 1);
   const int t = threadIdx.x;
   const int32_t u32 = static_cast<int32_t>(u);
+  const int n32 = static_cast<int>(P.n);  // < 2^30 entries, so entry indices fit in int
   int carry = 0;
-  for (int64_t hi4 = (P.n + 3) & ~int64_t(3);;) {  // workgroup-uniform
+  for (int hi4 = (n32 + 3) & ~3;;) {  // workgroup-uniform
     // m4[r] bit s: entry 4q + 3 - s of row r is node u (s = 0 is the highest);
     // below[r]: matches of the lower lanes of this wavefront in row r
     uint32_t m4[kTopRows];
     int below[kTopRows];
 #pragma unroll
     for (int r = 0; r < kTopRows; ++r) {
-      const int64_t top = hi4 - 4 * (static_cast<int64_t>(r) * kThreads + t) - 1;  // 4q + 3
-      uint32_t m = 0;
-      // entries n .. hi4 - 1 (at most 3) hold stale nodes; 4q < n always
-      m |= static_cast<uint32_t>(nd[r].w == u32 && top < P.n);
-      m |= static_cast<uint32_t>(nd[r].z == u32 && top - 1 < P.n) << 1;
-      m |= static_cast<uint32_t>(nd[r].y == u32 && top - 2 < P.n) << 2;
-      m |= static_cast<uint32_t>(nd[r].x == u32) << 3;
+      const int top = hi4 - 4 * (r * kThreads + t) - 1;  // 4q + 3
+      uint32_t m = static_cast<uint32_t>(nd[r].w == u32) | static_cast<uint32_t>(nd[r].z == u32) << 1 |
+                   static_cast<uint32_t>(nd[r].y == u32) << 2 | static_cast<uint32_t>(nd[r].x == u32) << 3;
+      // entries n .. hi4 - 1 (at most 3, in the topmost load of the first step)
+      // hold stale nodes: entry top - s is valid iff s >= top - n + 1
+      if (top >= n32) m &= (0xfu << (top - n32 + 1)) & 0xfu;
       m4[r] = m;
       const int cnt = __popc(m);
       int bl = 0, tot = 0;
@@ -528,9 +528,9 @@ __device__ __forceinline__ void fast_large(const AppendParams& P, int64_t u, int
     for (int r = 0; r < kTopRows; ++r) {
       int e = carry + __shfl(incl - x, r * kCommitWaves + wv, kWave) + below[r];
       uint32_t m = m4[r];
-      const int64_t top = hi4 - 4 * (static_cast<int64_t>(r) * kThreads + t) - 1;
+      const int top = hi4 - 4 * (r * kThreads + t) - 1;
       // only ranks below B are kept
-      for (; m != 0u && e < P.B; m &= m - 1, ++e) R[e] = static_cast<int32_t>(top - __builtin_ctz(m));
+      for (; m != 0u && e < P.B; m &= m - 1, ++e) R[e] = top - __builtin_ctz(m);
     }
     carry += step_total;
     hi4 -= kTopChunk;
