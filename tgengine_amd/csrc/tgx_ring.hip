@@ -58,9 +58,14 @@ constexpr int kWinWords = kWinBits / 32;       // 256 words = 1 KB
 static_assert(kWinWords == kThreads, "one bitmap word per thread");
 constexpr int64_t kSmallGroupBlocks = 256;  // commit blocks for small groups (4 waves each)
 constexpr int64_t kLargeGroupBlocks = 64;   // four-launch commit blocks for large groups
-constexpr int kTopRows = 8;                 // 16-byte loads (4 entry nodes each) in flight per thread
-constexpr int kTopChunk = 4 * kTopRows * kThreads;  // entries per top-down step
+// the two-launch commit runs 512-thread workgroups, so that the large-group
+// role's step of kTopChunk entries is kTopRows 16-byte loads per thread
+constexpr int kFastThreads = 512;
+constexpr int kFastWaves = kFastThreads / kWave;
+constexpr int kTopRows = 4;                 // 16-byte loads (4 entry nodes each) in flight per thread
+constexpr int kTopChunk = 4 * kTopRows * kFastThreads;  // entries per top-down step
 constexpr int64_t kFastLargeBlocks = 128;   // two-launch commit blocks for large groups
+constexpr int64_t kFastSmallBlocks = 128;   // two-launch commit blocks for small groups (8 waves each)
 
 // (write_pos + off) % B for write_pos >= 0, 0 <= off < B
 __device__ __forceinline__ int64_t ring_slot(int64_t w, int off, int B) {
@@ -331,7 +336,7 @@ __device__ __forceinline__ void commit_singletons(const AppendParams& P, int blk
   using V = typename VecT<VEC>::T;
   const int nv = static_cast<int>(P.row_bytes / VEC);
   const int tpe = 1 << P.tpe_log2;
-  const int epb = kThreads >> P.tpe_log2;
+  const int epb = static_cast<int>(blockDim.x) >> P.tpe_log2;
   const int64_t i = static_cast<int64_t>(blk) * epb + (threadIdx.x >> P.tpe_log2);
   const int l = threadIdx.x & (tpe - 1);
   if (i >= P.n) return;
@@ -444,24 +449,24 @@ __global__ __launch_bounds__(kThreads) void append_commit(AppendParams P) {
 
 // ---- two-launch 2. commit -------------------------------------------------------
 // The plan's node of every entry, four per 16-byte load, top-down: row r of
-// thread t holds entries 4q .. 4q + 3 of q = hi4 / 4 - 1 - (r kThreads + t)
+// thread t holds entries 4q .. 4q + 3 of q = hi4 / 4 - 1 - (r kFastThreads + t)
 // (hi4 a multiple of 4; the node array is padded to whole 256-byte lines, and
-// indices >= n are masked by the caller), so each row covers 4 kThreads
+// indices >= n are masked by the caller), so each row covers 4 kFastThreads
 // consecutive entries in descending order.
 __device__ __forceinline__ void load_top(const AppendParams& P, int64_t hi4,
                                          int4 (&nd)[kTopRows]) {
 #pragma unroll
   for (int r = 0; r < kTopRows; ++r) {
-    const int64_t q = hi4 / 4 - 1 - (static_cast<int64_t>(r) * kThreads + threadIdx.x);
+    const int64_t q = hi4 / 4 - 1 - (static_cast<int64_t>(r) * kFastThreads + threadIdx.x);
     nd[r] = q >= 0 ? reinterpret_cast<const int4*>(P.ticket)[q] : make_int4(-1, -1, -1, -1);
   }
 }
 
 // LDS of the top-down ranking: the match count of every (row, wavefront)
 struct TopLds {
-  int32_t tot[kTopRows][kCommitWaves];
+  int32_t tot[kTopRows][kFastWaves];
 };
-static_assert(kTopRows * kCommitWaves <= kWave, "one lane per (row, wavefront) count");
+static_assert(kTopRows * kFastWaves <= kWave, "one lane per (row, wavefront) count");
 
 // set bits of the wave mask b below this lane
 __device__ __forceinline__ int lanes_below(uint64_t b) {
@@ -495,7 +500,7 @@ __device__ __forceinline__ void fast_large(const AppendParams& P, int64_t u, int
     int below[kTopRows];
 #pragma unroll
     for (int r = 0; r < kTopRows; ++r) {
-      const int top = hi4 - 4 * (r * kThreads + t) - 1;  // 4q + 3
+      const int top = hi4 - 4 * (r * kFastThreads + t) - 1;  // 4q + 3
       uint32_t m = static_cast<uint32_t>(nd[r].w == u32) | static_cast<uint32_t>(nd[r].z == u32) << 1 |
                    static_cast<uint32_t>(nd[r].y == u32) << 2 | static_cast<uint32_t>(nd[r].x == u32) << 3;
       // entries n .. hi4 - 1 (at most 3, in the topmost load of the first step)
@@ -514,21 +519,21 @@ __device__ __forceinline__ void fast_large(const AppendParams& P, int64_t u, int
       if (lane == 0) T.tot[r][wv] = tot;
     }
     __syncthreads();
-    // lane l < kTopRows kCommitWaves: the count of (row l / kCommitWaves,
-    // wavefront l % kCommitWaves); an exclusive scan in that order gives bases
-    const int x = lane < kTopRows * kCommitWaves ? T.tot[lane / kCommitWaves][lane % kCommitWaves] : 0;
+    // lane l < kTopRows kFastWaves: the count of (row l / kFastWaves,
+    // wavefront l % kFastWaves); an exclusive scan in that order gives bases
+    const int x = lane < kTopRows * kFastWaves ? T.tot[lane / kFastWaves][lane % kFastWaves] : 0;
     int incl = x;
 #pragma unroll
-    for (int off = 1; off < kTopRows * kCommitWaves; off <<= 1) {
+    for (int off = 1; off < kTopRows * kFastWaves; off <<= 1) {
       const int y = __shfl_up(incl, off, kWave);
       if (lane >= off) incl += y;
     }
-    const int step_total = __shfl(incl, kTopRows * kCommitWaves - 1, kWave);
+    const int step_total = __shfl(incl, kTopRows * kFastWaves - 1, kWave);
 #pragma unroll
     for (int r = 0; r < kTopRows; ++r) {
-      int e = carry + __shfl(incl - x, r * kCommitWaves + wv, kWave) + below[r];
+      int e = carry + __shfl(incl - x, r * kFastWaves + wv, kWave) + below[r];
       uint32_t m = m4[r];
-      const int top = hi4 - 4 * (r * kThreads + t) - 1;
+      const int top = hi4 - 4 * (r * kFastThreads + t) - 1;
       // only ranks below B are kept
       for (; m != 0u && e < P.B; m &= m - 1, ++e) R[e] = top - __builtin_ctz(m);
     }
@@ -543,7 +548,7 @@ __device__ __forceinline__ void fast_large(const AppendParams& P, int64_t u, int
   // first wait would otherwise wait for it too (one round trip more); here it
   // shares the round trip of the kept rows' loads
   const int64_t w = P.wp[u];
-  write_kept<VEC>(P, R, u, kept, w, t, kThreads);
+  write_kept<VEC>(P, R, u, kept, w, t, kFastThreads);
   if (t == 0) {
     P.wp[u] = w + kept;
     P.cnt[u] = 0;
@@ -583,8 +588,8 @@ __device__ __forceinline__ void fast_diagnostics(const AppendParams& P, uint32_t
 // before it uses them, so they cost one round trip together: loads and their
 // wait counter are in order, and a wait for a younger load is a wait for all.
 template <int VEC>
-__global__ __launch_bounds__(kThreads) void fast_commit(AppendParams P) {
-  __shared__ int32_t rows[kCommitWaves][TGX_MAX_SLOTS];
+__global__ __launch_bounds__(kFastThreads) void fast_commit(AppendParams P) {
+  __shared__ int32_t rows[kFastWaves][TGX_MAX_SLOTS];
   __shared__ TopLds top;
   const int blk = static_cast<int>(blockIdx.x);
   const int wv = threadIdx.x / kWave;
@@ -598,8 +603,8 @@ __global__ __launch_bounds__(kThreads) void fast_commit(AppendParams P) {
   } else if (blk < P.ga + P.gb) {
     // the first group id of this wavefront is read with the cursor (in bounds of
     // the n/2 + 1 list), so a group costs three round trips
-    const int gstride = P.gb * kCommitWaves;
-    int gid = (blk - P.ga) * kCommitWaves + wv;
+    const int gstride = P.gb * kFastWaves;
+    int gid = (blk - P.ga) * kFastWaves + wv;
     int64_t u = gid <= P.n / 2 ? P.groups[gid] : 0;
     const int ngroups = field(plan_cursor(c0, c1), kFGroups);
     if (blk == P.ga && threadIdx.x == 0) fast_diagnostics(P, c1.y);
@@ -784,9 +789,14 @@ int setup_append(const char* who, const tgx_ring* ring, const int64_t* src, cons
 template <int VEC>
 void launch_commit_vec(const AppendParams& P, hipStream_t stream) {
   if (plan_fused_ok(P)) {
-    const int64_t gc = std::min<int64_t>(P.n / (kListCap + 1) + 1, kFastLargeBlocks);
-    hipLaunchKernelGGL(fast_commit<VEC>, dim3(static_cast<unsigned>(P.ga + P.gb + gc)),
-                       dim3(kThreads), 0, stream, P);
+    // 512-thread workgroups: the roles' block counts for that size
+    AppendParams Q = P;
+    const int64_t epb = kFastThreads >> Q.tpe_log2;
+    Q.ga = static_cast<int>((Q.n + epb - 1) / epb);
+    Q.gb = static_cast<int>(std::min<int64_t>((Q.n / 2 + kFastWaves) / kFastWaves, kFastSmallBlocks));
+    const int64_t gc = std::min<int64_t>(Q.n / (kListCap + 1) + 1, kFastLargeBlocks);
+    hipLaunchKernelGGL(fast_commit<VEC>, dim3(static_cast<unsigned>(Q.ga + Q.gb + gc)),
+                       dim3(kFastThreads), 0, stream, Q);
   } else {
     const int64_t gc = std::min<int64_t>(P.n / (kWave + 1) + 1, kLargeGroupBlocks);
     hipLaunchKernelGGL(append_commit<VEC>, dim3(static_cast<unsigned>(P.ga + P.gb + gc)),
