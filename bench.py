@@ -207,8 +207,11 @@ def main():
     avail = num_batches(cfg)
     # a short stream (C1) keeps a few batches after the timed work for the CPU baseline
     reserve = 0 if a.no_cpu else min(64, avail // 10)
-    K = min(a.steps, avail)
-    R = min(a.roofline_steps, max(0, avail - K - reserve))
+    # a short stream still gets a short warm-up (the first batches freeze the CSR,
+    # build the launch context and grow the allocator's pools)
+    w0 = min(a.warmup, 32, avail // 8)
+    K = min(a.steps, max(1, avail - reserve - w0))
+    R = min(a.roofline_steps, max(0, avail - K - reserve - w0))
     W = min(a.warmup, max(0, avail - K - R - reserve))
     total = W + K + R
     t0 = time.time()
