@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define TGX_ABI_VERSION 10
+#define TGX_ABI_VERSION 11
 
 /* status codes */
 #define TGX_OK 0
@@ -141,7 +141,10 @@ typedef struct tgx_recent_args {
    *     groups: group g = event g holds, for each query group in order,
    *     its times_per queries of event g (the reference grouping [src, dst,
    *     neg row-major, neg_src], pipeline/__init__.py:40-70, read as one
-   *     group per event); group = sum of times_per, num_groups = events;
+   *     group per event); group = sum of times_per, num_groups = events.
+   *     With event_query_groups = E > 0, only the first E query groups form
+   *     the events (group = their sum of times_per); the queries of the other
+   *     groups follow in workgroups of `group` consecutive queries;
    *   TGX_PLAN_LIST (plan set): group g handles queries plan[g*group + j],
    *     j < group (-1 = none).
    * Co-occurrence needs TGX_PLAN_EVENTS or TGX_PLAN_LIST (its pairs are
@@ -187,6 +190,9 @@ typedef struct tgx_recent_args {
   int64_t append_b;
   void* append_workspace;
   size_t append_workspace_bytes;
+  /* TGX_PLAN_EVENTS: the number of leading query groups that form the events
+   * (0 = all of them; see plan_mode) */
+  int32_t event_query_groups;
 } tgx_recent_args;
 
 #define TGX_MAX_SLOTS 64

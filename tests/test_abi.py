@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(L, n), n
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
-    assert L.tgx_abi_version() == _lib.TGX_ABI_VERSION == 10
+    assert L.tgx_abi_version() == _lib.TGX_ABI_VERSION == 11
     nm = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
                         text=True).stdout
     exported = set(re.findall(r"\bT (tgx_\w+)", nm))
@@ -53,6 +53,7 @@ int main(void) {
   F(tgx_recent_args, num_query_groups) F(tgx_recent_args, query_groups)
   F(tgx_recent_args, timing_start) F(tgx_recent_args, timing_stop)
   F(tgx_recent_args, append_src) F(tgx_recent_args, append_b) F(tgx_recent_args, append_workspace_bytes)
+  F(tgx_recent_args, event_query_groups)
   S(tgx_csr_build_args) F(tgx_csr_build_args, num_entries) F(tgx_csr_build_args, event)
   F(tgx_csr_build_args, num_events) F(tgx_csr_build_args, feat_dtype) F(tgx_csr_build_args, out_offsets)
   F(tgx_csr_build_args, out_eids) F(tgx_csr_build_args, workspace_bytes) F(tgx_csr_build_args, status)
@@ -350,3 +351,44 @@ def test_last_error_is_per_thread():
     th.join()
     assert "negative" in main_msg and "above 4096" in seen[0]
     assert _err() == main_msg
+
+
+def test_event_groups_with_a_tiled_tail():
+    """TGX_PLAN_EVENTS with event_query_groups = 2: the first two query groups
+    (src, dst) form one pair per event, and the remaining groups' queries follow
+    in workgroups of `group` consecutive queries, so a small launch can split
+    each query over more wavefronts."""
+    L = _lib.lib()
+    b, K = 200, 32
+    ring = _lib.TgxRing(num_nodes=10, slots=32, feat_dim=172, feat_dtype=0, ids=16, times=16,
+                        feats=16, write_pos=16)
+
+    def args(eqg, per_neg=1):
+        groups = [(b, 1), (b, 1), (b * per_neg, per_neg)]
+        a = _lib.TgxRecentArgs(k=K, plan_mode=_lib.TGX_PLAN_EVENTS, num_groups=b,
+                               num_queries=sum(c for c, _ in groups), out_ids=16, out_times=16,
+                               out_mask=16, out_feats=16, d_t=100, te_w=16, out_te=16,
+                               co_mode=_lib.TGX_CO_FREQ, co_a=16, co_c=16, event_query_groups=eqg)
+        a.group = 2 if eqg == 2 else 2 + per_neg
+        a.num_query_groups = len(groups)
+        for g, (cnt, per) in enumerate(groups):
+            a.query_groups[g].nodes = 16
+            a.query_groups[g].times = 16
+            a.query_groups[g].count = cnt
+            a.query_groups[g].times_per = per
+        return a
+
+    rc, full = _shape(ctypes.byref(ring), None, args(0))
+    assert rc == 0, _err()
+    assert full[0] == b and full[5] == 3 and full[4] == 2  # 3 queries x split 2 per workgroup
+    rc, tail = _shape(ctypes.byref(ring), None, args(2))
+    assert rc == 0, _err()
+    assert tail[4] == 4 and tail[5] == 2 and tail[1] == 64 * 8  # 2 queries x split 4
+    assert tail[0] == b + b // 2  # the pairs, then 200 negatives two per workgroup
+    rc, tail3 = _shape(ctypes.byref(ring), None, args(2, per_neg=3))
+    assert rc == 0 and tail3[0] == b + (3 * b + 1) // 2
+    a = args(4)
+    assert L.tgx_recent(ctypes.byref(ring), None, ctypes.byref(a), None) == 1 and "event_query_groups" in _err()
+    a = args(2)
+    a.group = 3  # must be the event groups' sum of times_per
+    assert L.tgx_recent(ctypes.byref(ring), None, ctypes.byref(a), None) == 1 and "times_per" in _err()

@@ -25,6 +25,15 @@ namespace py = pybind11;
 
 namespace {
 
+// Event-major launches (co-occurrence) of at most this many queries group only the
+// (src, dst) pair of each event and tile the other query groups after them, so that
+// more wavefronts share each query (a workgroup holds at most 8 wavefronts: query
+// slots x split); larger launches keep every query of an event in its group
+constexpr int64_t kPairTailMaxQueries = 4096;
+
+// event_query_groups of an event-major launch over ng query groups and Q queries
+int pair_tail_groups(size_t ng, int64_t Q) { return ng > 2 && Q <= kPairTailMaxQueries ? 2 : 0; }
+
 void check(int rc, const char* what) {
   if (rc != TGX_OK) throw std::runtime_error(std::string(what) + " failed: " + tgx_last_error());
 }
@@ -158,14 +167,17 @@ struct Out {
 // launches of DataPipeline.launch).  Queries arrive as groups (nodes, times,
 // times_per[, valid]) read in place by the kernel.  append_src/dst/time +
 // append_ws (all or none): the caller's next ring batch, planned by the same
-// launch when plannable() allows.
+// launch when plannable() allows.  event_query_groups: as tgx_recent_args, or -1
+// for the layout DataPipeline's prepare picks (pair_tail_groups; the group size
+// then becomes the pair's times_per sum when the tail applies).
 // Returns (planned, tensors): per group ids, times, feats, mask, [te], [eids],
 // then co_a, co_c, co_pair with co-occurrence.
 py::tuple recent(int64_t ring_addr, int64_t csr_addr, const std::vector<at::Tensor>& gnodes,
                  const std::vector<at::Tensor>& gtimes, const std::vector<int64_t>& gper,
                  const std::vector<c10::optional<at::Tensor>>& gvalid, int64_t k,
                  int64_t feat_dim, at::ScalarType feat_dtype, const c10::optional<at::Tensor>& plan,
-                 int64_t plan_mode, int64_t group, int64_t num_groups, int64_t d_t,
+                 int64_t plan_mode, int64_t group, int64_t num_groups,
+                 int64_t event_query_groups, int64_t d_t,
                  const c10::optional<at::Tensor>& te_w, const c10::optional<at::Tensor>& te_b,
                  int64_t dt_mode, int64_t co_mode, bool want_eids, const at::Tensor& status,
                  int64_t stream, int64_t ev0, int64_t ev1,
@@ -204,6 +216,11 @@ py::tuple recent(int64_t ring_addr, int64_t csr_addr, const std::vector<at::Tens
   a.plan_mode = plan.has_value() ? TGX_PLAN_LIST : static_cast<int32_t>(plan_mode);
   a.group = static_cast<int32_t>(group);
   a.num_groups = num_groups < 0 ? 0 : num_groups;
+  if (event_query_groups < 0) {
+    event_query_groups = a.plan_mode == TGX_PLAN_EVENTS ? pair_tail_groups(ng, Q) : 0;
+    if (event_query_groups > 0) a.group = static_cast<int32_t>(gper[0] + gper[1]);
+  }
+  a.event_query_groups = static_cast<int32_t>(event_query_groups);
   out.fill(a);
   a.d_t = static_cast<int32_t>(d_t);
   a.te_w = te_w.has_value() ? te_w->data_ptr<float>() : nullptr;
@@ -310,6 +327,8 @@ class Prepare {
     }
     // event-major groups when the pair must meet in one workgroup
     const bool events = co_mode_ != TGX_CO_NONE;
+    const bool tail = events && pair_tail_groups(static_cast<size_t>(ng), Q) > 0;
+    if (tail) G = per[0] + per[1];
     if (events && G > TGX_MAX_GROUP)
       throw std::invalid_argument("prepare: " + std::to_string(G) +
                                   " queries per event exceed the fused group limit");
@@ -320,6 +339,7 @@ class Prepare {
     a.plan_mode = events ? TGX_PLAN_EVENTS : TGX_PLAN_TILES;
     a.group = events ? G : static_cast<int32_t>(qpw_);
     a.num_groups = events ? b : 0;
+    a.event_query_groups = tail ? 2 : 0;
     out.fill(a);
     a.d_t = static_cast<int32_t>(d_t_);
     a.te_w = te_w_.has_value() ? te_w_->data_ptr<float>() : nullptr;

@@ -122,6 +122,9 @@ struct Params {
   // group, index_j: the slot's index among them)
   uint64_t ev_code[2];
   int64_t ev_b;
+  // queries of the query groups after the event groups: from ev_tail on, G
+  // consecutive ones per workgroup, workgroups [ev_b, ...) of the plan
+  int64_t ev_tail;
 };
 
 template <int VEC>
@@ -232,6 +235,10 @@ __device__ __forceinline__ int64_t wave_lower_bound(const double* __restrict__ t
 __device__ __forceinline__ int64_t query_of(const Params& P, int64_t g, int j) {
   if (j >= P.G) return -1;
   if (P.plan_mode == TGX_PLAN_EVENTS) {
+    if (g >= P.ev_b) {
+      const int64_t q = P.ev_tail + (g - P.ev_b) * P.G + j;
+      return q < P.Q ? q : -1;
+    }
     const uint64_t w = j < 5 ? P.ev_code[0] >> (12 * j) : P.ev_code[1] >> (12 * (j - 5));
     const int before = static_cast<int>(w & 15u), per = static_cast<int>((w >> 4) & 15u);
     return P.ev_b * before + g * per + static_cast<int>((w >> 8) & 15u);
@@ -750,7 +757,9 @@ void recent_fused(Params P) {
   // ---- co-occurrence of the plan group's (query 0, query 1) pair ----
   if (P.co_mode != TGX_CO_NONE) {
     __syncthreads();
-    const int64_t qa = query_of(P, g, 0), qc = query_of(P, g, 1);
+    // workgroups from ev_b on (an event-major plan's tail) hold no pair
+    const int64_t qa = g < P.ev_b ? query_of(P, g, 0) : -1;
+    const int64_t qc = query_of(P, g, 1);
     if (qa >= 0 && qc >= 0 && wv == 0) {
       const int32_t* A = reinterpret_cast<const int32_t*>(smem + P.te_bytes + P.off_pid);
       const int32_t* Cc = reinterpret_cast<const int32_t*>(smem + P.te_bytes +
@@ -869,7 +878,7 @@ int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args
                               a->append_b, a->append_workspace, a->append_workspace_bytes, L.pl);
     if (rc != TGX_OK) return rc;
   }
-  const int64_t ngroups_eff = mode == TGX_PLAN_TILES ? 1 : a->num_groups;
+  const int64_t ngroups_eff = mode == TGX_PLAN_LIST ? a->num_groups : 1;  // events: their tail may hold queries
   if (a->num_queries == 0 || ngroups_eff == 0) {
     L.empty = true;
     return TGX_OK;
@@ -937,6 +946,10 @@ int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args
   {
     int64_t off = 0;
     int per_event = 0;
+    const int ev_groups = a->event_query_groups > 0 ? a->event_query_groups : a->num_query_groups;
+    if (mode == TGX_PLAN_EVENTS && (a->event_query_groups < 0 || ev_groups > a->num_query_groups))
+      return fail(TGX_ERR_ARG, "tgx_recent: event_query_groups=%d outside [0, %d]", a->event_query_groups,
+                  a->num_query_groups);
     for (int g = 0; g < a->num_query_groups; ++g) {
       const tgx_query_group& qg = a->query_groups[g];
       if (qg.count < 0 || qg.times_per < 1 || (qg.count > 0 && (qg.nodes == nullptr || qg.times == nullptr)) ||
@@ -949,6 +962,7 @@ int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args
       P.gdiv[g] = qg.times_per;
       P.goff[g] = off;
       off += qg.count;
+      if (mode == TGX_PLAN_EVENTS && g >= ev_groups) continue;  // a tail group
       per_event += qg.times_per;
       if (mode == TGX_PLAN_EVENTS && qg.count != a->num_groups * qg.times_per)
         return fail(TGX_ERR_ARG, "tgx_recent: event-major plan: query group %d holds %lld queries, "
@@ -968,7 +982,8 @@ int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args
       int j = 0, before = 0;
       P.ev_code[0] = P.ev_code[1] = 0;
       P.ev_b = a->num_groups;
-      for (int g = 0; g < a->num_query_groups; ++g) {
+      P.ev_tail = P.goff[ev_groups];
+      for (int g = 0; g < ev_groups; ++g) {
         const int per = a->query_groups[g].times_per;
         for (int i = 0; i < per; ++i, ++j) {
           const uint64_t c = static_cast<uint64_t>(before | (per << 4) | (i << 8));
@@ -978,6 +993,7 @@ int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args
       }
     }
   }
+  if (mode == TGX_PLAN_LIST) P.ev_b = a->num_groups;  // pairs: every group of the list
   P.Q = a->num_queries;
   P.K = a->k;
   P.plan = a->plan;
@@ -1066,6 +1082,7 @@ int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args
   if (waves < 1 || waves > kMaxWaves)
     return fail(TGX_ERR_LIMIT, "tgx_recent: %d wavefronts per workgroup outside [1, %d]", waves, kMaxWaves);
   int64_t nblocks = a->num_groups;
+  if (mode == TGX_PLAN_EVENTS) nblocks += (a->num_queries - P.ev_tail + a->group - 1) / a->group;
   if (mode == TGX_PLAN_TILES) {
     const int64_t ntiles = (a->num_queries + P.m - 1) / P.m;
     nblocks = (ntiles + qslots - 1) / qslots;

@@ -271,16 +271,16 @@ class DataPipeline:
 
     def _fused(self, qgroups, k, b, per_event, d_t, te_w, te_b, dt_mode, co_mode) -> dict:
         """One tgx_recent launch over the query groups (no ring plan); with
-        co-occurrence the event-major plan puts each event's queries in one
-        workgroup."""
+        co-occurrence the event-major plan puts each event's (src, dst) pair in one
+        workgroup, in the layout prepare() launches."""
         g = self.graph
         if co_mode != _lib.TGX_CO_NONE:
             G = sum(per_event)
             if G > _lib.TGX_MAX_GROUP:
                 raise ValueError(f"{G} queries per event exceed the fused group limit {_lib.TGX_MAX_GROUP}")
             return g._query(None, None, k, groups=qgroups, plan_mode=_lib.TGX_PLAN_EVENTS, group=G,
-                            num_groups=b, d_t=d_t, te_w=te_w, te_b=te_b, dt_mode=dt_mode,
-                            co_mode=co_mode, want_eids=self.spec.edge_ids)
+                            num_groups=b, event_query_groups=-1, d_t=d_t, te_w=te_w, te_b=te_b,
+                            dt_mode=dt_mode, co_mode=co_mode, want_eids=self.spec.edge_ids)
         return g._query(None, None, k, groups=qgroups, group=self.queries_per_workgroup,
                         d_t=d_t, te_w=te_w, te_b=te_b, dt_mode=dt_mode,
                         want_eids=self.spec.edge_ids)
