@@ -343,6 +343,27 @@ __device__ __forceinline__ void encode_rows(const Params& P, int64_t r0, int np,
 __device__ __forceinline__ void co_occurrence_pair(const Params& P, int64_t g, int64_t qa, int64_t qc,
                                                    const int32_t* A, const int32_t* Cc, int lane) {
   const int K = P.K;
+  if (P.co_mode == TGX_CO_FREQ && K <= kWave / 2) {
+    // both sides in one pass: lanes [0, 32) take A's positions, lanes [32, 64) C's
+    const int side = lane >> 5;
+    const int i = lane & 31;
+    const int32_t x = i < K ? (side == 0 ? A[i] : Cc[i]) : -1;
+    int na = 0, nc = 0;
+    if (x != -1) {
+      for (int j = 0; j < K; ++j) {
+        na += A[j] == x;
+        nc += Cc[j] == x;
+      }
+    }
+    if (i < K) {
+      int32_t* out = side == 0 ? P.co_a : P.co_c;
+      out[(g * K + i) * 2 + 0] = na;
+      out[(g * K + i) * 2 + 1] = nc;
+    }
+    const int pc = __popcll(__ballot(side == 0 && i < K && x != -1 && nc > 0));
+    if (lane == 0 && P.co_pair != nullptr) P.co_pair[g] = static_cast<float>(pc);
+    return;
+  }
   if (P.co_mode == TGX_CO_FREQ) {
     for (int side = 0; side < 2; ++side) {
       const int32_t* X = side == 0 ? A : Cc;
