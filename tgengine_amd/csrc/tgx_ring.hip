@@ -528,10 +528,13 @@ __device__ __forceinline__ void fast_large(const AppendParams& P, int64_t u, int
       const int y = __shfl_up(incl, off, kWave);
       if (lane >= off) incl += y;
     }
-    const int step_total = __shfl(incl, kTopRows * kFastWaves - 1, kWave);
+    // the lane index is wavefront-uniform: read the bases with readlane
+    const int step_total = __builtin_amdgcn_readlane(incl, kTopRows * kFastWaves - 1);
+    const int exc = incl - x;
+    const int wvu = __builtin_amdgcn_readfirstlane(wv);
 #pragma unroll
     for (int r = 0; r < kTopRows; ++r) {
-      int e = carry + __shfl(incl - x, r * kFastWaves + wv, kWave) + below[r];
+      int e = carry + __builtin_amdgcn_readlane(exc, r * kFastWaves + wvu) + below[r];
       uint32_t m = m4[r];
       const int top = hi4 - 4 * (r * kFastThreads + t) - 1;
       // only ranks below B are kept
