@@ -522,12 +522,15 @@ __device__ __forceinline__ void fast_large(const AppendParams& P, int64_t u, int
     // lane l < kTopRows kFastWaves: the count of (row l / kFastWaves,
     // wavefront l % kFastWaves); an exclusive scan in that order gives bases
     const int x = lane < kTopRows * kFastWaves ? T.tot[lane / kFastWaves][lane % kFastWaves] : 0;
+    // inclusive scan over lanes [0, 32) in registers (DPP): shifts by 1, 2, 4
+    // and 8 lanes within each 16-lane row, then row 0's last lane into row 1
+    static_assert(kTopRows * kFastWaves == 32, "the scan covers two DPP rows");
     int incl = x;
-#pragma unroll
-    for (int off = 1; off < kTopRows * kFastWaves; off <<= 1) {
-      const int y = __shfl_up(incl, off, kWave);
-      if (lane >= off) incl += y;
-    }
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x111, 0xf, 0xf, false);  // row_shr:1
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xf, 0xf, false);  // row_shr:2
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xf, 0xf, false);  // row_shr:4
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xf, 0xf, false);  // row_shr:8
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x142, 0xa, 0xf, false);  // row_bcast:15, rows 1, 3
     // the lane index is wavefront-uniform: read the bases with readlane
     const int step_total = __builtin_amdgcn_readlane(incl, kTopRows * kFastWaves - 1);
     const int exc = incl - x;
