@@ -390,9 +390,57 @@ __device__ __forceinline__ void commit_singletons(const AppendParams& P, int blk
   }
 }
 
-// one group of c <= kWave entries listed in idx (lane j < c holds one entry
-// index), ranked in registers by one wavefront, then written
+// copy the kept rows R[0..kept) (kept <= kListCap) of node u (row r -> slot
+// (w + kept - 1 - r) % B) by one wavefront: lanes 8r .. 8r + 7 take row r, lane
+// 8r + j its chunks j, j + 8, ..., kSmallDepth of them per round, so a row of up
+// to 8 kSmallDepth chunks costs one round trip
+constexpr int kSmallDepth = 8;
+static_assert(kListCap * 8 == kWave, "eight lanes per listed row");
 template <int VEC>
+__device__ __forceinline__ void write_listed(const AppendParams& P, const int32_t* R, int64_t u,
+                                             int kept, int64_t w) {
+  using V = typename VecT<VEC>::T;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int r = lane >> 3;
+  const int j = lane & 7;
+  if (r >= kept) return;
+  const int nv = static_cast<int>(P.row_bytes / VEC);
+  const int64_t i = R[r];
+  const int64_t e = i < P.b ? i : i - P.b;
+  const int64_t slot = u * P.B + ring_slot(w, kept - 1 - r, P.B);
+  const V* srow = reinterpret_cast<const V*>(P.feat + e * P.row_bytes);
+  V* drow = reinterpret_cast<V*>(P.feats + slot * P.row_bytes);
+  int32_t id = 0;
+  double tm = 0.0;
+  if (j == 0) {
+    id = static_cast<int32_t>(i < P.b ? P.dst[e] : P.src[e]);
+    tm = P.time[e];
+  }
+  for (int c0 = j; c0 < nv || j == 0; c0 += 8 * kSmallDepth) {
+    V v[kSmallDepth];
+#pragma unroll
+    for (int k = 0; k < kSmallDepth; ++k) {
+      const int c = c0 + 8 * k;
+      v[k] = (P.feat != nullptr && c < nv) ? srow[c] : V{};
+    }
+    if (j == 0 && c0 == 0) {
+      P.ids[slot] = id;
+      P.times[slot] = tm;
+      if (P.eids != nullptr) P.eids[slot] = P.eid_base + e;
+    }
+#pragma unroll
+    for (int k = 0; k < kSmallDepth; ++k) {
+      const int c = c0 + 8 * k;
+      if (c < nv) drow[c] = v[k];
+    }
+    if (c0 + 8 * kSmallDepth >= nv) break;
+  }
+}
+
+// one group of c <= kWave entries listed in idx (lane j < c holds one entry
+// index), ranked in registers by one wavefront, then written (LISTED: c <=
+// kListCap, copied by write_listed)
+template <int VEC, bool LISTED = false>
 __device__ __forceinline__ void commit_small(const AppendParams& P, int64_t u, int c, int32_t idx,
                                              int64_t w, int32_t* R) {
   const int lane = threadIdx.x & (kWave - 1);
@@ -401,7 +449,10 @@ __device__ __forceinline__ void commit_small(const AppendParams& P, int64_t u, i
   for (int j = 0; j < c; ++j) e += __shfl(idx, j, kWave) > idx;
   if (lane < c && e < kept) R[e] = idx;
   wave_sync_lds();
-  write_kept<VEC>(P, R, u, kept, w, lane, kWave);
+  if constexpr (LISTED)
+    write_listed<VEC>(P, R, u, kept, w);
+  else
+    write_kept<VEC>(P, R, u, kept, w, lane, kWave);
   if (lane == 0) {
     P.wp[u] = w + kept;
     P.cnt[u] = 0;
@@ -621,7 +672,7 @@ __global__ __launch_bounds__(kFastThreads) void fast_commit(AppendParams P) {
       const int64_t u_next = gid + gstride < ngroups ? P.groups[gid + gstride] : 0;
       // a larger group has its own role; its counter reads c > kListCap, or 0
       // once that role restored it
-      if (c >= 2 && c <= kListCap) commit_small<VEC>(P, u, c, lane < c ? idx : -1, w, rows[wv]);
+      if (c >= 2 && c <= kListCap) commit_small<VEC, true>(P, u, c, lane < c ? idx : -1, w, rows[wv]);
       u = u_next;
     }
   } else {
