@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define TGX_ABI_VERSION 11
+#define TGX_ABI_VERSION 12
 
 /* status codes */
 #define TGX_OK 0
@@ -193,6 +193,12 @@ typedef struct tgx_recent_args {
   /* TGX_PLAN_EVENTS: the number of leading query groups that form the events
    * (0 = all of them; see plan_mode) */
   int32_t event_query_groups;
+  /* d_t > 0: upper bounds of max|te_w[i]| and max|te_b[i]| (0 without bias),
+   * which let the cosine skip its large-argument reduction where no argument
+   * can need it.  te_bound_w <= 0 (or NaN): unknown, every element takes the
+   * full-range reduction (same results, slower). */
+  float te_bound_w;
+  float te_bound_b;
 } tgx_recent_args;
 
 #define TGX_MAX_SLOTS 64

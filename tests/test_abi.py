@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(L, n), n
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
-    assert L.tgx_abi_version() == _lib.TGX_ABI_VERSION == 11
+    assert L.tgx_abi_version() == _lib.TGX_ABI_VERSION == 12
     nm = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
                         text=True).stdout
     exported = set(re.findall(r"\bT (tgx_\w+)", nm))
@@ -54,6 +54,8 @@ int main(void) {
   F(tgx_recent_args, timing_start) F(tgx_recent_args, timing_stop)
   F(tgx_recent_args, append_src) F(tgx_recent_args, append_b) F(tgx_recent_args, append_workspace_bytes)
   F(tgx_recent_args, event_query_groups)
+  F(tgx_recent_args, te_bound_w)
+  F(tgx_recent_args, te_bound_b)
   S(tgx_csr_build_args) F(tgx_csr_build_args, num_entries) F(tgx_csr_build_args, event)
   F(tgx_csr_build_args, num_events) F(tgx_csr_build_args, feat_dtype) F(tgx_csr_build_args, out_offsets)
   F(tgx_csr_build_args, out_eids) F(tgx_csr_build_args, workspace_bytes) F(tgx_csr_build_args, status)

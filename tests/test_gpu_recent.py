@@ -15,6 +15,7 @@ import torch
 
 from oracle import spec as O
 from tgengine_amd import DataPipeline, GatherSpec, NeighborSpec, RawBatch, TemporalGraph
+from tgengine_amd.core import _lib
 from tgengine_amd.pipeline import cosine_time_weights
 
 pytestmark = pytest.mark.gpu
@@ -277,6 +278,36 @@ def test_time_encoding_large_arguments():
     exp = O.time_encode_exact(dt, w)
     assert np.max(np.abs(pb.src_neighbors.time_enc.cpu().numpy() - exp)) <= TE_ATOL
     assert (np.abs(O.time_args(dt, w)) >= 2 ** 40).any()
+
+
+def test_time_encoding_caller_bounds():
+    """The fixed-weight pipeline passes its weights' bound (max|w| = 1) to the
+    kernel: arguments past 2^29 still take the full-range reduction (1e-6 bound),
+    and the same launch without bounds (every element on the full-range path)
+    gives the same bits."""
+    g = TemporalGraph(4, edge_feat_dim=2, device="cuda", buffer_size=4)
+    g.freeze_csr()
+    times = np.array([1.0, 3.5e7, 7.1e8, 9.9e8])
+    g.advance(cu([0, 0, 0, 0]), cu([1, 2, 3, 1]), cu(times), torch.zeros(4, 2).cuda())
+    spec = GatherSpec(neighbors=NeighborSpec(k=4, for_nodes=("src",)), time_encoding=4, dt_mode="tgn")
+    pipe = DataPipeline(spec, g)
+    qt = np.array([2.0e9, 1.0e9 + 0.25, 5.0e8, 3.6e7])
+    src = cu([0, 0, 0, 0])
+    pb = pipe.prepare(RawBatch(src=src, dst=cu([1, 1, 1, 1]), time=cu(qt)))
+    r = g.recent(src, cu(qt), 4)
+    dt = O.dt_tgn(qt, r.timestamps.cpu().numpy())
+    w = cosine_time_weights(4)
+    args = np.abs(O.time_args(dt, w))
+    assert (args >= 2 ** 29).any() and (args[np.isfinite(args)] < 2 ** 29).any()
+    exp = O.time_encode_exact(dt, w)
+    assert np.max(np.abs(pb.src_neighbors.time_enc.cpu().numpy() - exp)) <= TE_ATOL
+    wt = torch.from_numpy(w).cuda()
+    groups = [(src, cu(qt), 1)]
+    with_b = g._query(None, None, 4, groups=groups, d_t=4, te_w=wt, dt_mode=_lib.TGX_DT_TGN,
+                      te_bounds=(1.0, 0.0))["te"][0]
+    without = g._query(None, None, 4, groups=groups, d_t=4, te_w=wt, dt_mode=_lib.TGX_DT_TGN)["te"][0]
+    assert torch.equal(with_b.view(torch.int32), without.view(torch.int32))
+    assert np.max(np.abs(with_b.cpu().numpy() - exp)) <= TE_ATOL
 
 
 @pytest.mark.parametrize("mode", ["freq", "dygformer"])

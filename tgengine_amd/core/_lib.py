@@ -24,7 +24,7 @@ TGX_CO_DYGFORMER = 2
 TGX_PLAN_TILES = 0
 TGX_PLAN_EVENTS = 1
 TGX_PLAN_LIST = 2
-TGX_ABI_VERSION = 11
+TGX_ABI_VERSION = 12
 TGX_STATUS_WORDS = 8
 TGX_ST_BAD_EVENT_NODE = 0
 TGX_ST_KEY_COLLISION = 1
@@ -70,7 +70,8 @@ class TgxRecentArgs(ctypes.Structure):
                 ("append_src", c_vp), ("append_dst", c_vp), ("append_time", c_vp),
                 ("append_b", c_i64), ("append_workspace", c_vp),
                 ("append_workspace_bytes", ctypes.c_size_t),
-                ("event_query_groups", c_i32)]
+                ("event_query_groups", c_i32), ("te_bound_w", ctypes.c_float),
+                ("te_bound_b", ctypes.c_float)]
 
 
 class TgxCsrBuildArgs(ctypes.Structure):

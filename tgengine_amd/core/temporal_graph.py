@@ -409,6 +409,7 @@ class TemporalGraph:
                plan_mode: int = _lib.TGX_PLAN_TILES, group: int = 4,
                num_groups: Optional[int] = None, event_query_groups: int = 0, d_t: int = 0,
                te_w: Optional[Tensor] = None, te_b: Optional[Tensor] = None,
+               te_bounds: tuple = (0.0, 0.0),
                dt_mode: int = _lib.TGX_DT_DYGFORMER, co_mode: int = _lib.TGX_CO_NONE,
                want_eids: bool = False, append: Optional[tuple] = None) -> dict:
         """One tgx_recent launch.
@@ -423,7 +424,8 @@ class TemporalGraph:
         ``event_query_groups``: of an event-major plan, the leading query groups
         grouped per event (0: all); the rest are tiled after them.  -1 picks the
         layout of DataPipeline.prepare (a launch of at most 4096 queries groups only
-        the (src, dst) pair per event).
+        the (src, dst) pair per event).  ``te_bounds``: upper bounds of max|te_w| and
+        max|te_b| (0, 0: unknown, every encoding takes the full-range reduction).
         """
         if not self._frozen:
             self.freeze_csr()
@@ -437,8 +439,8 @@ class TemporalGraph:
         if len(groups) > _lib.TGX_MAX_QUERY_GROUPS:
             raise ValueError(f"at most {_lib.TGX_MAX_QUERY_GROUPS} query groups")
         planned, res = self._gather(groups, k, plan, plan_mode, group, num_groups,
-                                    event_query_groups, d_t, te_w, te_b, dt_mode, co_mode,
-                                    want_eids, append)
+                                    event_query_groups, d_t, (te_w, te_b, te_bounds), dt_mode,
+                                    co_mode, want_eids, append)
         nf = 4 + (d_t > 0) + bool(want_eids)
         ng = len(groups)
         out = {"ids": res[0:ng * nf:nf], "times": res[1:ng * nf:nf], "feats": res[2:ng * nf:nf],
@@ -451,7 +453,7 @@ class TemporalGraph:
             out["co_a"], out["co_c"], out["co_pair"] = res[ng * nf:ng * nf + 3]
         return out
 
-    def _gather(self, groups, k, plan, plan_mode, group, num_groups, ev_groups, d_t, te_w, te_b,
+    def _gather(self, groups, k, plan, plan_mode, group, num_groups, ev_groups, d_t, te,
                 dt_mode, co_mode, want_eids, append) -> tuple:
         """One tgx_recent launch over checked query groups: the extension's
         (planned, tensors) pair.  When ``append`` is given and the ring exists,
@@ -466,7 +468,7 @@ class TemporalGraph:
         stream = _stream_handle(self.device)
         if append is None or ring is None:
             return self._launch_recent(ring, csr, groups, k, plan, plan_mode, group, num_groups,
-                                       ev_groups, d_t, te_w, te_b, dt_mode, co_mode, want_eids, ev0,
+                                       ev_groups, d_t, te, dt_mode, co_mode, want_eids, ev0,
                                        ev1, None, None, stream)
         # the extension plans the batch when its tensors allow it (int64 / float64
         # contiguous 1-D device tensors of one non-zero length)
@@ -475,14 +477,15 @@ class TemporalGraph:
                 self._discard_plan()
             ws = self._plan_workspace(int(append[0].shape[0]))
             res = self._launch_recent(ring, csr, groups, k, plan, plan_mode, group, num_groups,
-                                      ev_groups, d_t, te_w, te_b, dt_mode, co_mode, want_eids, ev0,
+                                      ev_groups, d_t, te, dt_mode, co_mode, want_eids, ev0,
                                       ev1, append, ws, stream)
             if res[0]:
                 self._plan = _Plan(append[0], append[1], append[2], stream)
         return res
 
     def _launch_recent(self, ring, csr, groups, k, plan, plan_mode, group, num_groups, ev_groups,
-                       d_t, te_w, te_b, dt_mode, co_mode, want_eids, ev0, ev1, append, ws, stream):
+                       d_t, te, dt_mode, co_mode, want_eids, ev0, ev1, append, ws, stream):
+        te_w, te_b, te_bounds = te
         a_src, a_dst, a_time = append if append is not None else (None, None, None)
         gn, gt, gp, gv = [], [], [], []
         for grp in groups:
@@ -498,7 +501,7 @@ class TemporalGraph:
             ctypes.addressof(csr) if csr is not None else 0,
             gn, gt, gp, gv, k, self.edge_feat_dim, self.feat_dtype, plan, int(plan_mode), int(group),
             -1 if num_groups is None else int(num_groups), int(ev_groups), int(d_t), te_w, te_b,
-            int(dt_mode),
+            float(te_bounds[0]), float(te_bounds[1]), int(dt_mode),
             int(co_mode), bool(want_eids), self._status, stream, ev0, ev1,
             a_src, a_dst, a_time, ws)
 

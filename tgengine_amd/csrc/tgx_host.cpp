@@ -179,6 +179,7 @@ py::tuple recent(int64_t ring_addr, int64_t csr_addr, const std::vector<at::Tens
                  int64_t plan_mode, int64_t group, int64_t num_groups,
                  int64_t event_query_groups, int64_t d_t,
                  const c10::optional<at::Tensor>& te_w, const c10::optional<at::Tensor>& te_b,
+                 double te_bound_w, double te_bound_b,
                  int64_t dt_mode, int64_t co_mode, bool want_eids, const at::Tensor& status,
                  int64_t stream, int64_t ev0, int64_t ev1,
                  const c10::optional<at::Tensor>& append_src,
@@ -225,6 +226,8 @@ py::tuple recent(int64_t ring_addr, int64_t csr_addr, const std::vector<at::Tens
   a.d_t = static_cast<int32_t>(d_t);
   a.te_w = te_w.has_value() ? te_w->data_ptr<float>() : nullptr;
   a.te_b = te_b.has_value() ? te_b->data_ptr<float>() : nullptr;
+  a.te_bound_w = static_cast<float>(te_bound_w);
+  a.te_bound_b = static_cast<float>(te_bound_b);
   a.dt_mode = static_cast<int32_t>(dt_mode);
   a.co_mode = static_cast<int32_t>(co_mode);
   a.status = status.data_ptr<int32_t>();
@@ -278,10 +281,13 @@ class Prepare {
  public:
   Prepare(int64_t ring_addr, int64_t csr_addr, int64_t groups_mask, int64_t k, int64_t feat_dim,
           at::ScalarType feat_dtype, int64_t d_t, const c10::optional<at::Tensor>& te_w,
-          const c10::optional<at::Tensor>& te_b, int64_t dt_mode, int64_t co_mode, bool want_eids,
+          const c10::optional<at::Tensor>& te_b, double te_bound_w, double te_bound_b,
+          int64_t dt_mode, int64_t co_mode, bool want_eids,
           int64_t qpw, const at::Tensor& status)
       : ring_(ring_addr), csr_(csr_addr), mask_(groups_mask), k_(k), feat_dim_(feat_dim),
-        feat_dtype_(feat_dtype), d_t_(d_t), te_w_(te_w), te_b_(te_b), dt_mode_(dt_mode),
+        feat_dtype_(feat_dtype), d_t_(d_t), te_w_(te_w), te_b_(te_b),
+        te_bound_w_(static_cast<float>(te_bound_w)), te_bound_b_(static_cast<float>(te_bound_b)),
+        dt_mode_(dt_mode),
         co_mode_(co_mode), want_eids_(want_eids), qpw_(qpw), status_(status),
         dev_(status.device()) {
     if (k < 1 || k > TGX_MAX_K) throw std::invalid_argument("Prepare: k outside [1, TGX_MAX_K]");
@@ -344,6 +350,8 @@ class Prepare {
     a.d_t = static_cast<int32_t>(d_t_);
     a.te_w = te_w_.has_value() ? te_w_->data_ptr<float>() : nullptr;
     a.te_b = te_b_.has_value() ? te_b_->data_ptr<float>() : nullptr;
+    a.te_bound_w = te_bound_w_;
+    a.te_bound_b = te_bound_b_;
     a.dt_mode = static_cast<int32_t>(dt_mode_);
     a.co_mode = static_cast<int32_t>(co_mode_);
     a.status = status_.data_ptr<int32_t>();
@@ -384,6 +392,7 @@ class Prepare {
   at::ScalarType feat_dtype_;
   int64_t d_t_;
   c10::optional<at::Tensor> te_w_, te_b_;
+  float te_bound_w_, te_bound_b_;
   int64_t dt_mode_, co_mode_;
   bool want_eids_;
   int64_t qpw_;
@@ -446,8 +455,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("recent", &recent, "allocate outputs, launch tgx_recent, return (planned, tensors)");
   py::class_<Prepare>(m, "Prepare")
       .def(py::init<int64_t, int64_t, int64_t, int64_t, int64_t, at::ScalarType, int64_t,
-                    const c10::optional<at::Tensor>&, const c10::optional<at::Tensor>&, int64_t,
-                    int64_t, bool, int64_t, const at::Tensor&>())
+                    const c10::optional<at::Tensor>&, const c10::optional<at::Tensor>&, double,
+                    double, int64_t, int64_t, bool, int64_t, const at::Tensor&>())
       .def("run", &Prepare::run, "one 1-hop prepare launch: (planned, tensors)");
   m.def("ring_append", &ring_append, "launch tgx_ring_append on one batch");
   m.def("ring_plan", &ring_plan, "launch tgx_ring_plan (first half of an append)");

@@ -125,6 +125,8 @@ struct Params {
   // queries of the query groups after the event groups: from ev_tail on, G
   // consecutive ones per workgroup, workgroups [ev_b, ...) of the plan
   int64_t ev_tail;
+  // |dt| below which no encoding argument reaches kRevArg (0: none is known)
+  float te_dt_small;
 };
 
 template <int VEC>
@@ -540,15 +542,6 @@ void recent_fused(Params P) {
   }
 
   // |w| and |b| bounds of the cosine domain check, computed while the loads fly
-  float te_wmax = 0.f, te_bmax = 0.f;
-  if (P.d_t > 0) {
-    for (int i = lane; i < P.d_t; i += kWave) {
-      te_wmax = fmaxf(te_wmax, fabsf(s_w[i]));
-      te_bmax = fmaxf(te_bmax, fabsf(s_b[i]));
-    }
-    te_wmax = wave_max(te_wmax);
-    te_bmax = wave_max(te_bmax);
-  }
 
   // ---- CSR windows: a 64-ary search per query of the wave, all lanes ----
   int ncsr = 0;
@@ -595,7 +588,7 @@ void recent_fused(Params P) {
     pt[pp] = t;
     pcode[pp] = code;
     pid[pp] = id;
-    lane_big |= (!dyg || code >= 0) && !(fabsf(dt) * te_wmax + te_bmax < kRevArg);
+    lane_big |= (!dyg || code >= 0) && !(fabsf(dt) < P.te_dt_small);
   };
   // fast path: no CSR candidates, and the filled slots are the newest ones in
   // write order (oldest = slot write_pos % B) with strictly increasing times;
@@ -873,6 +866,21 @@ struct Launch {
   int nreg = 0;
 };
 
+// |dt| below which every encoding argument fl32(fl32(dt w) + b) stays below
+// kRevArg for weights |w| <= bw and biases |b| <= bb, rounded down; 0 when the
+// bounds are unknown (bw <= 0 or not finite), so that every element takes the
+// full-range reduction.  Each of the two float roundings grows a value by at
+// most 2^-24 relative; the margin r covers both.
+float te_small_dt(float bw, float bb) {
+  if (!(bw > 0.0f) || !std::isfinite(bw) || !(bb >= 0.0f) || !std::isfinite(bb)) return 0.0f;
+  const double r = 1.0 + std::ldexp(1.0, -22);
+  const double lim = static_cast<double>(kRevArg) / r - static_cast<double>(bb);
+  if (!(lim > 0.0)) return 0.0f;
+  const double t = lim / (static_cast<double>(bw) * r);
+  const float f = static_cast<float>(t);
+  return static_cast<double>(f) > t ? std::nextafter(f, 0.0f) : f;
+}
+
 int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args* a, Launch& L) {
   L = Launch{};
   Params& P = L.P;
@@ -1034,6 +1042,7 @@ int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args
     return fail(TGX_ERR_ARG, "tgx_recent: unknown dt_mode %d", a->dt_mode);
   P.te_w = a->te_w;
   P.te_b = a->te_b;
+  P.te_dt_small = te_small_dt(a->te_bound_w, a->te_bound_b);
   P.dt_mode = a->dt_mode;
   P.o_te = a->out_te;
   P.te_vec4 = (a->d_t % 4 == 0 && aligned16(a->out_te)) ? 1 : 0;

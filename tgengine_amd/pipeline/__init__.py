@@ -72,9 +72,12 @@ class DataPipeline:
 
     # -- cached device constants ------------------------------------------
     def _te_params(self, d_t: int):
-        """(w, b) device tensors; b is None for no bias.  With an encoder module
-        its parameters are passed as they are when already contiguous float32 on
-        the graph's device (a zero bias gives the same encodings as none)."""
+        """(w, b, bounds): device tensors, b None for no bias, and the upper
+        bounds (max|w|, max|b|) that let the kernel skip the cosine's large-argument
+        reduction, (0, 0) when unknown.  With an encoder module its parameters are
+        passed as they are when already contiguous float32 on the graph's device
+        (a zero bias gives the same encodings as none); their bounds are left
+        unknown, since reading them would wait for the device."""
         enc = self.time_encoder
         if enc is not None:
             dev = self.graph.device
@@ -83,12 +86,13 @@ class DataPipeline:
             b = None if bias is None else bias.detach().to(dev, torch.float32).contiguous()
             if w.numel() != d_t:
                 raise ValueError(f"time encoder has {w.numel()} frequencies, spec asks for {d_t}")
-            return w, b
+            return w, b, (0.0, 0.0)
         t = self._te.get(d_t)
         if t is None:
-            t = torch.from_numpy(cosine_time_weights(d_t)).to(self.graph.device)
+            wn = cosine_time_weights(d_t)
+            t = (torch.from_numpy(wn).to(self.graph.device), (float(np.abs(wn).max()), 0.0))
             self._te[d_t] = t
-        return t, None
+        return t[0], None, t[1]
 
     def _context(self):
         """The extension's Prepare context for the current graph arrays and spec."""
@@ -114,11 +118,13 @@ class DataPipeline:
         co_mode = _CO_MODES[spec.co_occurrence_mode] if want_co else _lib.TGX_CO_NONE
         d_t = int(spec.time_encoding)
         te_w = te_b = None
+        te_bounds = (0.0, 0.0)
         if d_t > 0:
-            te_w, te_b = self._te_params(d_t)
+            te_w, te_b, te_bounds = self._te_params(d_t)
         ring, csr = g._structs()
         prep = _host().Prepare(ring, csr, mask, int(nb.k), g.edge_feat_dim, g.feat_dtype, d_t, te_w,
-                               te_b, _DT_MODES[spec.dt_mode], co_mode, bool(spec.edge_ids),
+                               te_b, te_bounds[0], te_bounds[1], _DT_MODES[spec.dt_mode], co_mode,
+                               bool(spec.edge_ids),
                                self.queries_per_workgroup, g._status)
         self._ctx = (key, prep, 4 + (d_t > 0) + bool(spec.edge_ids), d_t > 0, bool(spec.edge_ids),
                      mask, want_co)
@@ -149,27 +155,30 @@ class DataPipeline:
         return names, qgroups, sizes, per_event
 
     def launch_args(self, raw_batch: RawBatch) -> tuple:
-        """(d_t, te_w, te_b, dt_mode, co_mode) of the fused launch for this spec."""
+        """(d_t, te_w, te_b, te_bounds, dt_mode, co_mode) of the fused launch for
+        this spec."""
         spec = self.spec
         fn = spec.neighbors.for_nodes
         want_co = spec.co_occurrence and "src" in fn and "dst" in fn
         co_mode = _CO_MODES[spec.co_occurrence_mode] if want_co else _lib.TGX_CO_NONE
         d_t = int(spec.time_encoding)
         te_w = te_b = None
+        te_bounds = (0.0, 0.0)
         if d_t > 0:
-            te_w, te_b = self._te_params(d_t)
-        return d_t, te_w, te_b, _DT_MODES[spec.dt_mode], co_mode
+            te_w, te_b, te_bounds = self._te_params(d_t)
+        return d_t, te_w, te_b, te_bounds, _DT_MODES[spec.dt_mode], co_mode
 
     def launch(self, raw_batch: RawBatch, args: Optional[tuple] = None) -> dict:
         """The one fused tgx_recent launch of ``prepare`` (1-hop) without its ring
         plan, returning its raw output tensors (lists per query group) without
         building a PreparedBatch; for timing loops and graph capture."""
         names, qgroups, _, per_event = self._query_groups(raw_batch)
-        d_t, te_w, te_b, dt_mode, co_mode = args if args is not None else self.launch_args(raw_batch)
+        d_t, te_w, te_b, te_bounds, dt_mode, co_mode = (args if args is not None
+                                                         else self.launch_args(raw_batch))
         if "src" not in names or "dst" not in names:
             co_mode = _lib.TGX_CO_NONE
         return self._fused(qgroups, self.spec.neighbors.k, raw_batch.src.shape[0], per_event, d_t,
-                           te_w, te_b, dt_mode, co_mode)
+                           te_w, te_b, te_bounds, dt_mode, co_mode)
 
     def prepare(self, raw_batch: RawBatch) -> PreparedBatch:
         if self.spec.neighbors.k2 == 0:
@@ -221,7 +230,7 @@ class DataPipeline:
         names, qgroups, sizes, per_event = self._query_groups(raw_batch)
         if spec.edge_ids and not self.graph.track_edge_ids:
             raise ValueError("GatherSpec.edge_ids needs a TemporalGraph built with track_edge_ids=True")
-        d_t, te_w, te_b, dt_mode, co_mode = self.launch_args(raw_batch)
+        d_t, te_w, te_b, te_bounds, dt_mode, co_mode = self.launch_args(raw_batch)
         want_co = co_mode != _lib.TGX_CO_NONE
         if self.plan_updates:
             self.graph.plan_append(raw_batch.src, raw_batch.dst, raw_batch.time)
@@ -237,7 +246,7 @@ class DataPipeline:
                  "te": None}
         out = {}
         if d_t > 0 or want_co:
-            out = self._fused(qgroups, k, b, per_event, d_t, te_w, te_b, dt_mode, co_mode)
+            out = self._fused(qgroups, k, b, per_event, d_t, te_w, te_b, te_bounds, dt_mode, co_mode)
             parts["te"] = out.get("te")
         hparts = {kk: torch.split_with_sizes(v, sizes, dim=0)
                   for kk, v in (("hop2_ids", hop.hop2_ids), ("hop2_times", hop.hop2_times),
@@ -269,7 +278,7 @@ class DataPipeline:
             node_labels=raw_batch.node_labels, edge_labels=raw_batch.edge_labels,
             node_feat=raw_batch.node_feat, co_occurrence_freq=co_freq)
 
-    def _fused(self, qgroups, k, b, per_event, d_t, te_w, te_b, dt_mode, co_mode) -> dict:
+    def _fused(self, qgroups, k, b, per_event, d_t, te_w, te_b, te_bounds, dt_mode, co_mode) -> dict:
         """One tgx_recent launch over the query groups (no ring plan); with
         co-occurrence the event-major plan puts each event's (src, dst) pair in one
         workgroup, in the layout prepare() launches."""
@@ -280,9 +289,10 @@ class DataPipeline:
                 raise ValueError(f"{G} queries per event exceed the fused group limit {_lib.TGX_MAX_GROUP}")
             return g._query(None, None, k, groups=qgroups, plan_mode=_lib.TGX_PLAN_EVENTS, group=G,
                             num_groups=b, event_query_groups=-1, d_t=d_t, te_w=te_w, te_b=te_b,
-                            dt_mode=dt_mode, co_mode=co_mode, want_eids=self.spec.edge_ids)
+                            te_bounds=te_bounds, dt_mode=dt_mode, co_mode=co_mode,
+                            want_eids=self.spec.edge_ids)
         return g._query(None, None, k, groups=qgroups, group=self.queries_per_workgroup,
-                        d_t=d_t, te_w=te_w, te_b=te_b, dt_mode=dt_mode,
+                        d_t=d_t, te_w=te_w, te_b=te_b, te_bounds=te_bounds, dt_mode=dt_mode,
                         want_eids=self.spec.edge_ids)
 
     @staticmethod
