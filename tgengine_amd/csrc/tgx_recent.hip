@@ -528,17 +528,21 @@ void recent_fused(Params P) {
 #pragma unroll
   for (int k = 0; k < (NREG > 0 ? NREG : 1); ++k) rows[k] = VT{};
   if (live && B > 0) {
+    // the slot's id and time and the write position first: the rank waits for
+    // them, and loads complete in order, so the rows (NREG > 0) come last
     if (sl < B) {
       rid = P.r_ids[ur * B + sl];
       rt = P.r_times[ur * B + sl];
-      if constexpr (NREG > 0) {
+    }
+    if (P.r_wp != nullptr) wp = P.r_wp[ur];
+    if constexpr (NREG > 0) {
+      if (sl < B) {
         const VT* src = reinterpret_cast<const VT*>(P.r_feats + (ur * B + sl) * P.row_bytes);
 #pragma unroll
         for (int k = 0; k < NREG; ++k)
           if (k < P.nch) rows[k] = src[k];
       }
     }
-    if (P.r_wp != nullptr) wp = P.r_wp[ur];
   }
 
   // |w| and |b| bounds of the cosine domain check, computed while the loads fly
