@@ -6,7 +6,8 @@ runs the whole batch -- gather, feature rows, optional FixedCosineTimeEncoder
 and co-occurrence -- in ONE ``tgx_recent`` launch.  With co-occurrence the
 launch uses the event-major plan (computed in the kernel from the query
 groups): workgroup p holds event p's queries, src first and dst second, so the
-pair meets in one LDS.
+pair meets in one LDS; a launch of at most 4,096 queries puts only that pair in
+the event's workgroup and tiles the negatives after them.
 
 The per-batch host path is one call into the extension's ``Prepare`` context,
 configured once per (graph arrays, spec) and rebuilt when either changes.
