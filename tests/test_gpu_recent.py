@@ -310,20 +310,26 @@ def test_time_encoding_caller_bounds():
     assert np.max(np.abs(with_b.cpu().numpy() - exp)) <= TE_ATOL
 
 
-@pytest.mark.parametrize("mode", ["freq", "dygformer"])
-def test_co_occurrence_modes(mode):
+# k <= 32 counts both sides in one pass, k > 32 side by side; 90 events with 1 or 3
+# negatives each put the (src, dst) pair in the event's workgroup and tile the
+# negatives after them
+@pytest.mark.parametrize("mode,k,n_neg", [("freq", 12, 1), ("dygformer", 12, 1), ("freq", 40, 3),
+                                          ("dygformer", 40, 3)])
+def test_co_occurrence_modes(mode, k, n_neg):
     rng, g, csr, ring, tmax = _build(14, 12, 16, 4, 12, True, True, b=80)
-    spec = GatherSpec(neighbors=NeighborSpec(k=12), co_occurrence=True, co_occurrence_mode=mode)
+    spec = GatherSpec(neighbors=NeighborSpec(k=k), co_occurrence=True, co_occurrence_mode=mode)
     pipe = DataPipeline(spec, g)
     b = 90
     src = rng.integers(-1, 12, b)
     dst = np.where(rng.random(b) < 0.2, src, rng.integers(0, 12, b))
-    neg = rng.integers(0, 12, b)
+    neg = rng.integers(0, 12, (b, n_neg)) if n_neg > 1 else rng.integers(0, 12, b)
     t = tmax + rng.uniform(0.0, 5.0, b)
     pb = pipe.prepare(RawBatch(src=cu(src), dst=cu(dst), time=cu(t), neg=cu(neg)))
     a = pb.src_neighbors.neighbor_ids.cpu().numpy()
     c = pb.dst_neighbors.neighbor_ids.cpu().numpy()
-    o = O.recent(np.concatenate([src, dst]), np.concatenate([t, t]), 12, csr, ring, 4)
+    o = O.recent(np.concatenate([src, dst]), np.concatenate([t, t]), k, csr, ring, 4)
+    on = O.recent(neg.reshape(-1), np.repeat(t, n_neg), k, csr, ring, 4)
+    assert np.array_equal(pb.neg_neighbors.neighbor_ids.cpu().numpy().reshape(-1, k), on.ids)
     assert np.array_equal(np.concatenate([a, c]), o.ids)
     if mode == "freq":
         ea, ec = O.co_occurrence_freq(a, c)
