@@ -97,8 +97,10 @@ def test_ring_small_nodes_many_groups(B):
     _run(1, 50, B, 16, False, _uniform(50, 300, 6))
 
 
+# rows past 1 KB (300 f32, 2048 bf16) take more than one round of a group's copy
 @pytest.mark.parametrize("d,bf16", [(0, False), (1, False), (3, True), (5, True), (16, True),
-                                    (172, False), (512, True), (37, False)])
+                                    (172, False), (512, True), (37, False), (300, False),
+                                    (2048, True)])
 def test_ring_row_widths(d, bf16):
     _run(2, 200, 8, d, bf16, _hot(200, 500, 4, 0.2))
 
