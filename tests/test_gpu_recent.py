@@ -308,6 +308,17 @@ def test_time_encoding_caller_bounds():
     without = g._query(None, None, 4, groups=groups, d_t=4, te_w=wt, dt_mode=_lib.TGX_DT_TGN)["te"][0]
     assert torch.equal(with_b.view(torch.int32), without.view(torch.int32))
     assert np.max(np.abs(with_b.cpu().numpy() - exp)) <= TE_ATOL
+    # with a bias: bounds (max|w|, max|b|) against none, and the oracle
+    bias = np.float32([0.5, -3.0e8, 2.0, -0.25])
+    bt = torch.from_numpy(bias).cuda()
+    bounds = (float(np.abs(w).max()), float(np.abs(bias).max()))
+    with_b = g._query(None, None, 4, groups=groups, d_t=4, te_w=wt, te_b=bt, dt_mode=_lib.TGX_DT_TGN,
+                      te_bounds=bounds)["te"][0]
+    without = g._query(None, None, 4, groups=groups, d_t=4, te_w=wt, te_b=bt,
+                       dt_mode=_lib.TGX_DT_TGN)["te"][0]
+    assert torch.equal(with_b.view(torch.int32), without.view(torch.int32))
+    exp_b = O.time_encode_exact(dt, w, None, bias)
+    assert np.max(np.abs(with_b.cpu().numpy() - exp_b)) <= TE_ATOL
 
 
 # k <= 32 counts both sides in one pass, k > 32 side by side; 90 events with 1 or 3
