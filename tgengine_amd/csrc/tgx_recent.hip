@@ -155,12 +155,6 @@ __device__ __forceinline__ float cos_full(float x) {
   return __builtin_amdgcn_cosf(static_cast<float>(rev_frac(x, kRevTableDev)));
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 1; m < kWave; m <<= 1) v = fmaxf(v, __shfl_xor(v, m));
-  return v;
-}
-
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -544,8 +538,6 @@ void recent_fused(Params P) {
       }
     }
   }
-
-  // |w| and |b| bounds of the cosine domain check, computed while the loads fly
 
   // ---- CSR windows: a 64-ary search per query of the wave, all lanes ----
   int ncsr = 0;
