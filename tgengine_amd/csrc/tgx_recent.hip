@@ -448,7 +448,10 @@ __device__ __forceinline__ void co_occurrence_pair(const Params& P, int64_t g, i
 template <int NREG>
 constexpr int kWavesPerEu = NREG > 0 ? 1 : 8;
 
-template <int VEC, int NREG>
+// TILES: the launch's plan mode is TGX_PLAN_TILES (no event or list plan, so no
+// co-occurrence); that copy of the kernel carries none of their code, which
+// shortens its start-up
+template <int VEC, int NREG, bool TILES>
 __global__ __launch_bounds__(kMaxWaves * kWave) __attribute__((amdgpu_waves_per_eu(kWavesPerEu<NREG>)))
 void recent_fused(Params P) {
   using VT = typename Vec<VEC>::T;
@@ -498,7 +501,7 @@ void recent_fused(Params P) {
   const int qs = wv / split;
   const int part = wv - qs * split;
   int64_t q;
-  if (P.plan_mode != TGX_PLAN_TILES) {
+  if (!TILES && P.plan_mode != TGX_PLAN_TILES) {
     q = query_of(P, g, qs);
   } else {
     const int64_t t = g * (blockDim.x / kWave / split) + qs;
@@ -765,7 +768,7 @@ void recent_fused(Params P) {
   store_ids();
 
   // ---- co-occurrence of the plan group's (query 0, query 1) pair ----
-  if (P.co_mode != TGX_CO_NONE) {
+  if (!TILES && P.co_mode != TGX_CO_NONE) {
     __syncthreads();
     // workgroups from ev_b on (an event-major plan's tail) hold no pair
     const int64_t qa = g < P.ev_b ? query_of(P, g, 0) : -1;
@@ -1169,11 +1172,16 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
     return fail(TGX_ERR_ARG, "tgx_recent: timing_start and timing_stop must both be set or both NULL");
   static std::once_flag attr_once;
   std::call_once(attr_once, [] {
-    const void* fns[] = {reinterpret_cast<const void*>(recent_fused<16, 0>),
-                         reinterpret_cast<const void*>(recent_fused<16, 2>),
-                         reinterpret_cast<const void*>(recent_fused<16, 4>),
-                         reinterpret_cast<const void*>(recent_fused<4, 0>),
-                         reinterpret_cast<const void*>(recent_fused<2, 0>)};
+    const void* fns[] = {reinterpret_cast<const void*>(recent_fused<16, 0, false>),
+                         reinterpret_cast<const void*>(recent_fused<16, 2, false>),
+                         reinterpret_cast<const void*>(recent_fused<16, 4, false>),
+                         reinterpret_cast<const void*>(recent_fused<4, 0, false>),
+                         reinterpret_cast<const void*>(recent_fused<2, 0, false>),
+                         reinterpret_cast<const void*>(recent_fused<16, 0, true>),
+                         reinterpret_cast<const void*>(recent_fused<16, 2, true>),
+                         reinterpret_cast<const void*>(recent_fused<16, 4, true>),
+                         reinterpret_cast<const void*>(recent_fused<4, 0, true>),
+                         reinterpret_cast<const void*>(recent_fused<2, 0, true>)};
     for (const void* f : fns)
       (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     (void)hipGetLastError();
@@ -1186,17 +1194,25 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
     else
       hipLaunchKernelGGL(kernel, grid, block, L.lds, stream, L.P);
   };
+  // a tiled launch runs the kernel's TILES copy
+  const bool tiles = L.P.plan_mode == TGX_PLAN_TILES;
+  auto pick = [&](auto k_tiles, auto k_other) {
+    if (tiles)
+      launch(k_tiles);
+    else
+      launch(k_other);
+  };
   if (L.vec == 16) {
     if (L.nreg == 2)
-      launch(recent_fused<16, 2>);
+      pick(recent_fused<16, 2, true>, recent_fused<16, 2, false>);
     else if (L.nreg == 4)
-      launch(recent_fused<16, 4>);
+      pick(recent_fused<16, 4, true>, recent_fused<16, 4, false>);
     else
-      launch(recent_fused<16, 0>);
+      pick(recent_fused<16, 0, true>, recent_fused<16, 0, false>);
   } else if (L.vec == 4) {
-    launch(recent_fused<4, 0>);
+    pick(recent_fused<4, 0, true>, recent_fused<4, 0, false>);
   } else {
-    launch(recent_fused<2, 0>);
+    pick(recent_fused<2, 0, true>, recent_fused<2, 0, false>);
   }
   rc = check_launch("recent_fused");
   if (rc != TGX_OK || !L.want_plan || L.fuse_plan) return rc;
