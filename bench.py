@@ -205,8 +205,9 @@ def main():
     torch.cuda.set_device(device)
     # batches: W warm-up, K timed (value), R roofline window (kernel-dispatch events)
     avail = num_batches(cfg)
-    # a short stream (C1) keeps a few batches after the timed work for the CPU baseline
-    reserve = 0 if a.no_cpu else min(64, avail // 10)
+    # a short stream (C1) keeps a few batches after the timed work for the CPU baseline,
+    # also under --no-cpu, so that a profiling run times the same window as the default run
+    reserve = min(64, avail // 10)
     # a short stream still gets a short warm-up (the first batches freeze the CSR,
     # build the launch context and grow the allocator's pools)
     w0 = min(a.warmup, 32, avail // 8)
