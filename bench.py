@@ -57,33 +57,49 @@ def stage_stream(cfg, first: int, count: int, torch, device):
 
 
 def measure_ceilings(torch, device, launch_bytes: int, log) -> dict:
-    """HBM ceilings of plain device kernels: a copy (reads + writes the size) and a
-    store-only fill, at 1 GiB and at the gather launch's byte count, each the best of
-    5 event-timed repetitions after a warm-up."""
+    """HBM ceilings of plain device kernels, each the best of 5 event-timed
+    repetitions after a warm-up: at 1 GiB and at the gather launch's byte count, a
+    copy (the runtime's copy kernel, reads + writes the size), an elementwise copy
+    (torch's vectorized elementwise kernel, `neg` into another buffer) and a
+    store-only fill; then a row gather of the large-row config's shape: 1 KB rows
+    at random from a 6.55 GB table (100,000 nodes x 64 slots, the rows read as
+    16-byte elements) into a 1 GiB output."""
     out = {}
+
+    def timed(key, fn, moved):
+        fn()
+        torch.cuda.synchronize()
+        best = None
+        for _ in range(5):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1)
+            best = ms if best is None else min(best, ms)
+        out[key] = {"bytes": moved, "us": best * 1e3, "GB/s": moved / (best * 1e-3) / 1e9}
+        log(f"ceiling {key}: {moved / 1e6:.1f} MB in {best * 1e3:.1f} us = "
+            f"{moved / (best * 1e-3) / 1e9:.0f} GB/s")
+
     for name, nbytes in (("1GiB", 1 << 30), ("launch", max(launch_bytes, 1 << 20))):
         n = nbytes // 4
         src = torch.ones(n, dtype=torch.float32, device=device)
         dst = torch.empty_like(src)
-        for kind, fn, moved in (("copy", lambda: dst.copy_(src), 2 * n * 4),
-                                ("store", lambda: dst.fill_(2.0), n * 4)):
-            fn()
-            torch.cuda.synchronize()
-            best = None
-            for _ in range(5):
-                e0 = torch.cuda.Event(enable_timing=True)
-                e1 = torch.cuda.Event(enable_timing=True)
-                e0.record()
-                fn()
-                e1.record()
-                torch.cuda.synchronize()
-                ms = e0.elapsed_time(e1)
-                best = ms if best is None else min(best, ms)
-            out[f"{kind}_{name}"] = {"bytes": moved, "us": best * 1e3, "GB/s": moved / (best * 1e-3) / 1e9}
-            log(f"ceiling {kind} {name}: {moved / 1e6:.1f} MB in {best * 1e3:.1f} us = "
-                f"{moved / (best * 1e-3) / 1e9:.0f} GB/s")
+        timed(f"copy_{name}", lambda: dst.copy_(src), 2 * n * 4)
+        timed(f"elementwise_copy_{name}", lambda: torch.neg(src, out=dst), 2 * n * 4)
+        timed(f"store_{name}", lambda: dst.fill_(2.0), n * 4)
         del src, dst
         torch.cuda.synchronize()
+    rows = 1 << 20
+    table = torch.zeros(100_000 * 64, 64, dtype=torch.complex128, device=device)
+    idx = torch.randint(0, table.shape[0], (rows,), device=device)
+    got = torch.empty(rows, 64, dtype=torch.complex128, device=device)
+    timed("row_gather_1KB_1GiB", lambda: torch.index_select(table, 0, idx, out=got),
+          2 * rows * 1024 + rows * 8)
+    del table, idx, got
+    torch.cuda.synchronize()
     return out
 
 
@@ -189,8 +205,8 @@ def main():
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after timing, run a plain device copy of this size (PMC byte calibration)")
     ap.add_argument("--ceilings", action="store_true",
-                    help="after timing, measure the device's copy and store ceilings (torch copy_ / "
-                         "fill_ of 1 GiB and of the gather's write size) and report them")
+                    help="after timing, measure the device's copy, store and row-gather ceilings "
+                         "(plain torch kernels at 1 GiB and at the gather's byte count) and report them")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only: the fused pipeline path has no multi-GPU mode "

@@ -170,7 +170,6 @@ __device__ __forceinline__ u32x4 shfl_v(u32x4 x, int src) {
   return r;
 }
 
-// x / n for x * n < 2^32 (n >= 1): one multiply-high by ceil(2^32 / n)
 // Output stores.  Small-row launches write with ordinary stores (the encodings
 // then stream out of L2 at a higher rate); large-row launches, whose row copy
 // already streams, use nontemporal stores (measured faster for both shapes).
@@ -195,6 +194,7 @@ constexpr int64_t kSplitBytes = 8192;
 // row chunks each lane loads before storing them (large-row copy)
 constexpr int kCopyDepth = 4;
 
+// x / n for x * n < 2^32 (n >= 1): one multiply-high by ceil(2^32 / n)
 struct FastDiv {
   uint32_t n, m;
   // the multiplier of divisor n (computed on the host: a division is tens of
