@@ -190,6 +190,242 @@ def cpu_baseline(cfg, g, pipe, first, seconds, torch, log, last):
             "sample_1thread": f"{cfg.name} batches {b1}..{b1 + nb1 - 1} ({q_1} queries) on 1 thread"}
 
 
+def run_rows(a, log) -> None:
+    """--rows: the functions beside the streaming path, on the C3 graph (1M nodes,
+    16-d bf16 rows): freeze_csr (tgx_csr_build) of a pre-freeze prefix of the
+    stream, recent() on the frozen CSR, recent_2hop() and HistoricalNegPool
+    update + sample.  Each is timed on the device (HIP events; the gathers and the
+    pool as graph replays of successive batches) and priced against its
+    algorithmic bytes, and the oracle's restatement of the same function is timed
+    on a bounded sample whose outputs are compared with the device's.  One JSON
+    line per row."""
+    import numpy as np
+    import torch
+    from oracle import spec  # the CPU legs only
+    from tgengine_amd.pipeline.negatives import HistoricalNegPool
+    from tgengine_amd.synthetic import CONFIGS, make_graph
+    cfg = CONFIGS["c3"]
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    P, R, S = a.rows_batches, 200, a.rows_cpu_batches
+    N, d, K = cfg.num_nodes, cfg.feat_dim, cfg.k
+    rb = d * cfg.feat_bytes
+    t0 = time.time()
+    dev, lens, bts = stage_stream(cfg, 0, P + R, torch, device)
+    offs = np.concatenate([[0], np.cumsum(lens)])
+    log(f"rows: staged {P + R} batches in {time.time() - t0:.1f}s")
+
+    def ev(i):
+        s_, e_ = int(offs[i]), int(offs[i + 1])
+        return dev["src"][s_:e_], dev["dst"][s_:e_], dev["time"][s_:e_], dev["feat"][s_:e_]
+
+    def filled(n):
+        g = make_graph(cfg)
+        for i in range(n):
+            g.advance(*ev(i))
+        torch.cuda.synchronize()
+        return g
+
+    def timed_ms(fn):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1)
+
+    def replay_ms(calls):
+        """HIP-event time of one replay of a graph that captures calls()."""
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            kept = calls()
+        graph.replay()
+        ms = min(timed_ms(graph.replay) for _ in range(3))
+        return ms, kept
+
+    def line(row, workload, unit, value, ms, nbytes, cpu, parity, extra=None):
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out = {"row": row, "metric": f"{unit} ({row})", "value": value, "unit": unit,
+               "ms_per_call": ms, "workload": workload,
+               "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                            "frac": gbs / PEAK_HBM_GBS, "bytes_per_call": nbytes},
+               "cpu_baseline": cpu, "parity": parity}
+        out.update(extra or {})
+        print(json.dumps(out), flush=True)
+
+    def gather_bytes(masks, k):
+        """recent() without encodings: per query the CSR offsets (16 B) and V taken
+        entries (id, time, row) read; K slots (id, time, row, mask) written."""
+        q = sum(int(m.shape[0]) for m in masks)
+        v = sum(int(m.sum()) for m in masks)
+        return q * 16 + v * (12 + rb) + q * k * (13 + rb), q, v
+
+    # ---- freeze_csr: P batches frozen on a fresh graph, three times ----
+    E = int(offs[P])
+    gw = filled(4)
+    gw.freeze_csr()
+    del gw
+    fr = []
+    for rep in range(3):
+        g = filled(P)
+        fr.append(timed_ms(g.freeze_csr))
+        if rep < 2:
+            del g
+            torch.cuda.synchronize()
+    ms = min(fr)
+    fbytes = E * (24 + rb) + 2 * E * (12 + rb) + (N + 1) * 8
+    # CPU: the oracle's freeze of the first S batches, compared with a device freeze of them
+    evs = [(bt["src"], bt["dst"], bt["time"], bt["feat"], int(offs[i])) for i, bt in enumerate(bts[:S])]
+    c0 = time.perf_counter()
+    csr_s = spec.csr_freeze(N, d, evs, feat_dtype=np.uint16)
+    cs = time.perf_counter() - c0
+    gs = filled(S)
+    gs.freeze_csr()
+    same = (np.array_equal(gs._offsets.cpu().numpy(), csr_s.offsets)
+            and np.array_equal(gs._nbr_ids.cpu().numpy(), csr_s.ids)
+            and np.array_equal(gs._nbr_times.cpu().numpy().view(np.int64), csr_s.times.view(np.int64))
+            and np.array_equal(gs._nbr_feats.view(torch.int16).cpu().numpy().view(np.uint16), csr_s.feats))
+    del gs
+    if not same:
+        raise RuntimeError("rows: the device CSR of the sample differs from the oracle's")
+    ES = int(offs[S])
+    line("csr_build", f"freeze_csr of C3 batches 0..{P - 1}: {E} events, {2 * E} directed entries, "
+         f"{N} nodes, {d}-d bf16 rows", "events/s", E / (ms * 1e-3), ms, fbytes,
+         {"value": ES / cs, "unit": "events/s", "cores": 1, "kind": "port",
+          "sample": f"oracle.spec.csr_freeze (numpy) of batches 0..{S - 1} ({ES} events)"},
+         f"CSR arrays of batches 0..{S - 1} equal to the oracle's", {"reps_ms": fr})
+    log(f"rows: csr_build {ms:.2f} ms for {E} events")
+
+    # ---- recent() on the frozen CSR: the next R batches' src/dst/neg queries ----
+    qs = []
+    for i in range(P, P + R):
+        s_, d_, t_, _ = ev(i)
+        neg = dev["neg"][int(offs[i]):int(offs[i + 1])].reshape(-1)
+        qs.append((torch.cat([s_, d_, neg]), torch.cat([t_, t_, t_])))
+    ref = g.recent(qs[0][0], qs[0][1], K)
+    torch.cuda.synchronize()
+
+    def recent_calls():
+        return [g.recent(n_, t_, K).mask for (n_, t_) in qs]
+    ms, masks = replay_ms(recent_calls)
+    ms /= R
+    nbytes, q, v = gather_bytes(masks, K)
+    nbytes //= R
+    # CPU: the oracle's recent() over the full CSR, for the first batch's queries
+    evs_all = [(bt["src"], bt["dst"], bt["time"], bt["feat"], int(offs[i])) for i, bt in enumerate(bts[:P])]
+    csr_all = spec.csr_freeze(N, d, evs_all, feat_dtype=np.uint16)
+    del evs_all
+    n0, t0_ = qs[0][0].cpu().numpy(), qs[0][1].cpu().numpy()
+    c0 = time.perf_counter()
+    o = spec.recent(n0, t0_, K, csr_all, None, d, feat_dtype=np.uint16)
+    cs = time.perf_counter() - c0
+    same = (np.array_equal(ref.neighbor_ids.cpu().numpy(), o.ids) and np.array_equal(ref.mask.cpu().numpy(), o.mask)
+            and np.array_equal(ref.timestamps.cpu().numpy().view(np.int64), o.times.view(np.int64))
+            and np.array_equal(ref.edge_feats.view(torch.int16).cpu().numpy().view(np.uint16), o.feats))
+    if not same:
+        raise RuntimeError("rows: recent() on the frozen CSR differs from the oracle's")
+    line("recent_csr", f"recent() of C3 batches {P}..{P + R - 1}'s src/dst/neg ({q // R} queries per call, "
+         f"K={K}) on the frozen CSR of batches 0..{P - 1}, mean V {v / q:.2f}", "queries/s", q / (ms * 1e-3 * R),
+         ms, nbytes, {"value": len(n0) / cs, "unit": "queries/s", "cores": 1, "kind": "port",
+                      "sample": f"oracle.spec.recent (numpy) of batch {P}'s {len(n0)} queries"},
+         f"batch {P}'s ids, times, rows and masks equal to the oracle's",
+         {"timing": f"HIP event pair around a graph replay of {R} calls"})
+    log(f"rows: recent_csr {ms * 1e3:.2f} us per call")
+
+    # ---- recent_2hop(): each next batch's src, k1 = k2 = K ----
+    R2 = 50
+    ref2 = g.recent_2hop(qs[0][0][:lens[P]], qs[0][1][:lens[P]], K, K)
+    torch.cuda.synchronize()
+
+    def hop_calls():
+        out = []
+        for i in range(R2):
+            b_ = lens[P + i]
+            r_ = g.recent_2hop(qs[i][0][:b_], qs[i][1][:b_], K, K)
+            out += [r_.mask, r_.hop2_mask.reshape(-1, K)]
+        return out
+    ms, masks = replay_ms(hop_calls)
+    ms /= R2
+    nbytes, q, v = gather_bytes(masks, K)
+    nbytes //= R2
+    ns = 500
+    n1, t1 = n0[:ns], t0_[:ns]
+    c0 = time.perf_counter()
+    h1 = spec.recent(n1, t1, K, csr_all, None, d, feat_dtype=np.uint16)
+    n2 = np.where(h1.mask, h1.ids, -1).reshape(-1).astype(np.int64)
+    h2 = spec.recent(n2, h1.times.reshape(-1), K, csr_all, None, d, feat_dtype=np.uint16)
+    cs = time.perf_counter() - c0
+    m2 = h2.mask.reshape(ns, K, K)
+    same = (np.array_equal(ref2.neighbor_ids[:ns].cpu().numpy(), h1.ids)
+            and np.array_equal(ref2.hop2_mask[:ns].cpu().numpy(), m2)
+            and np.array_equal(ref2.hop2_ids[:ns].cpu().numpy(), np.where(m2, h2.ids.reshape(ns, K, K), -1)))
+    if not same:
+        raise RuntimeError("rows: recent_2hop differs from the oracle's composition")
+    line("recent_2hop", f"recent_2hop() of C3 batches {P}..{P + R2 - 1}'s src ({lens[P]} queries per call, "
+         f"k1=k2={K}: {lens[P] * K} hop-2 queries) on the frozen CSR", "hop-2 queries/s",
+         sum(lens[P:P + R2]) * K / (ms * 1e-3 * R2), ms, nbytes,
+         {"value": ns * K / cs, "unit": "hop-2 queries/s", "cores": 1, "kind": "port",
+          "sample": f"oracle.spec.recent twice (numpy), batch {P}'s first {ns} src queries"},
+         f"hop-1 ids and hop-2 ids and masks of batch {P}'s first {ns} queries equal to the oracle's",
+         {"timing": f"HIP event pair around a graph replay of {R2} calls (two launches each)"})
+    log(f"rows: recent_2hop {ms * 1e3:.2f} us per call")
+    del g, csr_all
+    torch.cuda.synchronize()
+
+    # ---- HistoricalNegPool: update with batch i's edges, then sample batch i's src ----
+    Pp = 512
+    pool = HistoricalNegPool(N, Pp, device=str(device), seed=12345)
+    for i in range(4):
+        s_, d_, _, _ = ev(i)
+        pool.update(s_, d_)
+        pool.sample(s_)
+    torch.cuda.synchronize()
+
+    def pool_calls():
+        out = []
+        for i in range(4, 4 + R):
+            s_, d_, _, _ = ev(i)
+            pool.update(s_, d_)
+            out.append(pool.sample(s_))
+        return out
+    ms, _ = replay_ms(pool_calls)
+    ms /= R
+    nev = sum(lens[4:4 + R]) / R
+    nbytes = int(nev * (16 + 8 + 4 + 8) + nev * (8 + 8 + 4 + 8))
+    del pool
+    torch.cuda.synchronize()
+    # CPU: the oracle's edge-by-edge update and sample over the first S2 batches of a
+    # fresh pool, compared call by call with a fresh device pool of the same seed
+    S2 = min(S, 20)
+    pool = HistoricalNegPool(N, Pp, device=str(device), seed=777)
+    cp = np.full((N, Pp), -1, np.int32)
+    cc = np.zeros(N, np.int64)
+    cs = 0.0
+    for i in range(S2):
+        s_, d_, _, _ = ev(i)
+        pool.update(s_, d_)
+        got = pool.sample(s_).cpu().numpy()
+        c0 = time.perf_counter()
+        spec.negpool_update(cp, cc, bts[i]["src"], bts[i]["dst"], 777, 2 * i)
+        want = spec.negpool_sample(cp, cc, bts[i]["src"], 777, 2 * i + 1)
+        cs += time.perf_counter() - c0
+        if not np.array_equal(got, want):
+            raise RuntimeError(f"rows: negative pool sample {i} differs from the oracle's")
+    if not (np.array_equal(pool._pool.cpu().numpy(), cp) and np.array_equal(pool._count.cpu().numpy(), cc)):
+        raise RuntimeError("rows: negative pool state differs from the oracle's")
+    del pool, cp
+    ES2 = int(offs[S2])
+    line("negpool", f"HistoricalNegPool({N} nodes, pool {Pp}): update with a C3 batch's edges, then sample its "
+         f"src ({nev:.0f} edges per call, batches 4..{3 + R})", "edges/s", nev / (ms * 1e-3), ms, nbytes,
+         {"value": ES2 / cs, "unit": "edges/s", "cores": 1, "kind": "port",
+          "sample": f"oracle.spec.negpool_update + negpool_sample (numpy), batches 0..{S2 - 1} ({ES2} edges)"},
+         f"every sample of batches 0..{S2 - 1} and the final pool and counts equal to the oracle's",
+         {"timing": f"HIP event pair around a graph replay of {R} update + sample pairs"})
+    log(f"rows: negpool {ms * 1e3:.2f} us per update + sample")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -204,6 +440,13 @@ def main():
                     help="batches after the timed region whose prepare kernels are timed back to back")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after timing, run a plain device copy of this size (PMC byte calibration)")
+    ap.add_argument("--rows", action="store_true",
+                    help="instead of the streaming step, time the rows beside it (freeze_csr, recent() "
+                         "on the frozen CSR, recent_2hop, the negative pool), one JSON line each")
+    ap.add_argument("--rows-batches", type=int, default=2500,
+                    help="--rows: C3 batches frozen into the CSR")
+    ap.add_argument("--rows-cpu-batches", type=int, default=100,
+                    help="--rows: C3 batches in the oracle's samples")
     ap.add_argument("--ceilings", action="store_true",
                     help="after timing, measure the device's copy, store and row-gather ceilings "
                          "(plain torch kernels at 1 GiB and at the gather's byte count) and report them")
@@ -213,6 +456,9 @@ def main():
               f"(asked for --gpus {a.gpus}); see DESIGN.md for how it would shard.", file=sys.stderr)
         sys.exit(2)
     log = (lambda *x: None) if a.quiet else (lambda *x: print(*x, file=sys.stderr, flush=True))
+    if a.rows:
+        run_rows(a, log)
+        return
 
     import torch
     from tgengine_amd.synthetic import CONFIGS, make_graph, make_pipeline, num_batches

@@ -43,6 +43,30 @@ def test_negpool_matches_the_oracle(N, P, b):
     assert st[0] == 5  # the five out-of-range sources of call 3
 
 
+@pytest.mark.parametrize("n", [1, 63, 64, 65, 1000, 4095, 4096, 4097, 9000])
+def test_negpool_batch_sizes(n):
+    """Batches on both sides of the single-workgroup update (at most 4,096 edges)
+    and at the sort network's padding edges: three updates of n edges each, hot
+    sources and a two-slot pool (many edges on one cell), pool and counts bit for
+    bit after every call."""
+    N, P = 64, 2
+    rng = np.random.default_rng(n)
+    pool = HistoricalNegPool(N, pool_size=P, device="cuda", seed=99 + n)
+    ref = np.full((N, P), -1, np.int32)
+    cnt = np.zeros(N, np.int64)
+    for call in range(3):
+        src = rng.integers(0, N, n)
+        src[: n // 2] = rng.integers(0, 2, n // 2)
+        if n > 8:
+            src[3] = -1
+            src[7] = N
+        dst = rng.integers(0, 1 << 30, n)
+        pool.update(torch.from_numpy(src).cuda(), torch.from_numpy(dst).cuda())
+        O.negpool_update(ref, cnt, src, dst, pool.seed, 2 * call)
+        _check(pool, ref, cnt, f"n={n} update {call}")
+        pool._call += 1  # the sample call the reference stream would make
+
+
 def test_negpool_empty_and_fresh_sources():
     pool = HistoricalNegPool(30, pool_size=8, device="cuda", seed=5)
     pool.update(torch.empty(0, dtype=torch.int64, device="cuda"), torch.empty(0, dtype=torch.int64, device="cuda"))
