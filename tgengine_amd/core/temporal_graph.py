@@ -377,8 +377,15 @@ class TemporalGraph:
                 raise IndexError("advance() got node ids outside [0, num_nodes)")
             to = torch.cat([t for (s_, t_, _, _, _) in batches for t in (t_, s_)])
             tt = torch.cat([tm for (_, _, tm, _, _) in batches for _ in (0, 1)])
-            ev = torch.cat([torch.arange(eb, eb + s_.shape[0], dtype=torch.int64, device=dev)
-                            for (s_, _, _, _, eb) in batches for _ in (0, 1)])
+            # edge ids eb + i of each batch's two directed segments, in one pass:
+            # entry e of a segment starting at entry s with base eb is eb + (e - s)
+            seg_len = torch.tensor([int(s_.shape[0]) for (s_, _, _, _, _) in batches for _ in (0, 1)],
+                                   dtype=torch.int64)
+            seg_base = torch.tensor([int(eb) for (_, _, _, _, eb) in batches for _ in (0, 1)],
+                                    dtype=torch.int64)
+            seg_shift = (seg_base - (torch.cumsum(seg_len, 0) - seg_len)).to(dev)
+            ev = (torch.repeat_interleave(seg_shift, seg_len.to(dev), output_size=n)
+                  + torch.arange(n, dtype=torch.int64, device=dev))
             # event-major feature rows (row eb + i of the event), zeros for None
             feats = None
             if d > 0 and any(f is not None for (_, _, _, f, _) in batches):
