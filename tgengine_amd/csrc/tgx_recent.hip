@@ -207,15 +207,28 @@ struct FastDiv {
 };
 
 // smallest i in [lo, hi] with i == hi or t[i] >= q (t ascending); wave-uniform result
+template <bool CLAMP>
 __device__ __forceinline__ int64_t wave_lower_bound(const double* __restrict__ t, int64_t lo,
                                                     int64_t hi, double q, int lane) {
   while (hi - lo > kWave) {
     const int64_t step = (hi - lo + kWave - 1) / kWave;
-    const int64_t pos = lo + static_cast<int64_t>(lane + 1) * step - 1;
-    const bool pr = pos < hi && t[pos] < q;
-    const int c = __popcll(__ballot(pr));
-    const int64_t pc = lo + static_cast<int64_t>(c + 1) * step - 1;
-    lo = lo + static_cast<int64_t>(c) * step;
+    const int64_t pos0 = lo + static_cast<int64_t>(lane + 1) * step - 1;
+    int64_t pc, nl;
+    if constexpr (CLAMP) {
+      // probes clamped to the window's last entry, so they stay in order and the
+      // top lane reads t[hi - 1]: a query after the whole window ends in one round
+      const int64_t pos = pos0 < hi ? pos0 : hi - 1;
+      const int c = __popcll(__ballot(t[pos] < q));
+      pc = lo + static_cast<int64_t>(c + 1) * step - 1;
+      nl = lo + static_cast<int64_t>(c) * step;
+      nl = nl < hi ? nl : hi;  // every probe below q: lo = hi, and the search ends
+    } else {
+      const bool pr = pos0 < hi && t[pos0] < q;
+      const int c = __popcll(__ballot(pr));
+      pc = lo + static_cast<int64_t>(c + 1) * step - 1;
+      nl = lo + static_cast<int64_t>(c) * step;
+    }
+    lo = nl;
     hi = pc < hi ? pc : hi;
   }
   const int64_t pos = lo + lane;
@@ -553,7 +566,7 @@ void recent_fused(Params P) {
       if (lh && nh >= 0) {
         const int64_t s0 = P.c_off[nh];
         const int64_t s1 = P.c_off[nh + 1];
-        const int64_t cnt = wave_lower_bound(P.c_times, s0, s1, th, lane) - s0;
+        const int64_t cnt = wave_lower_bound<TILES>(P.c_times, s0, s1, th, lane) - s0;
         const int take = static_cast<int>(cnt < K ? cnt : K);
         if (h == hh) {
           ncsr = take;
