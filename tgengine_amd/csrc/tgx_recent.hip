@@ -111,7 +111,10 @@ struct Params {
   int m, lg_bp;
   // FastDiv multipliers of K, d_t / 4, d_t and nch
   uint32_t fd_k, fd_q, fd_d, fd_c;
-  int split;  // wavefronts per query (m == 1): each writes every split-th output chunk
+  // wavefronts per query (m == 1), each writing every split-th output chunk: the
+  // count itself for tiled launches, its log2 for the others (each copy of the
+  // kernel divides or shifts, whichever measured faster there)
+  int split;
   // fused ring plan: workgroups [0, plan_blocks) plan the caller's next batch
   PlanParams pl;
   int plan_blocks;
@@ -510,9 +513,9 @@ void recent_fused(Params P) {
 
   // ---- the wave's queries: query slot wv / split of the workgroup; the split
   // waves of one query repeat its (cheap) gather and share its outputs ----
-  const int split = P.split;
-  const int qs = wv / split;
-  const int part = wv - qs * split;
+  const int split = TILES ? P.split : 1 << P.split;
+  const int qs = TILES ? wv / split : wv >> P.split;
+  const int part = TILES ? wv - qs * split : wv & (split - 1);
   int64_t q;
   if (!TILES && P.plan_mode != TGX_PLAN_TILES) {
     q = query_of(P, g, qs);
@@ -1116,7 +1119,8 @@ int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args
     while (split < 8 && qbytes / (split * 2) >= kSplitBytes && qwant * split * 2 <= kMaxWaves)
       split *= 2;
   }
-  P.split = split;
+  const int lg_split = split == 1 ? 0 : split == 2 ? 1 : split == 4 ? 2 : 3;  // split is 1, 2, 4 or 8
+  P.split = mode == TGX_PLAN_TILES ? split : lg_split;
   // tiles: `group` query slots per workgroup, fewer when split waves fill it
   int qslots = a->group;
   if (mode == TGX_PLAN_TILES && qslots * split > kMaxWaves) qslots = kMaxWaves / split;
@@ -1243,7 +1247,7 @@ extern "C" int tgx_recent_launch_shape(const tgx_ring* ring, const tgx_csr* csr,
   shape[1] = L.threads;
   shape[2] = static_cast<int64_t>(L.lds);
   shape[3] = L.P.m;
-  shape[4] = L.P.split;
+  shape[4] = L.P.plan_mode == TGX_PLAN_TILES ? L.P.split : 1 << L.P.split;
   shape[5] = static_cast<int64_t>(L.qslots) * L.P.m;
   shape[6] = L.P.plan_blocks;
   shape[7] = L.vec;
