@@ -43,12 +43,12 @@ def test_negpool_matches_the_oracle(N, P, b):
     assert st[0] == 5  # the five out-of-range sources of call 3
 
 
-@pytest.mark.parametrize("n", [1, 63, 64, 65, 1000, 4095, 4096, 4097, 9000])
+@pytest.mark.parametrize("n", [1, 63, 64, 65, 1000, 4095, 4096, 4097, 5000, 8191, 8192, 8193, 12000])
 def test_negpool_batch_sizes(n):
-    """Batches on both sides of the single-workgroup update (at most 4,096 edges)
-    and at the sort network's padding edges: three updates of n edges each, hot
-    sources and a two-slot pool (many edges on one cell), pool and counts bit for
-    bit after every call."""
+    """Batch sizes on both sides of the single-workgroup updates (at most 4,096 and
+    8,192 edges, one thread per edge and round) and at a wavefront's boundary: three
+    updates of n edges each, hot sources and a two-slot pool (many edges on one
+    cell), pool and counts bit for bit after every call."""
     N, P = 64, 2
     rng = np.random.default_rng(n)
     pool = HistoricalNegPool(N, pool_size=P, device="cuda", seed=99 + n)

@@ -152,54 +152,65 @@ __global__ __launch_bounds__(kThreads) void np_sample(const int32_t* __restrict_
     atomicAdd(&status[TGX_ST_BAD_QUERY_NODE], __popcll(bm));
 }
 
-// Batches of at most kNpSmall edges: the whole update in one workgroup (the
+// Batches of at most 8,192 edges: the whole update in one workgroup (the
 // sort-based path above costs some 25 launches, which a small batch cannot
 // amortise).  Edge j is element j, held by thread j % 1024 in round j / 1024.
 //
-//   1. every source gets a slot of an LDS hash table (open addressing, 8,192
-//      slots for at most 4,096 sources); an out-of-range source gets key 8,192;
-//   2. a stable LSD radix sort of the words key << 12 | j by the 14-bit key, two
-//      passes of 7 bits: per round a wavefront ranks its 64 elements by digit
+//   1. every source gets a slot of an LDS hash table (open addressing, twice as
+//      many slots as edges); an out-of-range source gets the key after the slots;
+//   2. a stable LSD radix sort of the words key << IBITS | j by the key, in PASSES
+//      passes of DBITS bits: per round a wavefront ranks its 64 elements by digit
 //      with ballots, the (digit, round, wavefront) counts are scanned in that
 //      order, and each element lands at its offset plus its rank -- so a
 //      source's edges end up together, in batch order;
 //   3. rank r = position - first position of the key, the decision as on the
 //      sort-based path, and the count added at the last position of each key;
 //   4. accepted edges meet in a second LDS hash table on their cell u * P + slot,
-//      whose entry keeps the largest cell << 12 | j (atomicMax): that edge, the
+//      whose entry keeps the largest cell << IBITS | j (atomicMax): that edge, the
 //      batch's latest on the cell, writes it.
-constexpr int kNpSmall = 4096;
 constexpr int kNpSmallThreads = 1024;
 constexpr int kNpWaves = kNpSmallThreads / kWave;
-constexpr int kNpPer = kNpSmall / kNpSmallThreads;  // rounds (elements per thread)
-constexpr int kNpSlots = 8192;                       // hash slots of both tables
-constexpr int kNpBadKey = kNpSlots;                  // sorts after every slot
-constexpr int kNpDigitBits = 7;
-constexpr int kNpDigits = 1 << kNpDigitBits;
-constexpr int kNpTable = kNpDigits * kNpPer * kNpWaves;  // (digit, round, wavefront) counts
 constexpr int kNpEmpty = -1;
 constexpr uint64_t kNpNone = ~uint64_t(0);
-static_assert(kNpSmall <= 4096, "edge indices take 12 bits of a sort word");
-static_assert(kNpBadKey < (1 << (2 * kNpDigitBits)), "two digit passes cover the key");
-static_assert(kNpTable % kNpSmallThreads == 0, "the scan takes whole runs per thread");
-// LDS: the source table (int32) and the sort's two element arrays (uint32) share
-// bytes [0, 64 KB) with the later cell table (uint64); the count table follows
-constexpr size_t kNpLdsSrc = 0;
-constexpr size_t kNpLdsSort = kNpSlots * 4;
-constexpr size_t kNpLdsCell = 0;
-constexpr size_t kNpLdsTable = kNpSlots * 8;
-constexpr size_t kNpLds = kNpLdsTable + kNpTable * 4;
-static_assert(kNpLdsSort + 2 * kNpSmall * 4 <= kNpLdsTable, "the sort arrays end before the count table");
 
-__device__ __forceinline__ uint32_t np_hash32(uint32_t u) { return (u * 2654435761u) >> (32 - 13); }
+template <int CAP, int DBITS, int PASSES>
+struct NpShape {
+  static constexpr int kPer = CAP / kNpSmallThreads;  // rounds (elements per thread)
+  static constexpr int kIBits = CAP == 4096 ? 12 : 13;  // edge index bits
+  static constexpr int kSlots = 2 * CAP;                // hash slots of both tables
+  static constexpr int kSlotBits = kIBits + 1;
+  static constexpr int kBadKey = kSlots;                // sorts after every slot
+  static constexpr int kDigits = 1 << DBITS;
+  static constexpr int kTable = kDigits * kPer * kNpWaves;  // (digit, round, wavefront) counts
+  // LDS: the source table (int32) and the sort's two element arrays (uint32) share
+  // the bytes of the later cell table (uint64); the count table follows
+  static constexpr size_t kLdsSort = static_cast<size_t>(kSlots) * 4;
+  static constexpr size_t kLdsTable = static_cast<size_t>(kSlots) * 8;
+  static constexpr size_t kLds = kLdsTable + static_cast<size_t>(kTable) * 4;
+  static_assert((1 << kIBits) == CAP, "edge indices fill their bits");
+  static_assert(kBadKey < (1 << (DBITS * PASSES)), "the passes cover the key");
+  static_assert(kSlotBits + 1 + kIBits <= 32, "a sort word is 32 bits");
+  static_assert(kTable % kNpSmallThreads == 0, "the scan takes whole runs per thread");
+  static_assert(kLdsSort + 2 * static_cast<size_t>(CAP) * 4 <= kLdsTable, "the sort arrays end before the count table");
+  static_assert(kLds <= 160 * 1024, "the workgroup's LDS");
+};
+using NpSmall = NpShape<4096, 7, 2>;
+using NpMid = NpShape<8192, 5, 3>;
+
+template <class S>
+__device__ __forceinline__ uint32_t np_hash32(uint32_t u) {
+  return (u * 2654435761u) >> (32 - S::kSlotBits);
+}
+template <class S>
 __device__ __forceinline__ uint32_t np_hash64(uint64_t c) {
-  return static_cast<uint32_t>((c * 0x9e3779b97f4a7c15ull) >> (64 - 13));
+  return static_cast<uint32_t>((c * 0x9e3779b97f4a7c15ull) >> (64 - S::kSlotBits));
 }
 
-// exclusive scan of tab[0, kNpTable) in place by the workgroup (each thread a run
-// of kNpTable / kNpSmallThreads entries); wsum: kNpWaves ints of LDS
+// exclusive scan of tab[0, kTable) in place by the workgroup (each thread a run of
+// kTable / kNpSmallThreads entries); wsum: kNpWaves ints of LDS
+template <class S>
 __device__ void np_scan(int32_t* tab, int32_t* wsum) {
-  constexpr int per = kNpTable / kNpSmallThreads;
+  constexpr int per = S::kTable / kNpSmallThreads;
   const int t = static_cast<int>(threadIdx.x);
   const int lane = t & (kWave - 1);
   const int wv = t / kWave;
@@ -230,104 +241,118 @@ __device__ void np_scan(int32_t* tab, int32_t* wsum) {
 }
 
 // one stable pass: elements src[0, n) (round k of thread t at k * 1024 + t) to
-// dst by the digit (key >> shift) & (kNpDigits - 1) of the word's key (word >> 12)
+// dst by the digit (key >> shift) & (kDigits - 1) of the word's key
+template <class S, int DBITS>
 __device__ void np_radix_pass(const uint32_t* src, uint32_t* dst, int n, int shift, int32_t* tab,
                               int32_t* wsum) {
   const int t = static_cast<int>(threadIdx.x);
   const int lane = t & (kWave - 1);
   const int wv = t / kWave;
   const uint64_t below = (uint64_t(1) << lane) - 1;
-  for (int i = t; i < kNpTable; i += kNpSmallThreads) tab[i] = 0;
+  for (int i = t; i < S::kTable; i += kNpSmallThreads) tab[i] = 0;
   __syncthreads();
-  uint32_t e[kNpPer];
-  int dig[kNpPer], rank[kNpPer];
+  uint32_t e[S::kPer];
+  int dig[S::kPer], rank[S::kPer];
 #pragma unroll
-  for (int k = 0; k < kNpPer; ++k) {
+  for (int k = 0; k < S::kPer; ++k) {
     const int i = k * kNpSmallThreads + t;
     const bool valid = i < n;
     e[k] = valid ? src[i] : 0u;
-    const int d = static_cast<int>((e[k] >> 12 >> shift) & (kNpDigits - 1));
+    const int d = static_cast<int>((e[k] >> S::kIBits >> shift) & (S::kDigits - 1));
     uint64_t m = __ballot(valid);
 #pragma unroll
-    for (int b = 0; b < kNpDigitBits; ++b) {
+    for (int b = 0; b < DBITS; ++b) {
       const uint64_t bb = __ballot(valid && ((d >> b) & 1));
       m &= ((d >> b) & 1) ? bb : ~bb;
     }
     dig[k] = d;
     rank[k] = __popcll(m & below);
-    if (valid && rank[k] == 0) tab[(d * kNpPer + k) * kNpWaves + wv] = __popcll(m);
+    if (valid && rank[k] == 0) tab[(d * S::kPer + k) * kNpWaves + wv] = __popcll(m);
   }
   __syncthreads();
-  np_scan(tab, wsum);
+  np_scan<S>(tab, wsum);
 #pragma unroll
-  for (int k = 0; k < kNpPer; ++k) {
+  for (int k = 0; k < S::kPer; ++k) {
     const int i = k * kNpSmallThreads + t;
-    if (i < n) dst[tab[(dig[k] * kNpPer + k) * kNpWaves + wv] + rank[k]] = e[k];
+    if (i < n) dst[tab[(dig[k] * S::kPer + k) * kNpWaves + wv] + rank[k]] = e[k];
   }
   __syncthreads();
 }
 
+template <int CAP, int DBITS, int PASSES>
 __global__ __launch_bounds__(kNpSmallThreads) void np_update_small(int32_t* __restrict__ pool,
                                                                    int64_t* __restrict__ count, int64_t N,
                                                                    int P, const int64_t* __restrict__ src,
                                                                    const int64_t* __restrict__ dst, int n,
                                                                    uint64_t seed, uint64_t call,
                                                                    int32_t* __restrict__ status) {
+  using S = NpShape<CAP, DBITS, PASSES>;
+  constexpr int kPer = S::kPer;
+  constexpr int kIBits = S::kIBits;
+  constexpr uint32_t kIMask = (1u << kIBits) - 1;
   extern __shared__ __align__(16) uint8_t lds[];
-  int32_t* hsrc = reinterpret_cast<int32_t*>(lds + kNpLdsSrc);
-  uint32_t* sa = reinterpret_cast<uint32_t*>(lds + kNpLdsSort);
-  uint32_t* sb = sa + kNpSmall;
-  uint64_t* cells = reinterpret_cast<uint64_t*>(lds + kNpLdsCell);
-  int32_t* tab = reinterpret_cast<int32_t*>(lds + kNpLdsTable);
+  int32_t* hsrc = reinterpret_cast<int32_t*>(lds);
+  uint32_t* sa = reinterpret_cast<uint32_t*>(lds + S::kLdsSort);
+  uint32_t* sb = sa + CAP;
+  uint64_t* cells = reinterpret_cast<uint64_t*>(lds);
+  int32_t* tab = reinterpret_cast<int32_t*>(lds + S::kLdsTable);
   __shared__ int32_t wsum[kNpWaves];
   const int t = static_cast<int>(threadIdx.x);
   const int lane = t & (kWave - 1);
 
   // 1. the sources (loaded before any is used) into the source table
-  int64_t us[kNpPer];
+  int64_t us[kPer];
 #pragma unroll
-  for (int k = 0; k < kNpPer; ++k) {
+  for (int k = 0; k < kPer; ++k) {
     const int i = k * kNpSmallThreads + t;
     us[k] = i < n ? src[i] : 0;
   }
-  for (int i = t; i < kNpSlots; i += kNpSmallThreads) hsrc[i] = kNpEmpty;
+  for (int i = t; i < S::kSlots; i += kNpSmallThreads) hsrc[i] = kNpEmpty;
   __syncthreads();
   int nbad = 0;
 #pragma unroll
-  for (int k = 0; k < kNpPer; ++k) {
+  for (int k = 0; k < kPer; ++k) {
     const int i = k * kNpSmallThreads + t;
     const bool bad = i < n && (us[k] < 0 || us[k] >= N);
     nbad += __popcll(__ballot(bad));
     if (i < n) {
-      int key = kNpBadKey;
+      int key = S::kBadKey;
       if (!bad) {
         const int32_t u = static_cast<int32_t>(us[k]);
-        uint32_t h = np_hash32(static_cast<uint32_t>(u));
-        for (;;) {  // ends: at most kNpSmall of the kNpSlots slots are ever taken
+        uint32_t h = np_hash32<S>(static_cast<uint32_t>(u));
+        for (;;) {  // ends: at most CAP of the kSlots slots are ever taken
           int32_t cur = hsrc[h];
           if (cur == kNpEmpty) cur = atomicCAS(&hsrc[h], kNpEmpty, u);
           if (cur == kNpEmpty || cur == u) break;
-          h = (h + 1) & (kNpSlots - 1);
+          h = (h + 1) & (S::kSlots - 1);
         }
         key = static_cast<int>(h);
       }
-      sa[i] = static_cast<uint32_t>(key) << 12 | static_cast<uint32_t>(i);
+      sa[i] = static_cast<uint32_t>(key) << kIBits | static_cast<uint32_t>(i);
     }
   }
   if (lane == 0 && nbad != 0 && status != nullptr) atomicAdd(&status[TGX_ST_BAD_EVENT_NODE], nbad);
   __syncthreads();
 
-  // 2. stable sort by key: low digit, then high digit
-  np_radix_pass(sa, sb, n, 0, tab, wsum);
-  np_radix_pass(sb, sa, n, kNpDigitBits, tab, wsum);
+  // 2. stable sort by key, lowest digit first (the result is back in sa)
+  uint32_t* from = sa;
+  uint32_t* to = sb;
+#pragma unroll
+  for (int pass = 0; pass < PASSES; ++pass) {
+    np_radix_pass<S, DBITS>(from, to, n, pass * DBITS, tab, wsum);
+    uint32_t* x = from;
+    from = to;
+    to = x;
+  }
+  const uint32_t* sorted = from;
 
   // 3. position p: rank r among the key's edges, the source's count (loaded
   //    before any is used), the decision; the key's last position adds its length
-  uint32_t pu[kNpPer], pj[kNpPer];
-  int pr[kNpPer], plen[kNpPer];
-  int64_t pc[kNpPer];
+  uint32_t pu[kPer], pj[kPer];
+  int pr[kPer], plen[kPer];
+  int64_t pc[kPer];
 #pragma unroll
-  for (int k = 0; k < kNpPer; ++k) {
+  for (int k = 0; k < kPer; ++k) {
     const int p = k * kNpSmallThreads + t;
     pu[k] = 0;
     pj[k] = 0;
@@ -335,15 +360,15 @@ __global__ __launch_bounds__(kNpSmallThreads) void np_update_small(int32_t* __re
     plen[k] = 0;
     pc[k] = 0;
     if (p < n) {
-      const uint32_t x = sa[p];
-      const uint32_t key = x >> 12;
-      pj[k] = x & 0xfffu;
-      if (key != static_cast<uint32_t>(kNpBadKey)) {
-        const uint32_t first = key << 12;
+      const uint32_t x = sorted[p];
+      const uint32_t key = x >> kIBits;
+      pj[k] = x & kIMask;
+      if (key != static_cast<uint32_t>(S::kBadKey)) {
+        const uint32_t first = key << kIBits;
         int lo = 0, hi = p;
         while (lo < hi) {
           const int mid = (lo + hi) >> 1;
-          if (sa[mid] < first)
+          if (sorted[mid] < first)
             lo = mid + 1;
           else
             hi = mid;
@@ -351,13 +376,13 @@ __global__ __launch_bounds__(kNpSmallThreads) void np_update_small(int32_t* __re
         pu[k] = static_cast<uint32_t>(hsrc[key]);
         pr[k] = p - lo;
         pc[k] = count[pu[k]];
-        if (p + 1 == n || (sa[p + 1] >> 12) != key) plen[k] = p - lo + 1;
+        if (p + 1 == n || (sorted[p + 1] >> kIBits) != key) plen[k] = p - lo + 1;
       }
     }
   }
-  uint64_t cell[kNpPer];
+  uint64_t cell[kPer];
 #pragma unroll
-  for (int k = 0; k < kNpPer; ++k) {
+  for (int k = 0; k < kPer; ++k) {
     cell[k] = kNpNone;
     if (pr[k] >= 0) {
       const uint32_t j = pj[k];
@@ -373,43 +398,43 @@ __global__ __launch_bounds__(kNpSmallThreads) void np_update_small(int32_t* __re
   }
   __syncthreads();  // every read of the counts, the sorted words and the source table is done
 #pragma unroll
-  for (int k = 0; k < kNpPer; ++k)
+  for (int k = 0; k < kPer; ++k)
     if (plen[k] > 0) count[pu[k]] += plen[k];
 
-  // 4. the cell table: the largest cell << 12 | j per cell
-  for (int i = t; i < kNpSlots; i += kNpSmallThreads) cells[i] = kNpNone;
+  // 4. the cell table: the largest cell << kIBits | j per cell
+  for (int i = t; i < S::kSlots; i += kNpSmallThreads) cells[i] = kNpNone;
   __syncthreads();
-  uint32_t ch[kNpPer];
+  uint32_t ch[kPer];
 #pragma unroll
-  for (int k = 0; k < kNpPer; ++k) {
+  for (int k = 0; k < kPer; ++k) {
     ch[k] = 0;
     if (cell[k] != kNpNone) {
-      const uint64_t word = cell[k] << 12 | pj[k];
-      uint32_t h = np_hash64(cell[k]);
-      for (;;) {  // ends: at most kNpSmall of the kNpSlots slots are ever taken
+      const uint64_t word = cell[k] << kIBits | pj[k];
+      uint32_t h = np_hash64<S>(cell[k]);
+      for (;;) {  // ends: at most CAP of the kSlots slots are ever taken
         const uint64_t old = atomicCAS(reinterpret_cast<unsigned long long*>(&cells[h]),
                                        static_cast<unsigned long long>(kNpNone),
                                        static_cast<unsigned long long>(word));
         if (old == kNpNone) break;
-        if ((old >> 12) == cell[k]) {
+        if ((old >> kIBits) == cell[k]) {
           atomicMax(reinterpret_cast<unsigned long long*>(&cells[h]), static_cast<unsigned long long>(word));
           break;
         }
-        h = (h + 1) & (kNpSlots - 1);
+        h = (h + 1) & (S::kSlots - 1);
       }
       ch[k] = h;
     }
   }
   __syncthreads();
-  int64_t val[kNpPer];
-  bool win[kNpPer];
+  int64_t val[kPer];
+  bool win[kPer];
 #pragma unroll
-  for (int k = 0; k < kNpPer; ++k) {
-    win[k] = cell[k] != kNpNone && (cells[ch[k]] & 0xfffu) == pj[k];
+  for (int k = 0; k < kPer; ++k) {
+    win[k] = cell[k] != kNpNone && (cells[ch[k]] & kIMask) == pj[k];
     val[k] = win[k] ? dst[pj[k]] : 0;
   }
 #pragma unroll
-  for (int k = 0; k < kNpPer; ++k)
+  for (int k = 0; k < kPer; ++k)
     if (win[k]) pool[cell[k]] = static_cast<int32_t>(val[k]);
 }
 
@@ -471,15 +496,24 @@ extern "C" int tgx_negpool_update(int32_t* pool, int64_t* count, int64_t num_nod
   if (workspace == nullptr || workspace_bytes < w.total)
     return fail(TGX_ERR_ARG, "tgx_negpool_update: workspace of %zu bytes needed, got %zu", w.total,
                 workspace_bytes);
-  if (n <= kNpSmall) {
+  if (n <= 8192) {
+    // one workgroup: the 4,096-edge shape, or the 8,192-edge one (three digit passes)
     static std::once_flag attr_once;
     std::call_once(attr_once, [] {
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(np_update_small),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kNpLds));
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(np_update_small<4096, 7, 2>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(NpSmall::kLds));
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(np_update_small<8192, 5, 3>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(NpMid::kLds));
       (void)hipGetLastError();
     });
-    hipLaunchKernelGGL(np_update_small, dim3(1), dim3(kNpSmallThreads), kNpLds, stream, pool, count, num_nodes,
-                       static_cast<int>(pool_size), src, dst, static_cast<int>(n), seed, call, status);
+    if (n <= 4096)
+      hipLaunchKernelGGL((np_update_small<4096, 7, 2>), dim3(1), dim3(kNpSmallThreads), NpSmall::kLds, stream,
+                         pool, count, num_nodes, static_cast<int>(pool_size), src, dst, static_cast<int>(n), seed,
+                         call, status);
+    else
+      hipLaunchKernelGGL((np_update_small<8192, 5, 3>), dim3(1), dim3(kNpSmallThreads), NpMid::kLds, stream,
+                         pool, count, num_nodes, static_cast<int>(pool_size), src, dst, static_cast<int>(n), seed,
+                         call, status);
     return check_launch("np_update_small");
   }
   uint8_t* ws = static_cast<uint8_t*>(workspace);
