@@ -194,6 +194,10 @@ constexpr int64_t kPackMinQueries = 8192;
 // output bytes of one query below which its waves are not split further
 constexpr int64_t kSplitBytes = 8192;
 
+// waves of a launch up to which a small launch's queries are split further (half
+// the device's wave slots: 600 queries ran faster at 4 waves each than at 8)
+constexpr int64_t kSplitMaxWaves = 4096;
+
 // row chunks each lane loads before storing them (large-row copy)
 constexpr int kCopyDepth = 4;
 
@@ -1104,8 +1108,8 @@ int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args
   P.off_pe = P.off_pt + round16(P.m * K * 8);
   P.off_tab = P.off_pe + round16(P.m * K * 8);
   P.wave_bytes = P.off_tab + round16(P.m * 24);
-  // split: with one query per wave and fewer queries than wave slots, up to 8
-  // waves share each query's outputs; and up to 8 while each wave's share of a
+  // split: with one query per wave, up to 8 waves share each query's outputs while
+  // the launch stays within kSplitMaxWaves waves; and up to 8 while each wave's share of a
   // query's output bytes stays at least kSplitBytes, so a grid of long copies
   // (large rows, large K) ends with a shorter tail of lone waves.  A workgroup
   // holds at most kMaxWaves waves (the kernel's launch bound): its query slots
@@ -1113,7 +1117,7 @@ int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args
   const int qwant = mode != TGX_PLAN_TILES ? a->group : 1;
   int split = 1;
   if (P.m == 1) {
-    while (split < 8 && a->num_queries * (split * 2) <= kPackMinQueries && qwant * split * 2 <= kMaxWaves)
+    while (split < 8 && a->num_queries * (split * 2) <= kSplitMaxWaves && qwant * split * 2 <= kMaxWaves)
       split *= 2;
     const int64_t qbytes = static_cast<int64_t>(K) * (P.row_bytes + 4 * a->d_t + 13);
     while (split < 8 && qbytes / (split * 2) >= kSplitBytes && qwant * split * 2 <= kMaxWaves)
