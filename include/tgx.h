@@ -134,9 +134,8 @@ typedef struct tgx_recent_args {
   int32_t k;               /* neighbours per query, 1..TGX_MAX_K */
   /* work plan, by plan_mode:
    *   TGX_PLAN_TILES (plan NULL): consecutive queries; `group` queries per
-   *     workgroup (a hint: a workgroup holds at most 8 wavefronts, so the launch
-   *     may give fewer queries to a workgroup when a query is shared by several
-   *     wavefronts); num_groups is ignored;
+   *     workgroup (a hint: when a small launch shares each query among several
+   *     wavefronts, a query takes a workgroup of its own); num_groups is ignored;
    *   TGX_PLAN_EVENTS (plan NULL): event-major groups computed from the query
    *     groups: group g = event g holds, for each query group in order,
    *     its times_per queries of event g (the reference grouping [src, dst,

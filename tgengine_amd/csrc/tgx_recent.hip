@@ -1125,9 +1125,11 @@ int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args
   }
   const int lg_split = split == 1 ? 0 : split == 2 ? 1 : split == 4 ? 2 : 3;  // split is 1, 2, 4 or 8
   P.split = mode == TGX_PLAN_TILES ? split : lg_split;
-  // tiles: `group` query slots per workgroup, fewer when split waves fill it
+  // tiles: `group` query slots per workgroup; a query split over several waves
+  // takes a workgroup of its own (so a small launch spreads over more CUs: C1's
+  // 600 queries, 4 waves each, ran 0.5 us faster in 600 workgroups than in 300)
   int qslots = a->group;
-  if (mode == TGX_PLAN_TILES && qslots * split > kMaxWaves) qslots = kMaxWaves / split;
+  if (mode == TGX_PLAN_TILES && split > 1) qslots = 1;
   const int waves = qslots * split;
   if (waves < 1 || waves > kMaxWaves)
     return fail(TGX_ERR_LIMIT, "tgx_recent: %d wavefronts per workgroup outside [1, %d]", waves, kMaxWaves);

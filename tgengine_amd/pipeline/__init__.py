@@ -54,7 +54,9 @@ class DataPipeline:
     """``time_encoder``: optional module with a ``linear`` Linear(1, d_t) whose
     weight/bias replace the fixed cosine frequencies (read in place at every
     launch, so updates to them apply).  ``queries_per_workgroup``: queries one
-    workgroup gathers when no co-occurrence pair has to share a workgroup."""
+    workgroup gathers when no co-occurrence pair has to share a workgroup and no
+    query is shared by several wavefronts (a small launch gives each such query
+    a workgroup of its own)."""
 
     def __init__(self, spec: GatherSpec, graph: TemporalGraph, time_encoder=None,
                  queries_per_workgroup: int = 4):
