@@ -184,6 +184,49 @@ def _build(seed, N, B, d, K, with_pre, with_ring, bf16=False, eids=False, n_pre=
     return rng, g, csr, ring, t
 
 
+@pytest.mark.parametrize("K", [20, 64])
+def test_csr_window_search_sizes(K):
+    """recent() on a frozen CSR whose windows hold 1, 64, 65, 4,097 and about 5,000
+    entries (a 64-ary search of one to three rounds, probes clamped to the window's
+    last entry), with tied times, queried before the window, at exact entry times
+    around the 64-boundaries, between entries and after the window: ids, times,
+    rows and masks bit for bit against the oracle."""
+    rng = np.random.default_rng(K)
+    N, d = 8, 4
+    sizes = {0: 5003, 1: 65, 2: 64, 3: 4097, 4: 1}
+    src = np.concatenate([np.full(c, u) for u, c in sizes.items()])
+    rng.shuffle(src)
+    E = len(src)
+    dst = rng.integers(5, N, E)  # destinations outside the measured nodes 0..4
+    time = np.cumsum(rng.integers(0, 3, E).astype(np.float64)) + 100.0  # steps of 0: tied times
+    feat = rng.standard_normal((E, d)).astype(np.float32)
+    g = TemporalGraph(N, edge_feat_dim=d, device="cuda", buffer_size=8)
+    events = []
+    for lo in range(0, E, 2048):
+        hi = min(E, lo + 2048)
+        g.advance(cu(src[lo:hi]), cu(dst[lo:hi]), cu(time[lo:hi]), cu(feat[lo:hi]))
+        events.append((src[lo:hi], dst[lo:hi], time[lo:hi], feat[lo:hi], lo))
+    g.freeze_csr()
+    csr = O.csr_freeze(N, d, events)
+    nodes, qts = [], []
+    for u in sizes:
+        ts = np.sort(time[src == u])
+        picks = [ts[0] - 1.0, ts[-1] + 1.0, ts[-1], ts[0]]
+        for i in (1, 62, 63, 64, 65, 127, 128, 4095, 4096, len(ts) // 2, len(ts) - 2):
+            if 0 <= i < len(ts):
+                picks += [ts[i], ts[i] + 0.5]
+        nodes += [u] * len(picks)
+        qts += picks
+    nodes = np.array(nodes, np.int64)
+    qts = np.array(qts, np.float64)
+    r = g.recent(cu(nodes), cu(qts), K)
+    o = O.recent(nodes, qts, K, csr, None, d)
+    assert np.array_equal(r.mask.cpu().numpy(), o.mask)
+    assert np.array_equal(r.neighbor_ids.cpu().numpy(), o.ids)
+    assert np.array_equal(r.timestamps.cpu().numpy().view(np.int64), o.times.view(np.int64))
+    assert np.array_equal(r.edge_feats.cpu().numpy(), o.feats)
+
+
 def _feats_np(t):
     if t.dtype == torch.bfloat16:
         return t.view(torch.int16).cpu().numpy().view(np.uint16)
