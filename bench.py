@@ -115,13 +115,16 @@ def cpu_model() -> str:
 
 def cpu_baseline(cfg, g, pipe, first, seconds, torch, log, last):
     """Time the torch-CPU restatement of the reference path on batches first.. of the
-    stream, starting from the GPU ring state; its outputs must equal the GPU's.
+    stream, starting from the GPU ring state; its outputs must equal the GPU's on
+    every batch (ids, timestamps, masks, rows, encodings), and the oracle's
+    (oracle/spec.py) on the first batch.
 
     Two legs: the job's CPU share (OMP_NUM_THREADS where set, else the CPUs in
     this process's affinity mask; torch threads set to that count) for
     ``seconds``, then one thread for a third of that on the following batches.
     os.cpu_count() is reported beside it: on a shared GPU box it counts the whole
     host, not the CPUs this job was given."""
+    from oracle import spec
     from oracle.refpath_torch import RefPathCPU
     from tgengine_amd.synthetic import gen_batch, to_raw
     cpu = RefPathCPU(cfg.num_nodes, cfg.feat_dim, cfg.buffer_size)
@@ -136,6 +139,30 @@ def cpu_baseline(cfg, g, pipe, first, seconds, torch, log, last):
     share = min(int(omp), affinity) if omp.isdigit() and int(omp) > 0 else affinity
     prev_threads = torch.get_num_threads()
     state = {"i": first}
+    want = {}
+
+    def oracle_check(i, bt, src, dst, neg, tt):
+        """The oracle's gather + encodings of batch i on the ring state the CPU
+        restatement starts from (queries [src, dst, neg row-major])."""
+        # views of the CPU ring (read only here; the restatement runs afterwards)
+        ring = spec.Ring(ids=cpu.ids.numpy(), times=cpu.times.numpy(), feats=cpu.feats.numpy(),
+                         wp=cpu.wp.numpy())
+        nodes = np.concatenate([bt["src"], bt["dst"], bt["neg"].reshape(-1)])
+        per = bt["neg"].shape[1] if bt["neg"].ndim > 1 else 1
+        qt = np.concatenate([bt["time"], bt["time"], np.repeat(bt["time"], per)])
+        o = spec.recent(nodes, qt, cfg.k, None, ring, cfg.feat_dim)
+        te = spec.time_encode_exact(spec.dt_dygformer(qt, o.times), spec.time_weights(100), o.mask)
+        want.update(o=o, te=te)
+
+    def oracle_compare(i, out):
+        o = want["o"]
+        same = (np.array_equal(out["ids"].numpy(), o.ids) and np.array_equal(out["mask"].numpy(), o.mask)
+                and np.array_equal(out["times"].numpy().view(np.int64), o.times.view(np.int64))
+                and np.array_equal(out["feats"].numpy(), o.feats))
+        err = float(np.abs(out["te"].double().numpy() - want["te"]).max()) if o.ids.size else 0.0
+        if not same or err > 1e-6:
+            raise RuntimeError(f"CPU baseline and oracle disagree at batch {i} (te error {err:.2e})")
+        log(f"cpu baseline: batch {i} equal to the oracle (te max error {err:.2e})")
 
     def leg(threads, budget):
         torch.set_num_threads(threads)
@@ -154,17 +181,23 @@ def cpu_baseline(cfg, g, pipe, first, seconds, torch, log, last):
             f32 = torch.from_numpy(bt["feat"])
             if cfg.feat_dtype == "bf16":
                 f32 = f32.view(torch.bfloat16).float()
+            if i == first:
+                oracle_check(i, bt, src, dst, neg, tt)
             t0 = time.perf_counter()
             out = cpu.prepare(src, dst, neg, tt, cfg.k, co=cfg.co_occurrence)
             cpu.advance(src, dst, tt, f32)
             spent += time.perf_counter() - t0
+            if i == first:
+                oracle_compare(i, out)
             # parity of the CPU restatement with the GPU on this full-size window
             groups = [pb.src_neighbors, pb.dst_neighbors, pb.neg_neighbors]
             gids = torch.cat([x.neighbor_ids.cpu() for x in groups])
+            gtimes = torch.cat([x.timestamps.cpu() for x in groups])
             gmask = torch.cat([x.mask.cpu() for x in groups])
             gfeat = torch.cat([x.edge_feats.float().cpu() for x in groups])
             gte = torch.cat([x.time_enc.cpu() for x in groups])
             if not (torch.equal(gids, out["ids"]) and torch.equal(gmask, out["mask"])
+                    and torch.equal(gtimes.view(torch.int64), out["times"].view(torch.int64))
                     and torch.equal(gfeat, out["feats"])):
                 raise RuntimeError(f"CPU baseline and GPU disagree at batch {i}")
             te_err = float((gte.double() - out["te"].double()).abs().max()) if gte.numel() else 0.0
@@ -183,7 +216,8 @@ def cpu_baseline(cfg, g, pipe, first, seconds, torch, log, last):
     return {"value": q_n / s_n, "unit": "prepared queries/s", "cores": share,
             "kind": "port",
             "sample": (f"{cfg.name} batches {b0}..{b0 + nb - 1} ({q_n} queries, prepare+advance) "
-                       f"from the GPU ring state after batch {b0 - 1}; outputs equal to the GPU's"),
+                       f"from the GPU ring state after batch {b0 - 1}; outputs equal to the GPU's "
+                       f"(ids, timestamps, masks, rows, encodings), and to the oracle's on batch {b0}"),
             "batches": nb, "threads": share, "os_cpu_count": os.cpu_count(),
             "affinity_cpus": affinity, "cpu_model": cpu_model(),
             "value_1thread": q_1 / s_1 if s_1 > 0 else None,
@@ -499,9 +533,14 @@ def main():
                         edge_feat=dev["feat"][s:e], neg=neg)
 
     raws = [raw(i) for i in range(total)]
+    # warm-up steps exactly as the timed ones: each step's outputs live until the
+    # next step's replace them, so the caching allocator holds both output blocks
+    # before timing starts
+    pb = None
     for i in range(W):
-        pipe.prepare(raws[i])
+        pb = pipe.prepare(raws[i])
         g.advance(raws[i].src, raws[i].dst, raws[i].time, raws[i].edge_feat)
+    del pb
     torch.cuda.synchronize()
     log(f"warm-up {W} batches done")
 
@@ -556,6 +595,12 @@ def main():
         if replayed != eager:
             raise RuntimeError(f"graph replay disagrees with eager launches: {replayed} vs {eager}")
         del graph
+        # the replays leave the ring where the timed region did: stream the window's
+        # batches through it (untimed), so what follows sees the whole stream
+        for i in range(W + K, total):
+            pipe.prepare(raws[i])
+            g.advance(raws[i].src, raws[i].dst, raws[i].time, raws[i].edge_feat)
+        torch.cuda.synchronize()
     n_launch = max(R, 1)
     st = g.status()
     if any(st.values()):
@@ -588,10 +633,16 @@ def main():
     if a.ceilings:
         ceilings = measure_ceilings(torch, device, int(sum(rbyts) / n_launch) if rbyts else 1 << 27, log)
 
+    # HBM traffic per launch from the byte counters of a profiling run over the
+    # same roofline window (profiles/<config>_recent_fused_pmc.json, one entry per
+    # window); null when no profile covers this window
     traffic = None
+    window = f"{W + K}..{total - 1}"
     pmc = ROOT / "profiles" / f"{cfg.name}_recent_fused_pmc.json"
     if pmc.exists():
-        traffic = json.loads(pmc.read_text()).get("traffic_bytes_per_launch")
+        entry = json.loads(pmc.read_text()).get("windows", {}).get(window)
+        if entry is not None:
+            traffic = entry.get("traffic_bytes_per_launch")
 
     cpu = None
     if not a.no_cpu and total < avail:
@@ -616,6 +667,7 @@ def main():
                            "bytes_per_launch": sum(rbyts) / n_launch},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
+                     "traffic_window": window if traffic is not None else None,
                      "kernel": "recent_fused",
                      "timing": f"HIP event pair around a graph replay of the {R} launches of "
                                f"batches {W + K}..{total - 1}"},

@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define TGX_ABI_VERSION 12
+#define TGX_ABI_VERSION 13
 
 /* status codes */
 #define TGX_OK 0
@@ -195,13 +195,16 @@ typedef struct tgx_recent_args {
   /* d_t > 0: upper bounds of max|te_w[i]| and max|te_b[i]| (0 without bias),
    * which let the cosine skip its large-argument reduction where no argument
    * can need it.  te_bound_w <= 0 (or NaN): unknown, every element takes the
-   * full-range reduction (same results, slower). */
+   * full-range reduction (same results, slower).  The bounds are trusted and
+   * not checked on the device: a bound below the true maximum gives WRONG
+   * encodings (errors far above 1e-6) wherever |fl32(dt * w) + b| reaches 2^29.
+   * Pass 0 unless the bound is known on the host. */
   float te_bound_w;
   float te_bound_b;
 } tgx_recent_args;
 
 #define TGX_MAX_SLOTS 64
-#define TGX_MAX_K 256
+#define TGX_MAX_K 512
 #define TGX_MAX_GROUP 8
 #define TGX_MAX_DT 512
 

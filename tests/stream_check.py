@@ -131,7 +131,7 @@ def run(cfg_name: str, n_batches: int, check: set, ring_check_every: int = 0,
         if ring_check_every and (i % ring_check_every == ring_check_every - 1 or i == n_batches - 1):
             compare_ring(g, ring, np.concatenate([bt["src"], bt["dst"]]), f"{cfg.name} ring after {i}")
     st = g.status()
-    if st["bad_event_nodes"] or st["key_collisions"] or st["bad_query_nodes"]:
+    if any(st.values()):
         raise Mismatch(f"{cfg.name}: device diagnostics {st}")
     tot["graph"] = g
     tot["ring"] = ring

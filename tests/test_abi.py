@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(L, n), n
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
-    assert L.tgx_abi_version() == _lib.TGX_ABI_VERSION == 12
+    assert L.tgx_abi_version() == _lib.TGX_ABI_VERSION == 13
     nm = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
                         text=True).stdout
     exported = set(re.findall(r"\bT (tgx_\w+)", nm))
@@ -172,10 +172,12 @@ def test_launch_shapes_stay_within_the_kernel_bounds():
     csr = _lib.TgxCsr(num_nodes=10, num_entries=5, feat_dim=4, feat_dtype=0, offsets=8, ids=8,
                       times=8, feats=8)
     ring = _lib.TgxRing(num_nodes=10, slots=32, feat_dim=4, feat_dtype=0, ids=8, times=8, feats=16)
+    ring64 = _lib.TgxRing(num_nodes=10, slots=64, feat_dim=4, feat_dtype=0, ids=8, times=8, feats=16)
     for Q in (1, 2, 3, 511, 512, 513, 1024, 2049, 4096, 4097, 8192, 8193, 20000):
-        for k in (1, 3, 20, 64, 256):
+        for k in (1, 3, 20, 64, 256, 300, 512):
             for group in (1, 2, 4, 8):
-                for store in ((None, ctypes.byref(csr)), (ctypes.byref(ring), None)):
+                for store in ((None, ctypes.byref(csr)), (ctypes.byref(ring), None),
+                              (ctypes.byref(ring64), ctypes.byref(csr))):
                     a = _lib.TgxRecentArgs(k=k, group=group, num_queries=Q, nodes=8, times=8,
                                            out_ids=8, out_times=8, out_mask=8, out_feats=16)
                     rc, sh = _shape(store[0], store[1], a)

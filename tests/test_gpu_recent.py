@@ -252,6 +252,88 @@ def test_recent_matches_oracle(with_pre, with_ring, K, B, bf16):
     assert np.array_equal(r.edge_ids.cpu().numpy(), o.eids)
 
 
+def _tied_graph(seed, N, B, d, n_pre, b_pre, n_ring, b_ring):
+    """A frozen CSR whose windows exceed 512 entries and a full ring, with times on an
+    integer grid so that entries tie: within a CSR window, within a ring and
+    between the two."""
+    rng = np.random.default_rng(seed)
+    g = TemporalGraph(N, edge_feat_dim=d, device="cuda", buffer_size=B)
+    events, eb, t = [], 0, 5000.0
+    def batch(b):
+        nonlocal t
+        src, dst = rng.integers(0, N, b), rng.integers(0, N, b)
+        time = t + np.sort(rng.integers(0, b // 4, b)).astype(np.float64)
+        t = float(time[-1])
+        return src, dst, time, rng.standard_normal((b, d)).astype(np.float32)
+    for _ in range(n_pre):
+        s_, d_, tm, f = batch(b_pre)
+        g.advance(cu(s_), cu(d_), cu(tm), cu(f))
+        events.append((s_, d_, tm, f, eb))
+        eb += b_pre
+    g.freeze_csr()
+    csr = O.csr_freeze(N, d, events, np.float32)
+    ring = O.Ring.empty(N, B, d, np.float32)
+    t -= b_ring // 2  # the ring's first batch starts before the CSR's last entries
+    for _ in range(n_ring):
+        s_, d_, tm, f = batch(b_ring)
+        g.advance(cu(s_), cu(d_), cu(tm), cu(f))
+        O.ring_advance(ring, s_, d_, tm, f, eid_base=eb)
+        eb += b_ring
+    return rng, g, csr, ring, t
+
+
+# K up to 512 (LastFM's pipeline shape: K=512, 2-d fp32 rows): CSR windows longer
+# than K, a ring of 64 slots, ties inside and across them, queries before, inside
+# and after the windows; every output against the oracle
+@pytest.mark.parametrize("K,with_ring", [(512, True), (512, False), (300, True)])
+def test_recent_large_k_matches_oracle(K, with_ring):
+    rng, g, csr, ring, tmax = _tied_graph(51, 6, 64, 2, 5, 600, 3 if with_ring else 0, 200)
+    Q = 300
+    nodes = rng.integers(-1, 6, Q)
+    qt = np.floor(rng.uniform(5000.0, tmax + 5.0, Q))  # on the grid: ties with entries
+    r = g.recent(cu(nodes), cu(qt), K)
+    o = O.recent(nodes, qt, K, csr, ring if with_ring else None, 2)
+    assert int(o.mask.sum(1).max()) == K  # some windows are truncated to K
+    assert np.array_equal(r.neighbor_ids.cpu().numpy(), o.ids)
+    assert np.array_equal(r.timestamps.cpu().numpy().view(np.int64), o.times.view(np.int64))
+    assert np.array_equal(r.mask.cpu().numpy(), o.mask)
+    assert np.array_equal(r.edge_feats.cpu().numpy(), o.feats)
+
+
+@pytest.mark.parametrize("mode", ["freq", "dygformer"])
+def test_prepare_k512_lastfm_shape(mode):
+    """DataPipeline.prepare at K=512 on the CSR + ring, with time encodings and
+    co-occurrence (ii) / (iii)."""
+    rng, g, csr, ring, tmax = _tied_graph(52, 8, 64, 2, 6, 500, 3, 200)
+    K, b = 512, 40
+    spec = GatherSpec(neighbors=NeighborSpec(k=K), time_encoding=100, co_occurrence=True,
+                      co_occurrence_mode=mode)
+    pipe = DataPipeline(spec, g)
+    src, dst, neg = rng.integers(0, 8, b), rng.integers(0, 8, b), rng.integers(0, 8, b)
+    t = tmax + np.floor(rng.uniform(0.0, 3.0, b))
+    pb = pipe.prepare(RawBatch(src=cu(src), dst=cu(dst), time=cu(t), neg=cu(neg)))
+    nodes = np.concatenate([src, dst, neg])
+    qt = np.concatenate([t, t, t])
+    o = O.recent(nodes, qt, K, csr, ring, 2)
+    groups = [pb.src_neighbors, pb.dst_neighbors, pb.neg_neighbors]
+    assert np.array_equal(torch.cat([x.neighbor_ids for x in groups]).cpu().numpy(), o.ids)
+    assert np.array_equal(torch.cat([x.timestamps for x in groups]).cpu().numpy().view(np.int64),
+                          o.times.view(np.int64))
+    assert np.array_equal(torch.cat([x.mask for x in groups]).cpu().numpy(), o.mask)
+    assert np.array_equal(torch.cat([x.edge_feats for x in groups]).cpu().numpy(), o.feats)
+    te = torch.cat([x.time_enc for x in groups]).cpu().numpy()
+    exp = O.time_encode_exact(O.dt_dygformer(qt, o.times), O.time_weights(100), o.mask)
+    assert np.max(np.abs(te - exp)) <= TE_ATOL
+    a, c = o.ids[:b], o.ids[b:2 * b]
+    if mode == "freq":
+        ea, ec = O.co_occurrence_freq(a, c)
+    else:
+        ea, ec = O.co_dygformer(np.concatenate([src[:, None], a], 1), np.concatenate([dst[:, None], c], 1))
+    ga, gc = pb.co_occurrence_freq
+    assert np.array_equal(ga.cpu().numpy(), ea) and np.array_equal(gc.cpu().numpy(), ec)
+    assert np.array_equal(pb.co_occurrence.cpu().numpy(), O.co_pair_count(a, o.mask[:b], c, o.mask[b:2 * b]))
+
+
 def test_recent_bad_query_nodes_are_padding_and_flagged():
     rng, g, csr, ring, tmax = _build(12, 20, 4, 3, 4, True, True)
     r = g.recent(cu([0, 25, 3]), cu([tmax + 1] * 3, torch.float64), 4)
@@ -395,6 +477,49 @@ def test_co_occurrence_modes(mode, k, n_neg):
     assert np.array_equal(ga.cpu().numpy(), ea) and np.array_equal(gc.cpu().numpy(), ec)
     pair = O.co_pair_count(a, pb.src_neighbors.mask.cpu().numpy(), c, pb.dst_neighbors.mask.cpu().numpy())
     assert np.array_equal(pb.co_occurrence.cpu().numpy(), pair)
+
+
+# more queries per event than a workgroup takes (TGX_MAX_GROUP = 8): the (src, dst)
+# pair shares the event's workgroup and the negatives are tiled after them, for
+# launches below and above 4,096 queries; prepare(), launch() and the 2-hop prepare
+@pytest.mark.parametrize("n_neg,b,neg_src", [(7, 1000, False), (10, 300, False), (10, 1000, True),
+                                             (6, 700, True)])
+def test_co_occurrence_with_many_negatives(n_neg, b, neg_src):
+    rng, g, csr, ring, tmax = _build(31, 40, 16, 4, 12, True, True, b=80)
+    k = 12
+    spec = GatherSpec(neighbors=NeighborSpec(k=k), co_occurrence=True, time_encoding=8)
+    pipe = DataPipeline(spec, g)
+    src = rng.integers(0, 40, b)
+    dst = np.where(rng.random(b) < 0.2, src, rng.integers(0, 40, b))
+    neg = rng.integers(0, 40, (b, n_neg))
+    ns = rng.integers(0, 40, b) if neg_src else None
+    t = tmax + rng.uniform(0.0, 5.0, b)
+    rb = RawBatch(src=cu(src), dst=cu(dst), time=cu(t), neg=cu(neg),
+                  neg_src=cu(ns) if neg_src else None)
+    nodes = np.concatenate([src, dst, neg.reshape(-1)] + ([ns] if neg_src else []))
+    qt = np.concatenate([t, t, np.repeat(t, n_neg)] + ([t] if neg_src else []))
+    o = O.recent(nodes, qt, k, csr, ring, 4)
+    a, c = o.ids[:b], o.ids[b:2 * b]
+    ea, ec = O.co_occurrence_freq(a, c)
+    pair = O.co_pair_count(a, o.mask[:b], c, o.mask[b:2 * b])
+    pb = pipe.prepare(rb)
+    groups = [pb.src_neighbors, pb.dst_neighbors, pb.neg_neighbors] + ([pb.neg_src_neighbors] if neg_src else [])
+    assert np.array_equal(torch.cat([x.neighbor_ids for x in groups]).cpu().numpy(), o.ids)
+    assert np.array_equal(torch.cat([x.mask for x in groups]).cpu().numpy(), o.mask)
+    te = torch.cat([x.time_enc for x in groups]).cpu().numpy()
+    assert np.max(np.abs(te - O.time_encode_exact(O.dt_dygformer(qt, o.times), O.time_weights(8), o.mask))) <= TE_ATOL
+    ga, gc = pb.co_occurrence_freq
+    assert np.array_equal(ga.cpu().numpy(), ea) and np.array_equal(gc.cpu().numpy(), ec)
+    assert np.array_equal(pb.co_occurrence.cpu().numpy(), pair)
+    # the raw launch of prepare() and the 2-hop prepare take the same layout
+    out = pipe.launch(rb)
+    assert np.array_equal(torch.cat(out["ids"]).cpu().numpy(), o.ids)
+    assert np.array_equal(out["co_a"].cpu().numpy(), ea) and np.array_equal(out["co_c"].cpu().numpy(), ec)
+    spec2 = GatherSpec(neighbors=NeighborSpec(k=k, k2=3), co_occurrence=True)
+    pb2 = DataPipeline(spec2, g).prepare(rb)
+    ga2, gc2 = pb2.co_occurrence_freq
+    assert np.array_equal(ga2.cpu().numpy(), ea) and np.array_equal(gc2.cpu().numpy(), ec)
+    assert np.array_equal(pb2.co_occurrence.cpu().numpy(), pair)
 
 
 def test_standalone_co_occurrence_rows():

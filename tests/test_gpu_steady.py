@@ -79,4 +79,4 @@ def test_steady_state_window(name, T, K):
         nodes, _ = S.queries_of(bt)
         _ring_equal(g, ring, f"{name} ring after {i}", full, extra_rows=nodes)
     st = g.status()
-    assert not (st["bad_event_nodes"] or st["key_collisions"] or st["bad_query_nodes"]), st
+    assert not any(st.values()), st

@@ -21,6 +21,7 @@ LIB = OUT_DIR / "libtgx.so"
 SOURCES = ["tgx_common.hip", "tgx_ring.hip", "tgx_recent.hip", "tgx_csr.hip", "tgx_negpool.hip"]
 
 ARCH = "gfx950"
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17",
     # no packed-FP32 instructions anywhere in the device code
@@ -50,8 +51,10 @@ def build_host(verbose: bool = False) -> Path:
     cmd = ["g++", "-O2", "-shared", "-fPIC", "-std=c++17", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
            "-DTORCH_EXTENSION_NAME=_tgx_host", "-DTORCH_API_INCLUDE_EXTENSION_H",
            *[f"-I{p}" for p in ce.include_paths()], f"-I{sysconfig.get_paths()['include']}",
+           # torch's HIP stream API (the caller's current stream); host code only
+           "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include",
            f"-I{INCLUDE}", str(CSRC / "tgx_host.cpp"), "-o", str(tmp),
-           *[f"-L{p}" for p in ce.library_paths()], "-lc10", "-ltorch", "-ltorch_cpu",
+           *[f"-L{p}" for p in ce.library_paths()], "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu",
            "-ltorch_python", f"-L{OUT_DIR}", "-ltgx", "-Wl,-rpath,$ORIGIN/_lib"]
     if verbose:
         print(" ".join(cmd), flush=True)

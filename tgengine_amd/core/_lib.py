@@ -24,13 +24,13 @@ TGX_CO_DYGFORMER = 2
 TGX_PLAN_TILES = 0
 TGX_PLAN_EVENTS = 1
 TGX_PLAN_LIST = 2
-TGX_ABI_VERSION = 12
+TGX_ABI_VERSION = 13
 TGX_STATUS_WORDS = 8
 TGX_ST_BAD_EVENT_NODE = 0
 TGX_ST_KEY_COLLISION = 1
 TGX_ST_BAD_QUERY_NODE = 2
 TGX_MAX_SLOTS = 64
-TGX_MAX_K = 256
+TGX_MAX_K = 512
 TGX_MAX_GROUP = 8
 TGX_MAX_DT = 512
 

@@ -52,27 +52,13 @@ class Snapshot:
     overflow_eids: Optional[Tensor] = None
 
 
-class _Plan:
-    """A ring update planned ahead of its advance() (plan_append, or the plan
-    fused into a gather launch): the batch's tensors, their version counters
-    at planning time and the raw handle of the stream the plan was enqueued on."""
+class _PlanView:
+    """Read-only view of the pending ring plan (its stream), for diagnostics."""
 
-    __slots__ = ("src", "dst", "time", "versions", "stream")
+    __slots__ = ("stream",)
 
-    def __init__(self, src: Tensor, dst: Tensor, time: Tensor, stream: int):
-        self.src, self.dst, self.time = src, dst, time
-        self.versions = (src._version, dst._version, time._version)
+    def __init__(self, stream: int):
         self.stream = stream
-
-    def matches(self, src: Tensor, dst: Tensor, time: Tensor) -> bool:
-        """The same tensors (or views of the same storage, shape, strides and
-        dtype), unmodified since the plan (version counters unchanged)."""
-        if not (src is self.src and dst is self.dst and time is self.time):
-            for a, p in ((src, self.src), (dst, self.dst), (time, self.time)):
-                if (a.data_ptr() != p.data_ptr() or a.shape != p.shape or a.dtype != p.dtype
-                        or a.stride() != p.stride()):
-                    return False
-        return (src._version, dst._version, time._version) == self.versions
 
 
 try:
@@ -162,9 +148,10 @@ class TemporalGraph:
 
         self._status = torch.zeros(_lib.TGX_STATUS_WORDS, dtype=torch.int32, device=self.device)
         self._ws: Optional[Tensor] = None
-        # a ring update planned ahead of its advance() (see plan_append)
-        self._plan: Optional[_Plan] = None
-        self._plan_ws: Optional[Tensor] = None
+        # the ring update planned ahead of its advance() (see plan_append): the
+        # extension's PlanSlot of the current ring, with the plan workspace; the
+        # lock serialises the multi-step paths (discard, re-plan) between threads
+        self._slot = None
         self._plan_lock = threading.Lock()
         self._ring_struct: Optional[_lib.TgxRing] = None
         self._csr_struct: Optional[_lib.TgxCsr] = None
@@ -192,6 +179,8 @@ class TemporalGraph:
         nscr = int(_lib.lib().tgx_ring_scratch_size(N)) // 4
         self._ov_scratch = torch.zeros(nscr, dtype=torch.int32, device=dev)
         self._ring_struct = None
+        self._slot = _host().PlanSlot(ctypes.addressof(self._ring()), self._status, self.edge_feat_dim,
+                                      self.feat_dtype)
         self._gen += 1
 
     def _ring(self) -> Optional[_lib.TgxRing]:
@@ -259,8 +248,21 @@ class TemporalGraph:
                 and all(t.device == self.device and t.is_contiguous() for t in (src, dst, time)))
 
     def _plan_workspace(self, b: int) -> Tensor:
-        self._plan_ws = self._grown(self._plan_ws, _ws_size(b))
-        return self._plan_ws
+        slot = self._slot
+        ws = slot.workspace()
+        need = _ws_size(b)
+        if ws is None or ws.numel() < need:
+            ws = self._grown(ws, need)
+            slot.set_workspace(ws)
+        return ws
+
+    @property
+    def _plan(self) -> Optional[_PlanView]:
+        """The pending ring plan's stream, or None when no plan is pending."""
+        slot = self._slot
+        if slot is None or not slot.pending():
+            return None
+        return _PlanView(slot.stream())
 
     def _order_after(self, stream: int) -> int:
         """Raw handle of the current stream, made to wait for ``stream`` first when
@@ -285,52 +287,63 @@ class TemporalGraph:
         if not self._plannable(src, dst, time):
             return False
         with self._plan_lock:
-            if self._plan is not None:  # an earlier plan nobody advanced: drop it first
-                self._discard_plan()
+            self._discard_plan()  # an earlier plan nobody advanced
             stream = _stream_handle(self.device)
             ws = self._plan_workspace(int(src.shape[0]))
             _host().ring_plan(ctypes.addressof(self._ring()), src, dst, time, ws, stream)
-            self._plan = _Plan(src, dst, time, stream)
+            self._slot.record(src, dst, time, stream)
         return True
 
     def _adopt_plan(self, stream) -> None:
         """The caller has ordered ``stream`` (a torch stream) after the pending
         plan's stream: a commit or discard on ``stream`` needs no further wait."""
-        with self._plan_lock:
-            if self._plan is not None:
-                self._plan.stream = stream.cuda_stream
+        if self._slot is not None:
+            self._slot.set_stream(stream.cuda_stream)
 
     def _discard_plan(self) -> None:
-        """Discard the pending plan on the current stream (ordered after the plan)."""
-        plan, self._plan = self._plan, None
-        stream = self._order_after(plan.stream)
-        _host().ring_discard(ctypes.addressof(self._ring()), plan.src, plan.dst, self._plan_ws, stream)
+        """Discard the pending plan, if any, on the current stream (ordered after
+        the plan's stream)."""
+        plan = self._slot.take() if self._slot is not None else None
+        if plan is None:
+            return
+        src, dst, _, pstream = plan
+        stream = self._order_after(pstream)
+        _host().ring_discard(ctypes.addressof(self._ring()), src, dst, self._slot.workspace(), stream)
 
     def _drop_plan(self) -> None:
         """Discard a pending plan (before the ring or its scratch is replaced)."""
         with self._plan_lock:
-            if self._plan is not None:
-                self._discard_plan()
+            self._discard_plan()
 
     def advance(self, src: Tensor, dst: Tensor, time: Tensor,
                 edge_feat: Optional[Tensor] = None) -> None:
         """Append a batch of undirected events (reference temporal_graph.py:104-131)."""
+        slot = self._slot
+        if slot is not None:
+            # the planned batch, on the plan's stream, with a ready feature block:
+            # one call commits it
+            n = slot.commit(src, dst, time, edge_feat, self._num_edges)
+            if n:
+                self._num_edges += n
+                return
         b = int(src.shape[0])
         if dst.shape[0] != b or time.shape[0] != b:
             raise ValueError("src, dst and time must have the same length")
-        if self._plan is not None:
+        if slot is not None and slot.pending():
             with self._plan_lock:
-                plan = self._plan
-                if plan is not None and self._frozen and plan.matches(src, dst, time):
-                    self._plan = None
-                    feat = self._feat_in(edge_feat, b)
-                    stream = self._order_after(plan.stream)
+                if slot.matches(src, dst, time):
+                    try:
+                        feat = self._feat_in(edge_feat, b)
+                    except Exception:
+                        self._discard_plan()
+                        raise
+                    _, _, _, pstream = slot.take()
+                    stream = self._order_after(pstream)
                     _host().ring_commit(ctypes.addressof(self._ring()), src, dst, time, feat,
-                                        self._num_edges, self._plan_ws, self._status, stream)
+                                        self._num_edges, slot.workspace(), self._status, stream)
                     self._num_edges += b
                     return
-                if plan is not None:
-                    self._discard_plan()
+                self._discard_plan()
         if not self._frozen:
             # the values at call time, as device copies (the reference copies them
             # into host lists, temporal_graph.py:110-122)
@@ -480,14 +493,13 @@ class TemporalGraph:
         # the extension plans the batch when its tensors allow it (int64 / float64
         # contiguous 1-D device tensors of one non-zero length)
         with self._plan_lock:
-            if self._plan is not None:  # an earlier plan nobody advanced: drop it first
-                self._discard_plan()
+            self._discard_plan()  # an earlier plan nobody advanced
             ws = self._plan_workspace(int(append[0].shape[0]))
             res = self._launch_recent(ring, csr, groups, k, plan, plan_mode, group, num_groups,
                                       ev_groups, d_t, te, dt_mode, co_mode, want_eids, ev0,
                                       ev1, append, ws, stream)
             if res[0]:
-                self._plan = _Plan(append[0], append[1], append[2], stream)
+                self._slot.record(append[0], append[1], append[2], stream)
         return res
 
     def _launch_recent(self, ring, csr, groups, k, plan, plan_mode, group, num_groups, ev_groups,
@@ -515,20 +527,19 @@ class TemporalGraph:
     def _prepare(self, prep, src: Tensor, dst: Tensor, time: Tensor, neg: Optional[Tensor],
                  neg_src: Optional[Tensor], plan_updates: bool) -> tuple:
         """One DataPipeline 1-hop launch through its configured extension context
-        ``prep``: (planned, tensors).  With ``plan_updates`` and a ring, the launch
-        also plans the ring update of this batch for the advance() that follows."""
+        ``prep``: its tensors.  With ``plan_updates`` and a ring, the launch also
+        plans the ring update of this batch for the advance() that follows."""
         if not self._frozen:
             self.freeze_csr()
-        stream = _stream_handle(self.device)
-        if not plan_updates or self._ov_ids is None:
-            return prep.run(src, dst, time, neg, neg_src, stream, None)
-        with self._plan_lock:
-            if self._plan is not None:  # an earlier plan nobody advanced: drop it first
+        res = prep.run(src, dst, time, neg, neg_src, plan_updates)
+        if res is None:
+            # an earlier plan pending on another stream, or a workspace too small:
+            # settle the plan state, then launch
+            with self._plan_lock:
                 self._discard_plan()
-            ws = self._plan_workspace(int(src.shape[0]))
-            res = prep.run(src, dst, time, neg, neg_src, stream, ws)
-            if res[0]:
-                self._plan = _Plan(src, dst, time, stream)
+                if self._plannable(src, dst, time):
+                    self._plan_workspace(int(src.shape[0]))
+                res = prep.run(src, dst, time, neg, neg_src, plan_updates)
         return res
 
     def _structs(self) -> tuple:
@@ -585,6 +596,7 @@ class TemporalGraph:
         self._ov_ids = self._ov_times = self._ov_feats = self._ov_write_pos = self._ov_eids = None
         self._ov_scratch = None
         self._ring_struct = None
+        self._slot = None
         self._csr_struct = None
         self._gen += 1
         self._num_edges = 0

@@ -13,7 +13,12 @@
 // tensors, not autograd views of each other.  Keeping one tensor alive keeps
 // its whole block alive, so a caller that keeps only masks or ids does not pin
 // the feature rows and encodings.
+//
+// The per-batch calls of the streaming loop (Prepare.run, PlanSlot.commit) read
+// the caller's current HIP stream themselves and hand their tensors straight to
+// Python, so one step costs two calls into this module.
 #include <torch/extension.h>
+#include <c10/hip/HIPStream.h>
 
 #include <stdexcept>
 #include <string>
@@ -28,11 +33,21 @@ namespace {
 // Event-major launches (co-occurrence) of at most this many queries group only the
 // (src, dst) pair of each event and tile the other query groups after them, so that
 // more wavefronts share each query (a workgroup holds at most 8 wavefronts: query
-// slots x split); larger launches keep every query of an event in its group
+// slots x split); larger launches keep every query of an event in its group unless
+// an event holds more queries than a workgroup takes (TGX_MAX_GROUP, or the
+// waves whose LDS fits the CU at this k), when they too group only the pair
 constexpr int64_t kPairTailMaxQueries = 4096;
 
-// event_query_groups of an event-major launch over ng query groups and Q queries
-int pair_tail_groups(size_t ng, int64_t Q) { return ng > 2 && Q <= kPairTailMaxQueries ? 2 : 0; }
+// an upper bound of one wave's LDS in tgx_recent at k neighbours (k CSR
+// candidates and up to 64 ring slots, k ranked positions) plus the encoder weights
+int64_t group_lds_bound(int64_t G, int64_t k) { return G * ((k + 64) * 16 + k * 28 + 64) + 4096; }
+
+// event_query_groups of an event-major launch over ng query groups, Q queries,
+// G queries per event and k neighbours
+int pair_tail_groups(size_t ng, int64_t Q, int64_t G, int64_t k) {
+  const bool big = G > TGX_MAX_GROUP || group_lds_bound(G, k) > 160 * 1024;
+  return ng > 2 && (Q <= kPairTailMaxQueries || big) ? 2 : 0;
+}
 
 void check(int rc, const char* what) {
   if (rc != TGX_OK) throw std::runtime_error(std::string(what) + " failed: " + tgx_last_error());
@@ -57,6 +72,23 @@ at::Tensor typed_block(const at::Tensor& base, const caffe2::TypeMeta dt, int64_
 }
 
 int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
+
+// the caller's current stream on device `index`, as tgx takes it
+void* current_stream(c10::DeviceIndex index) {
+  return static_cast<void*>(c10::hip::getCurrentHIPStream(index).stream());
+}
+
+// identity of a tensor for the plan check: the same tensor, or a view of the
+// same memory with the same shape, strides and dtype
+bool same_tensor(const at::Tensor& a, const at::Tensor& b) {
+  if (a.unsafeGetTensorImpl() == b.unsafeGetTensorImpl()) return true;
+  return a.data_ptr() == b.data_ptr() && a.sizes() == b.sizes() && a.strides() == b.strides() &&
+         a.scalar_type() == b.scalar_type();
+}
+
+uint32_t version_of(const at::Tensor& t) {
+  return t.unsafeGetTensorImpl()->version_counter().current_version();
+}
 
 // Byte layout of the outputs of one tgx_recent launch over Q queries: the bulk
 // block (feature rows, encodings) and the small block (times, edge ids, ids,
@@ -163,6 +195,110 @@ struct Out {
   }
 };
 
+// the tensors as one Python tuple
+py::tuple as_tuple(std::vector<at::Tensor>& v) {
+  py::tuple t(v.size());
+  for (size_t i = 0; i < v.size(); ++i)
+    t[i] = py::reinterpret_steal<py::object>(THPVariable_Wrap(std::move(v[i])));
+  return t;
+}
+
+// The ring update planned ahead of its advance() (TemporalGraph.plan_append, or
+// the plan run by a gather launch): the batch's src/dst/time tensors, their
+// version counters when planned, and the stream the plan was enqueued on.  One
+// per ring; it also holds the plan workspace (grown by the Python layer).  Every
+// method runs under the GIL, so each is atomic for Python threads.
+class PlanSlot {
+ public:
+  PlanSlot(int64_t ring_addr, const at::Tensor& status, int64_t feat_dim, at::ScalarType feat_dtype)
+      : ring_(ring_addr), status_(status), feat_dim_(feat_dim), feat_dtype_(feat_dtype),
+        dev_(status.device()) {}
+
+  void set_workspace(const at::Tensor& ws) { ws_ = ws; }
+  c10::optional<at::Tensor> workspace() const {
+    return ws_.defined() ? c10::optional<at::Tensor>(ws_) : c10::nullopt;
+  }
+  bool pending() const { return has_; }
+  int64_t stream() const { return has_ ? stream_ : 0; }
+  void set_stream(int64_t stream) {
+    if (has_) stream_ = stream;
+  }
+  void record(const at::Tensor& s, const at::Tensor& d, const at::Tensor& t, int64_t stream) {
+    src_ = s;
+    dst_ = d;
+    time_ = t;
+    ver_[0] = version_of(s);
+    ver_[1] = version_of(d);
+    ver_[2] = version_of(t);
+    stream_ = stream;
+    has_ = true;
+  }
+  bool matches(const at::Tensor& s, const at::Tensor& d, const at::Tensor& t) const {
+    return has_ && same_tensor(s, src_) && same_tensor(d, dst_) && same_tensor(t, time_) &&
+           version_of(s) == ver_[0] && version_of(d) == ver_[1] && version_of(t) == ver_[2];
+  }
+  // (src, dst, time, stream) of the pending plan, which is no longer pending; None
+  py::object take() {
+    if (!has_) return py::none();
+    has_ = false;
+    py::tuple r = py::make_tuple(src_, dst_, time_, stream_);
+    src_ = dst_ = time_ = at::Tensor();
+    return r;
+  }
+  // advance() of the planned batch: commits it when src/dst/time are the planned
+  // tensors, feat is None or a contiguous (b, feat_dim) tensor of the ring's dtype
+  // on its device, and the current stream is the plan's.  Returns b, or 0 when it
+  // did nothing (the caller then takes the general path).
+  int64_t commit(const at::Tensor& s, const at::Tensor& d, const at::Tensor& t,
+                 const c10::optional<at::Tensor>& feat, int64_t eid_base) {
+    if (!matches(s, d, t)) return 0;
+    const int64_t b = s.numel();
+    const void* fp = nullptr;
+    if (feat.has_value()) {
+      const at::Tensor& f = *feat;
+      if (f.dim() != 2 || f.size(0) != b || f.size(1) != feat_dim_ || f.scalar_type() != feat_dtype_ ||
+          f.device() != dev_ || !f.is_contiguous())
+        return 0;
+      fp = f.data_ptr();
+    }
+    void* stream = current_stream(dev_.index());
+    if (reinterpret_cast<int64_t>(stream) != stream_) return 0;
+    has_ = false;
+    const int rc = tgx_ring_commit(reinterpret_cast<const tgx_ring*>(ring_), src_.data_ptr<int64_t>(),
+                                   dst_.data_ptr<int64_t>(), time_.data_ptr<double>(), fp, b, eid_base,
+                                   ws_.data_ptr(), static_cast<size_t>(ws_.numel()),
+                                   status_.data_ptr<int32_t>(), stream);
+    src_ = dst_ = time_ = at::Tensor();
+    check(rc, "tgx_ring_commit");
+    return b;
+  }
+  // drops a pending plan enqueued on `stream` (the caller's current one); false
+  // when the plan lives on another stream (the caller orders the streams first)
+  bool discard_here(void* stream) {
+    if (!has_) return true;
+    if (reinterpret_cast<int64_t>(stream) != stream_) return false;
+    has_ = false;
+    const int rc = tgx_ring_discard(reinterpret_cast<const tgx_ring*>(ring_), src_.data_ptr<int64_t>(),
+                                    dst_.data_ptr<int64_t>(), src_.numel(), ws_.data_ptr(),
+                                    static_cast<size_t>(ws_.numel()), stream);
+    src_ = dst_ = time_ = at::Tensor();
+    check(rc, "tgx_ring_discard");
+    return true;
+  }
+  const at::Tensor& ws() const { return ws_; }
+
+ private:
+  int64_t ring_;
+  at::Tensor status_, ws_;
+  int64_t feat_dim_;
+  at::ScalarType feat_dtype_;
+  at::Device dev_;
+  at::Tensor src_, dst_, time_;
+  uint32_t ver_[3] = {0, 0, 0};
+  int64_t stream_ = 0;
+  bool has_ = false;
+};
+
 // Generic launch (TemporalGraph.recent, recent_2hop, co_neighbors, the timing
 // launches of DataPipeline.launch).  Queries arrive as groups (nodes, times,
 // times_per[, valid]) read in place by the kernel.  append_src/dst/time +
@@ -218,7 +354,9 @@ py::tuple recent(int64_t ring_addr, int64_t csr_addr, const std::vector<at::Tens
   a.group = static_cast<int32_t>(group);
   a.num_groups = num_groups < 0 ? 0 : num_groups;
   if (event_query_groups < 0) {
-    event_query_groups = a.plan_mode == TGX_PLAN_EVENTS ? pair_tail_groups(ng, Q) : 0;
+    int64_t G = 0;
+    for (size_t g = 0; g < ng; ++g) G += gper[g];
+    event_query_groups = a.plan_mode == TGX_PLAN_EVENTS ? pair_tail_groups(ng, Q, G, k) : 0;
     if (event_query_groups > 0) a.group = static_cast<int32_t>(gper[0] + gper[1]);
   }
   a.event_query_groups = static_cast<int32_t>(event_query_groups);
@@ -275,29 +413,35 @@ py::tuple recent(int64_t ring_addr, int64_t csr_addr, const std::vector<at::Tens
 // The 1-hop prepare of one DataPipeline on one graph, configured once: the
 // query groups [src, dst, neg (row-major), neg_src] that the spec asks for,
 // k, the feature layout, the time encoding and the co-occurrence mode.
-// run() takes one batch and returns (planned, tensors) as recent() does, with
-// the groups present in this batch in that order.
+// run() takes one batch, launches on the caller's current stream and returns
+// the tensors of recent() (without the planned flag), the groups present in
+// this batch in that order.
 class Prepare {
  public:
   Prepare(int64_t ring_addr, int64_t csr_addr, int64_t groups_mask, int64_t k, int64_t feat_dim,
           at::ScalarType feat_dtype, int64_t d_t, const c10::optional<at::Tensor>& te_w,
           const c10::optional<at::Tensor>& te_b, double te_bound_w, double te_bound_b,
           int64_t dt_mode, int64_t co_mode, bool want_eids,
-          int64_t qpw, const at::Tensor& status)
+          int64_t qpw, const at::Tensor& status, std::shared_ptr<PlanSlot> slot)
       : ring_(ring_addr), csr_(csr_addr), mask_(groups_mask), k_(k), feat_dim_(feat_dim),
         feat_dtype_(feat_dtype), d_t_(d_t), te_w_(te_w), te_b_(te_b),
         te_bound_w_(static_cast<float>(te_bound_w)), te_bound_b_(static_cast<float>(te_bound_b)),
         dt_mode_(dt_mode),
         co_mode_(co_mode), want_eids_(want_eids), qpw_(qpw), status_(status),
-        dev_(status.device()) {
+        dev_(status.device()), slot_(std::move(slot)) {
     if (k < 1 || k > TGX_MAX_K) throw std::invalid_argument("Prepare: k outside [1, TGX_MAX_K]");
     if (co_mode != TGX_CO_NONE && (groups_mask & 3) != 3)
       throw std::invalid_argument("Prepare: co-occurrence needs the src and dst groups");
   }
 
-  py::tuple run(const at::Tensor& src, const at::Tensor& dst, const at::Tensor& time,
-                const c10::optional<at::Tensor>& neg, const c10::optional<at::Tensor>& neg_src,
-                int64_t stream, const c10::optional<at::Tensor>& append_ws) const {
+  // plan: also plan this batch's ring update in the launch (when the graph has a
+  // ring and the tensors allow it), for the advance() that follows; a pending
+  // plan of an earlier batch on this stream is discarded first.  Returns None,
+  // having done nothing, when the plan state needs the caller: an earlier plan
+  // pending on another stream, or a plan workspace smaller than this batch needs.
+  py::object run(const at::Tensor& src, const at::Tensor& dst, const at::Tensor& time,
+                 const c10::optional<at::Tensor>& neg, const c10::optional<at::Tensor>& neg_src,
+                 bool plan) const {
     const int64_t b = src.size(0);
     if (dst.size(0) != b || time.size(0) != b)
       throw std::invalid_argument("prepare: src, dst and time must have the same length");
@@ -333,11 +477,8 @@ class Prepare {
     }
     // event-major groups when the pair must meet in one workgroup
     const bool events = co_mode_ != TGX_CO_NONE;
-    const bool tail = events && pair_tail_groups(static_cast<size_t>(ng), Q) > 0;
+    const bool tail = events && pair_tail_groups(static_cast<size_t>(ng), Q, G, k_) > 0;
     if (tail) G = per[0] + per[1];
-    if (events && G > TGX_MAX_GROUP)
-      throw std::invalid_argument("prepare: " + std::to_string(G) +
-                                  " queries per event exceed the fused group limit");
     const Out out(dev_, Q, k_, feat_dim_, feat_dtype_, d_t_, want_eids_, co_mode_, b);
     tgx_recent_args a{};
     a.num_queries = Q;
@@ -363,19 +504,29 @@ class Prepare {
       a.query_groups[g].count = b * per[g];
       a.query_groups[g].times_per = per[g];
     }
-    const bool planned = append_ws.has_value() && ring_ != 0 && plannable(src, dst, time, dev_);
+    void* stream = current_stream(dev_.index());
+    PlanSlot* slot = plan && ring_ != 0 ? slot_.get() : nullptr;
+    const bool planned = slot != nullptr && plannable(src, dst, time, dev_);
+    if (slot != nullptr) {
+      // an earlier plan nobody advanced is dropped first (it shares the scratch)
+      if (slot->pending() && !slot->discard_here(stream)) return py::none();
+    }
     if (planned) {
+      const at::Tensor& ws = slot->ws();
+      if (!ws.defined() || static_cast<size_t>(ws.numel()) < tgx_ring_append_workspace_size(b))
+        return py::none();
       a.append_src = src.data_ptr<int64_t>();
       a.append_dst = dst.data_ptr<int64_t>();
       a.append_time = time.data_ptr<double>();
       a.append_b = b;
-      a.append_workspace = append_ws->data_ptr();
-      a.append_workspace_bytes = static_cast<size_t>(append_ws->numel());
+      a.append_workspace = ws.data_ptr();
+      a.append_workspace_bytes = static_cast<size_t>(ws.numel());
     }
     if (Q > 0 || a.append_b > 0)
       check(tgx_recent(reinterpret_cast<const tgx_ring*>(ring_),
-                       reinterpret_cast<const tgx_csr*>(csr_), &a, reinterpret_cast<void*>(stream)),
+                       reinterpret_cast<const tgx_csr*>(csr_), &a, stream),
             "tgx_recent");
+    if (planned) slot->record(src, dst, time, reinterpret_cast<int64_t>(stream));
     std::vector<at::Tensor> res;
     res.reserve(ng * 6 + 3);
     int64_t r0 = 0;
@@ -384,7 +535,7 @@ class Prepare {
       r0 += b * per[g];
     }
     if (out.co) out.co_out(res);
-    return py::make_tuple(planned, std::move(res));
+    return as_tuple(res);
   }
 
  private:
@@ -398,6 +549,7 @@ class Prepare {
   int64_t qpw_;
   at::Tensor status_;
   at::Device dev_;
+  std::shared_ptr<PlanSlot> slot_;
 };
 
 void ring_append(int64_t ring_addr, const at::Tensor& src, const at::Tensor& dst,
@@ -453,11 +605,23 @@ void ring_discard(int64_t ring_addr, const at::Tensor& src, const at::Tensor& ds
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("recent", &recent, "allocate outputs, launch tgx_recent, return (planned, tensors)");
+  py::class_<PlanSlot, std::shared_ptr<PlanSlot>>(m, "PlanSlot")
+      .def(py::init<int64_t, const at::Tensor&, int64_t, at::ScalarType>())
+      .def("set_workspace", &PlanSlot::set_workspace)
+      .def("workspace", &PlanSlot::workspace)
+      .def("pending", &PlanSlot::pending)
+      .def("stream", &PlanSlot::stream)
+      .def("set_stream", &PlanSlot::set_stream)
+      .def("record", &PlanSlot::record)
+      .def("matches", &PlanSlot::matches)
+      .def("take", &PlanSlot::take)
+      .def("commit", &PlanSlot::commit, "advance() of the planned batch: b, or 0 (nothing done)");
   py::class_<Prepare>(m, "Prepare")
       .def(py::init<int64_t, int64_t, int64_t, int64_t, int64_t, at::ScalarType, int64_t,
                     const c10::optional<at::Tensor>&, const c10::optional<at::Tensor>&, double,
-                    double, int64_t, int64_t, bool, int64_t, const at::Tensor&>())
-      .def("run", &Prepare::run, "one 1-hop prepare launch: (planned, tensors)");
+                    double, int64_t, int64_t, bool, int64_t, const at::Tensor&,
+                    std::shared_ptr<PlanSlot>>())
+      .def("run", &Prepare::run, "one 1-hop prepare launch: its tensors, or None");
   m.def("ring_append", &ring_append, "launch tgx_ring_append on one batch");
   m.def("ring_plan", &ring_plan, "launch tgx_ring_plan (first half of an append)");
   m.def("ring_commit", &ring_commit, "launch tgx_ring_commit (second half of an append)");

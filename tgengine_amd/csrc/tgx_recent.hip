@@ -639,10 +639,14 @@ void recent_fused(Params P) {
   wave_sync();
   if (q >= 0) {
     if (!fast) {
+      // counting rank by (time, CSR-before-ring, candidate index).  The CSR
+      // window is time-ascending with ties in CSR order, so CSR entry c has
+      // exactly c such predecessors among the CSR entries and only the ring
+      // candidates need counting; a ring candidate counts them all
       for (int c = sl; c < ncand; c += Bp) {
         const double tc = ct[h * C + c];
-        int r = 0;
-        for (int c0 = 0; c0 < ncand; c0 += 4) {
+        int r = c < ncsr ? c : 0;
+        for (int c0 = c < ncsr ? ncsr : 0; c0 < ncand; c0 += 4) {
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
             const int c2 = c0 + u;
@@ -1115,12 +1119,16 @@ int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args
   // holds at most kMaxWaves waves (the kernel's launch bound): its query slots
   // (the plan group, or `group` consecutive tiles) times split.
   const int qwant = mode != TGX_PLAN_TILES ? a->group : 1;
+  // waves whose LDS fits the CU's 160 KB next to the encoder weights (a large K
+  // with a CSR window takes about 24 KB per wave)
+  const int lds_waves = static_cast<int>((160 * 1024 - P.te_bytes) / P.wave_bytes);
+  const int wave_cap = lds_waves < kMaxWaves ? lds_waves : kMaxWaves;
   int split = 1;
   if (P.m == 1) {
-    while (split < 8 && a->num_queries * (split * 2) <= kSplitMaxWaves && qwant * split * 2 <= kMaxWaves)
+    while (split < 8 && a->num_queries * (split * 2) <= kSplitMaxWaves && qwant * split * 2 <= wave_cap)
       split *= 2;
     const int64_t qbytes = static_cast<int64_t>(K) * (P.row_bytes + 4 * a->d_t + 13);
-    while (split < 8 && qbytes / (split * 2) >= kSplitBytes && qwant * split * 2 <= kMaxWaves)
+    while (split < 8 && qbytes / (split * 2) >= kSplitBytes && qwant * split * 2 <= wave_cap)
       split *= 2;
   }
   const int lg_split = split == 1 ? 0 : split == 2 ? 1 : split == 4 ? 2 : 3;  // split is 1, 2, 4 or 8
@@ -1130,6 +1138,7 @@ int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args
   // 600 queries, 4 waves each, ran 0.5 us faster in 600 workgroups than in 300)
   int qslots = a->group;
   if (mode == TGX_PLAN_TILES && split > 1) qslots = 1;
+  if (mode == TGX_PLAN_TILES && qslots * split > wave_cap) qslots = wave_cap > split ? wave_cap / split : 1;
   const int waves = qslots * split;
   if (waves < 1 || waves > kMaxWaves)
     return fail(TGX_ERR_LIMIT, "tgx_recent: %d wavefronts per workgroup outside [1, %d]", waves, kMaxWaves);

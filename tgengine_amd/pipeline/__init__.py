@@ -128,7 +128,7 @@ class DataPipeline:
         prep = _host().Prepare(ring, csr, mask, int(nb.k), g.edge_feat_dim, g.feat_dtype, d_t, te_w,
                                te_b, te_bounds[0], te_bounds[1], _DT_MODES[spec.dt_mode], co_mode,
                                bool(spec.edge_ids),
-                               self.queries_per_workgroup, g._status)
+                               self.queries_per_workgroup, g._status, g._slot)
         self._ctx = (key, prep, 4 + (d_t > 0) + bool(spec.edge_ids), d_t > 0, bool(spec.edge_ids),
                      mask, want_co)
         return self._ctx
@@ -199,7 +199,9 @@ class DataPipeline:
         _, prep, nf, has_te, has_eids, mask, want_co = self._context()
         src, dst, tm = raw_batch.src, raw_batch.dst, raw_batch.time
         neg, neg_src = raw_batch.neg, raw_batch.neg_src
-        res = g._prepare(prep, src, dst, tm, neg, neg_src, self.plan_updates)[1]
+        res = prep.run(src, dst, tm, neg, neg_src, self.plan_updates)
+        if res is None:  # the plan state needs settling first
+            res = g._prepare(prep, src, dst, tm, neg, neg_src, self.plan_updates)
         nbrs = [None, None, None, None]
         i = 0
         for slot, bit, present in ((0, 1, True), (1, 2, True), (2, 4, neg is not None),
@@ -287,9 +289,11 @@ class DataPipeline:
         workgroup, in the layout prepare() launches."""
         g = self.graph
         if co_mode != _lib.TGX_CO_NONE:
+            # the extension picks the layout (event_query_groups=-1): every query of
+            # an event in its workgroup, or only the (src, dst) pair with the other
+            # groups tiled after them (small launches, or more queries per event
+            # than a workgroup takes)
             G = sum(per_event)
-            if G > _lib.TGX_MAX_GROUP:
-                raise ValueError(f"{G} queries per event exceed the fused group limit {_lib.TGX_MAX_GROUP}")
             return g._query(None, None, k, groups=qgroups, plan_mode=_lib.TGX_PLAN_EVENTS, group=G,
                             num_groups=b, event_query_groups=-1, d_t=d_t, te_w=te_w, te_b=te_b,
                             te_bounds=te_bounds, dt_mode=dt_mode, co_mode=co_mode,

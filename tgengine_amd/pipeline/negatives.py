@@ -23,7 +23,8 @@ from tgengine_amd.core.temporal_graph import TemporalGraph, _stream_handle
 
 
 class HistoricalNegPool:
-    """Per-node bounded pool for historically-correct negative sampling.
+    """For every source node, a fixed-size reservoir of the destinations it has
+    linked to, so a negative can be drawn from that node's own history.
 
     Usage (as the reference):
         pool = HistoricalNegPool(num_nodes, pool_size=512, device="cuda")
@@ -98,7 +99,8 @@ class NegativeStrategy(ABC):
         """(B,) or (B, N_neg) negative node ids."""
 
     def update(self, src: Tensor, dst: Tensor) -> None:
-        """Ingest new edges (called alongside graph.advance()). No-op by default."""
+        """Take in a batch of edges, next to graph.advance(); strategies without
+        state ignore it."""
 
 
 class HistoricalNegative(NegativeStrategy):
@@ -126,5 +128,6 @@ class FixedNegative(NegativeStrategy):
     def sample(self, src: Tensor, dst: Tensor, time: Tensor, graph: TemporalGraph,
                edge_indices: Optional[Tensor] = None) -> Tensor:
         if edge_indices is None:
-            raise ValueError("FixedNegative requires edge_indices in RawBatch")
+            raise ValueError("FixedNegative looks its lists up by global edge index: "
+                             "pass the batch's edge_indices")
         return self.neg_lists[edge_indices.long()].to(src.device)
