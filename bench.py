@@ -460,6 +460,138 @@ def run_rows(a, log) -> None:
     log(f"rows: negpool {ms * 1e3:.2f} us per update + sample")
 
 
+def run_csr_prepare(a, log) -> None:
+    """--csr-prepare: DataPipeline.prepare on a frozen CSR, as the reference's Engine
+    runs it (engine/__init__.py:174-195: advance the training events, freeze,
+    then prepare batches without advancing), at the shapes of its published
+    pipeline timings (docs/performance_report.md:29-31): Wikipedia (K=32),
+    Reddit (K=64) and LastFM (K=512, 2-d rows) node and event counts, batch 200,
+    one negative per event (600 queries), plus the 100-d cosine time encoding.
+    The first 70% of each synthetic stream is frozen; batches of the rest are
+    prepared.  Per shape: host-inclusive microseconds per prepare step (outputs
+    held to the next step, as a training loop does), the gather kernel's time
+    per launch (a HIP graph of R launches replayed between two HIP events), its
+    algorithmic bytes against the HBM roofline, and the oracle's restatement on
+    one batch (outputs compared, and its time as the CPU baseline).  One JSON
+    line per shape."""
+    import torch
+    from oracle import spec
+    from tgengine_amd import RawBatch
+    from tgengine_amd.synthetic import ENGINE_SHAPES, make_graph, make_pipeline, num_batches
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    published_ms = {"wikipedia": 1.83, "reddit": 3.69, "lastfm": 1.70}
+    for name in a.csr_shapes.split(","):
+        cfg = ENGINE_SHAPES[name]
+        nb = num_batches(cfg)
+        ntrain = int(0.7 * nb)
+        W, S, R = 20, min(a.csr_steps, nb - ntrain - 20), min(200, nb - ntrain)
+        t0 = time.time()
+        dev, lens, bts = stage_stream(cfg, 0, nb, torch, device)
+        offs = np.concatenate([[0], np.cumsum(lens)])
+
+        def raw(i):
+            s_, e_ = int(offs[i]), int(offs[i + 1])
+            return RawBatch(src=dev["src"][s_:e_], dst=dev["dst"][s_:e_], time=dev["time"][s_:e_],
+                            edge_feat=dev["feat"][s_:e_], neg=dev["neg"][s_:e_])
+        g = make_graph(cfg)
+        for i in range(ntrain):
+            r_ = raw(i)
+            g.advance(r_.src, r_.dst, r_.time, r_.edge_feat)
+        torch.cuda.synchronize()
+        f0 = time.perf_counter()
+        g.freeze_csr()
+        torch.cuda.synchronize()
+        freeze_ms = (time.perf_counter() - f0) * 1e3
+        pipe = make_pipeline(cfg, g)
+        pipe.plan_updates = False  # nothing is advanced after the freeze
+        raws = [raw(i) for i in range(ntrain, nb)]
+        log(f"{name}: staged {nb} batches, froze {ntrain} ({int(offs[ntrain])} events) in "
+            f"{freeze_ms:.1f} ms, {time.time() - t0:.1f}s so far")
+        # host-inclusive steps
+        pb = None
+        for i in range(W):
+            pb = pipe.prepare(raws[i])
+        torch.cuda.synchronize()
+        h0 = time.perf_counter()
+        for i in range(W, W + S):
+            pb = pipe.prepare(raws[i])
+        torch.cuda.synchronize()
+        step_us = (time.perf_counter() - h0) / S * 1e6
+        del pb
+        # kernel time per launch: the first R prepare launches, graph-replayed
+        args = pipe.launch_args(raws[0])
+        masks = []
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(R):
+                masks.append(tuple(pipe.launch(raws[i], args)["mask"]))
+        graph.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        kern_us = e0.elapsed_time(e1) * 1e3 / R
+        del graph
+        Q = sum(int(m.shape[0]) for ms in masks for m in ms)
+        V = sum(int(m.sum()) for ms in masks for m in ms)
+        rb_ = cfg.feat_dim * cfg.feat_bytes
+        # per query: query id + time and its CSR offsets read, V entries (id, time,
+        # row) read; K slots of id, time, mask, row and d_t encodings written
+        nbytes = (Q * (16 + 16) + V * (12 + rb_) + Q * cfg.k * (13 + rb_ + 4 * cfg.d_t)) / R
+        gbs = nbytes / (kern_us * 1e-6) / 1e9
+        # parity and CPU baseline: the oracle on the first prepared batch
+        evs = [(bt["src"], bt["dst"], bt["time"], bt["feat"], int(offs[i])) for i, bt in enumerate(bts[:ntrain])]
+        csr = spec.csr_freeze(cfg.num_nodes, cfg.feat_dim, evs, np.float32)
+        bt = bts[ntrain]
+        nodes = np.concatenate([bt["src"], bt["dst"], bt["neg"]])
+        qt = np.concatenate([bt["time"]] * 3)
+        c0 = time.perf_counter()
+        o = spec.recent(nodes, qt, cfg.k, csr, None, cfg.feat_dim)
+        te = spec.time_encode_exact(spec.dt_dygformer(qt, o.times), spec.time_weights(cfg.d_t), o.mask)
+        cpu_s = time.perf_counter() - c0
+        pb = pipe.prepare(raws[0])
+        groups = [pb.src_neighbors, pb.dst_neighbors, pb.neg_neighbors]
+        got = {k: torch.cat([getattr(x, f) for x in groups]).cpu().numpy()
+               for k, f in (("ids", "neighbor_ids"), ("times", "timestamps"), ("mask", "mask"),
+                            ("feats", "edge_feats"), ("te", "time_enc"))}
+        same = (np.array_equal(got["ids"], o.ids) and np.array_equal(got["mask"], o.mask)
+                and np.array_equal(got["times"].view(np.int64), o.times.view(np.int64))
+                and np.array_equal(got["feats"], o.feats))
+        te_err = float(np.abs(got["te"] - te).max())
+        if not same or te_err > 1e-6:
+            raise RuntimeError(f"csr prepare {name}: device and oracle differ (te error {te_err:.2e})")
+        del csr, evs, pb, got
+        line = {"row": f"prepare_csr_{name}",
+                "metric": "prepared queries/s (DataPipeline.prepare on a frozen CSR, Engine shape)",
+                "value": 600 / (step_us * 1e-6), "unit": "prepared queries/s",
+                "us_per_step": step_us, "kernel_us_per_launch": kern_us,
+                "workload": (f"{name}-shaped synthetic stream: {cfg.num_nodes} nodes, {cfg.num_events} events, "
+                             f"{ntrain} batches of 200 frozen, then prepare() of the next batches without "
+                             f"advancing: 600 queries (src, dst, 1 negative), K={cfg.k}, {cfg.feat_dim}-d f32 "
+                             f"rows, 100-d time encoding; mean V {V / Q:.1f}"),
+                "freeze_ms": freeze_ms,
+                "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                             "frac": gbs / PEAK_HBM_GBS, "bytes_per_launch": nbytes,
+                             "timing": f"HIP event pair around a graph replay of {R} launches"},
+                "cpu_baseline": {"value": len(nodes) / cpu_s, "unit": "prepared queries/s", "cores": 1,
+                                 "kind": "port",
+                                 "sample": f"oracle.spec.recent + time_encode_exact (numpy) of batch {ntrain}"},
+                "parity": f"batch {ntrain}'s ids, times, masks and rows equal to the oracle's, encodings "
+                          f"within {te_err:.1e}",
+                "reference_published_ms_per_step": published_ms[name],
+                "reference_published_note": "Pipeline/Sampling per step on an RTX 4080, DyGFormer spec "
+                                            "(no time encoding), docs/performance_report.md:47-74"}
+        print(json.dumps(line), flush=True)
+        log(f"{name}: {step_us:.1f} us/step, kernel {kern_us:.2f} us, {gbs:.0f} GB/s")
+        del g, pipe, raws, dev, bts
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -481,6 +613,11 @@ def main():
                     help="--rows: C3 batches frozen into the CSR")
     ap.add_argument("--rows-cpu-batches", type=int, default=100,
                     help="--rows: C3 batches in the oracle's samples")
+    ap.add_argument("--csr-prepare", action="store_true",
+                    help="instead of the streaming step, time DataPipeline.prepare on a frozen CSR at the "
+                         "reference's published Engine shapes (Wikipedia, Reddit, LastFM), one JSON line each")
+    ap.add_argument("--csr-shapes", default="wikipedia,reddit,lastfm")
+    ap.add_argument("--csr-steps", type=int, default=500)
     ap.add_argument("--ceilings", action="store_true",
                     help="after timing, measure the device's copy, store and row-gather ceilings "
                          "(plain torch kernels at 1 GiB and at the gather's byte count) and report them")
@@ -492,6 +629,9 @@ def main():
     log = (lambda *x: None) if a.quiet else (lambda *x: print(*x, file=sys.stderr, flush=True))
     if a.rows:
         run_rows(a, log)
+        return
+    if a.csr_prepare:
+        run_csr_prepare(a, log)
         return
 
     import torch

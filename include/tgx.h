@@ -270,7 +270,15 @@ int tgx_ring_discard(const tgx_ring* ring, const int64_t* src, const int64_t* ds
  * be NULL).  Entries whose node is outside [0, N), or whose event is outside
  * [0, num_events) while feats is set, are counted in
  * status[TGX_ST_BAD_EVENT_NODE] (out-of-range nodes sort after every node).
- * workspace: tgx_csr_build_workspace_size(n) bytes, no initialisation needed. */
+ * workspace: tgx_csr_build_workspace_size(n) bytes, no initialisation needed.
+ *
+ * flags & TGX_CSR_EVENT_PAIRS: from/to/time hold the n/2 EVENTS (src, dst,
+ * time) instead of the n entries, in an order where the stable sort by time
+ * is the identity on the entries 2k = from[k]->to[k], 2k+1 = to[k]->from[k]
+ * (both at time[k]; event index k, or event[k] when event is set): times
+ * strictly increasing within every advance() call and non-decreasing across
+ * calls, which makes this order the stable time order of the build order.  The
+ * time passes are skipped; the caller checks the condition. */
 typedef struct tgx_csr_build_args {
   int64_t num_nodes;
   int64_t num_entries;
@@ -290,7 +298,10 @@ typedef struct tgx_csr_build_args {
   void* workspace;
   size_t workspace_bytes;
   int32_t* status;         /* [TGX_STATUS_WORDS] or NULL */
+  uint32_t flags;          /* TGX_CSR_* */
 } tgx_csr_build_args;
+
+#define TGX_CSR_EVENT_PAIRS 1u
 
 size_t tgx_csr_build_workspace_size(int64_t num_entries);
 int tgx_csr_build(const tgx_csr_build_args* args, void* stream);

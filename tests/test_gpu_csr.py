@@ -132,6 +132,54 @@ def test_csr_build_three_level_count_scan():
     _compare(g, ref)
 
 
+def _ordered_batches(rng, N, sizes, d, bf16, feat_every=2, node_hi=None):
+    """A time-ordered stream: times strictly increasing within every batch, each
+    batch starting at its predecessor's last time (a tie across the boundary)."""
+    out, t = [], 100.0
+    hi = node_hi or N
+    for k, b in enumerate(sizes):
+        tt = t + np.cumsum(rng.exponential(1.0, b) + 1e-3)
+        if k > 0 and b > 0:
+            tt[0] = t
+        if b > 0:
+            t = float(tt[-1])
+        src = rng.integers(0, hi, b)
+        src[: b // 5] = 3 % N  # a hot node
+        feat = _feat(rng, b, d, bf16) if (feat_every and k % feat_every == 0) else None
+        out.append((src.astype(np.int64), rng.integers(0, hi, b).astype(np.int64), tt.astype(np.float64), feat))
+    return out
+
+
+@pytest.mark.parametrize("d,bf16,eids,N", [(16, True, True, 5000), (172, False, False, 300),
+                                           (3, False, True, 200_000), (0, False, False, 70_000)])
+def test_csr_build_time_ordered_stream(d, bf16, eids, N):
+    """A time-ordered stream is built from its events in pairs (node passes only):
+    the same CSR as the oracle's two stable sorts of the build order."""
+    rng = np.random.default_rng(20 + d)
+    batches = _ordered_batches(rng, N, [500, 1, 0, 2000, 777, 3], d, bf16, node_hi=N - 50)
+    g, ref = _build(N, d, bf16, batches, eids)
+    assert g._csr_time_sorted
+    _compare(g, ref)
+
+
+@pytest.mark.parametrize("where", ["tie", "step_back", "nan"])
+def test_csr_build_almost_ordered_stream_sorts_by_time(where):
+    """One tie inside a batch, one step back in time, or a NaN: the stream is not
+    time-ordered, so the build sorts the build order by time first."""
+    rng = np.random.default_rng(30)
+    batches = _ordered_batches(rng, 40, [300, 300, 300], 4, False)
+    t = batches[1][2]
+    if where == "tie":
+        t[100] = t[99]
+    elif where == "step_back":
+        t[150] = t[10] - 1.0
+    else:
+        t[7] = np.nan
+    g, ref = _build(40, 4, False, batches, True)
+    assert not g._csr_time_sorted
+    _compare(g, ref)
+
+
 def test_csr_build_rejects_out_of_range_nodes():
     g = TemporalGraph(10, edge_feat_dim=2, device="cuda")
     g.advance(torch.tensor([1, 10], device="cuda"), torch.tensor([2, 3], device="cuda"),

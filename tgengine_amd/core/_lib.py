@@ -79,7 +79,11 @@ class TgxCsrBuildArgs(ctypes.Structure):
                 ("time", c_vp), ("event", c_vp), ("feats", c_vp), ("num_events", c_i64),
                 ("feat_dim", c_i32), ("feat_dtype", c_i32), ("out_offsets", c_vp),
                 ("out_ids", c_vp), ("out_times", c_vp), ("out_feats", c_vp), ("out_eids", c_vp),
-                ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t), ("status", c_vp)]
+                ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t), ("status", c_vp),
+                ("flags", ctypes.c_uint32)]
+
+
+TGX_CSR_EVENT_PAIRS = 1
 
 
 # every symbol include/tgx.h declares, with its ctypes signature

@@ -131,7 +131,13 @@ class TemporalGraph:
         self.track_edge_ids = bool(track_edge_ids)
         self._num_edges = 0
 
-        self._build: list = []       # pre-freeze (src, dst, time, feat|None, eid_base) device copies
+        # pre-freeze events, appended in advance() order to device buffers that
+        # grow by doubling: src, dst (int64), time (float64), feat rows (made on
+        # the first batch with features, zero rows before it); the event index in
+        # them is the global edge id.  _build_starts: first event of each call
+        self._build: dict = {}
+        self._build_n = 0
+        self._build_starts: list = []
         self._frozen = False
         self._offsets: Optional[Tensor] = None
         self._nbr_ids: Optional[Tensor] = None
@@ -345,14 +351,10 @@ class TemporalGraph:
                     return
                 self._discard_plan()
         if not self._frozen:
-            # the values at call time, as device copies (the reference copies them
-            # into host lists, temporal_graph.py:110-122)
-            dev = self.device
-            feat = (None if edge_feat is None
-                    else self._feat_in(edge_feat, b).detach().clone(memory_format=torch.contiguous_format))
-            self._build.append((src.detach().to(dev, torch.int64).clone(),
-                                dst.detach().to(dev, torch.int64).clone(),
-                                time.detach().to(dev, torch.float64).clone(), feat, self._num_edges))
+            # the values at call time, copied into the device event buffers (the
+            # reference copies them into host lists, temporal_graph.py:110-122)
+            if b > 0:
+                self._build_append(src, dst, time, self._feat_in(edge_feat, b), b)
         else:
             self._ensure_overflow()
             if b > 0:
@@ -367,59 +369,111 @@ class TemporalGraph:
                             ws, self._status, _stream_handle(self.device))
 
     # ------------------------------------------------------------------ CSR
+    def _build_append(self, src: Tensor, dst: Tensor, time: Tensor, feat: Optional[Tensor],
+                      b: int) -> None:
+        """Copy one pre-freeze batch into the event buffers (grown by doubling)."""
+        dev, d = self.device, self.edge_feat_dim
+        n0 = self._build_n
+        n1 = n0 + b
+        bufs = self._build
+        cap = int(bufs["src"].shape[0]) if bufs else 0
+        if n1 > cap:
+            cap = max(n1, 2 * cap, 1 << 12)
+            grown = {"src": torch.empty(cap, dtype=torch.int64, device=dev),
+                     "dst": torch.empty(cap, dtype=torch.int64, device=dev),
+                     "time": torch.empty(cap, dtype=torch.float64, device=dev)}
+            if "feat" in bufs:
+                grown["feat"] = torch.empty((cap, d), dtype=self.feat_dtype, device=dev)
+            for k, v in bufs.items():
+                grown[k][:n0].copy_(v[:n0])
+            self._build = bufs = grown
+        bufs["src"][n0:n1].copy_(src.detach().reshape(-1))
+        bufs["dst"][n0:n1].copy_(dst.detach().reshape(-1))
+        bufs["time"][n0:n1].copy_(time.detach().reshape(-1))
+        if feat is not None and d > 0 and "feat" not in bufs:
+            bufs["feat"] = torch.empty((cap, d), dtype=self.feat_dtype, device=dev)
+            bufs["feat"][:n0].zero_()
+        if "feat" in bufs:
+            if feat is None:
+                bufs["feat"][n0:n1].zero_()
+            else:
+                bufs["feat"][n0:n1].copy_(feat)
+        self._build_starts.append(n0)
+        self._build_n = n1
+
     def freeze_csr(self) -> None:
         """Build the frozen CSR on the device from the pre-freeze events
         (reference :133-181), with tgx_csr_build.
 
         Build order per advance() call is [src->dst ..., dst->src ...]; entries
         are sorted stably by time, then stably by node, so a node's entries are
-        time-ascending with ties in build order.
+        time-ascending with ties in build order.  When the event times increase
+        strictly within every call and never decrease across calls (a
+        time-ordered stream), that time order is already the events' own order
+        with each event's two entries side by side, and the build sorts by node
+        only (TGX_CSR_EVENT_PAIRS); otherwise it sorts the build order by time
+        first.
         """
         N, d, dev = self.num_nodes, self.edge_feat_dim, self.device
-        batches = [x for x in self._build if x[0].shape[0] > 0]
-        n = 2 * sum(int(x[0].shape[0]) for x in batches)
+        E = self._build_n
+        n = 2 * E
         self._offsets = torch.zeros(N + 1, dtype=torch.int64, device=dev)
         self._nbr_ids = torch.empty(n, dtype=torch.int32, device=dev)
         self._nbr_times = torch.empty(n, dtype=torch.float64, device=dev)
         self._nbr_feats = torch.empty((n, d), dtype=self.feat_dtype, device=dev)
         self._nbr_eids = torch.empty(n, dtype=torch.int64, device=dev) if self.track_edge_ids else None
         if n > 0:
-            # directed entries in build order (gathered once more by the build)
-            frm = torch.cat([t for (s_, t_, _, _, _) in batches for t in (s_, t_)])
-            if int(frm.min()) < 0 or int(frm.max()) >= N:
+            bufs = self._build
+            src, dst, tt = bufs["src"][:E], bufs["dst"][:E], bufs["time"][:E]
+            feats = bufs["feat"][:E] if "feat" in bufs else None
+            # one device round trip: node range, and whether the stream is time-ordered
+            lo = torch.minimum(src.min(), dst.min())
+            hi = torch.maximum(src.max(), dst.max())
+            if E > 1:
+                step = tt[1:] - tt[:-1]
+                first = torch.zeros(E, dtype=torch.bool, device=dev)
+                first[torch.tensor(self._build_starts, dtype=torch.int64).to(dev)] = True
+                ordered = ((step > 0) | ((step == 0) & first[1:])).all()
+            else:
+                ordered = torch.ones((), dtype=torch.bool, device=dev)
+            lo, hi, ordered = (int(x) for x in torch.stack([lo, hi, ordered.long()]).cpu())
+            if lo < 0 or hi >= N:
                 raise IndexError("advance() got node ids outside [0, num_nodes)")
-            to = torch.cat([t for (s_, t_, _, _, _) in batches for t in (t_, s_)])
-            tt = torch.cat([tm for (_, _, tm, _, _) in batches for _ in (0, 1)])
-            # edge ids eb + i of each batch's two directed segments, in one pass:
-            # entry e of a segment starting at entry s with base eb is eb + (e - s)
-            seg_len = torch.tensor([int(s_.shape[0]) for (s_, _, _, _, _) in batches for _ in (0, 1)],
-                                   dtype=torch.int64)
-            seg_base = torch.tensor([int(eb) for (_, _, _, _, eb) in batches for _ in (0, 1)],
-                                    dtype=torch.int64)
-            seg_shift = (seg_base - (torch.cumsum(seg_len, 0) - seg_len)).to(dev)
-            ev = (torch.repeat_interleave(seg_shift, seg_len.to(dev), output_size=n)
-                  + torch.arange(n, dtype=torch.int64, device=dev))
-            # event-major feature rows (row eb + i of the event), zeros for None
-            feats = None
-            if d > 0 and any(f is not None for (_, _, _, f, _) in batches):
-                feats = torch.cat([f if f is not None else
-                                   torch.zeros((s_.shape[0], d), dtype=self.feat_dtype, device=dev)
-                                   for (s_, _, _, f, _) in batches])
+            flags = 0
+            self._csr_time_sorted = bool(ordered)  # which build ran (diagnostics)
+            if ordered:
+                frm, to, tm, ev = src, dst, tt, None
+                flags = _lib.TGX_CSR_EVENT_PAIRS
+            else:
+                # directed entries in build order: per call, the events as
+                # src->dst, then again as dst->src
+                starts = torch.tensor(self._build_starts + [E], dtype=torch.int64)
+                lens = (starts[1:] - starts[:-1]).to(dev)
+                seg = torch.arange(len(self._build_starts), device=dev).repeat_interleave(2 * lens, output_size=n)
+                s0 = starts[:-1].to(dev)
+                pos = torch.arange(n, dtype=torch.int64, device=dev) - 2 * s0[seg]
+                rev = pos >= lens[seg]
+                ev = s0[seg] + torch.where(rev, pos - lens[seg], pos)
+                frm = torch.where(rev, dst[ev], src[ev])
+                to = torch.where(rev, src[ev], dst[ev])
+                tm = tt[ev]
             ws = torch.empty(int(_lib.lib().tgx_csr_build_workspace_size(n)), dtype=torch.uint8, device=dev)
             a = _lib.TgxCsrBuildArgs(
                 num_nodes=N, num_entries=n, from_=frm.data_ptr(), to=to.data_ptr(),
-                time=tt.data_ptr(), event=ev.data_ptr(),
+                time=tm.data_ptr(), event=_lib.ptr(ev),
                 feats=feats.data_ptr() if feats is not None else None,
-                num_events=int(feats.shape[0]) if feats is not None else 0,
+                num_events=E if feats is not None else 0,
                 feat_dim=d, feat_dtype=_DTYPES[self.feat_dtype],
                 out_offsets=self._offsets.data_ptr(), out_ids=self._nbr_ids.data_ptr(),
                 out_times=self._nbr_times.data_ptr(),
                 out_feats=self._nbr_feats.data_ptr() if d > 0 else None,
                 out_eids=_lib.ptr(self._nbr_eids), workspace=ws.data_ptr(),
-                workspace_bytes=ws.numel(), status=self._status.data_ptr())
+                workspace_bytes=ws.numel(), status=self._status.data_ptr(), flags=flags)
             _lib.check(_lib.lib().tgx_csr_build(ctypes.byref(a), _stream_handle(dev)), "tgx_csr_build")
         self._frozen = True
-        self._build = []
+        self._build = {}
+        self._build_n = 0
+        self._build_starts = []
         self._csr_struct = None
         self._gen += 1
 
@@ -591,7 +645,9 @@ class TemporalGraph:
         if self._ov_ids is not None:
             self._drop_plan()
         self._frozen = False
-        self._build = []
+        self._build = {}
+        self._build_n = 0
+        self._build_starts = []
         self._offsets = self._nbr_ids = self._nbr_times = self._nbr_feats = self._nbr_eids = None
         self._ov_ids = self._ov_times = self._ov_feats = self._ov_write_pos = self._ov_eids = None
         self._ov_scratch = None

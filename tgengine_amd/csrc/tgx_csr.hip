@@ -10,6 +10,11 @@
 //
 // The passes are tgx_radix.h's.  Then offsets[u] = lower_bound(sorted nodes, u), and one gather writes the
 // ids, times, edge ids and feature rows (16-byte vectors where aligned).
+//
+// Event pairs (TGX_CSR_EVENT_PAIRS): the caller hands the events themselves in
+// an order whose entries 2k, 2k+1 are already the stable time order of the
+// build order (a time-ordered stream); the time passes are skipped and the
+// kernels read an entry's node, neighbour, time and event from its event.
 #include "tgx_radix.h"
 
 namespace tgx {
@@ -37,7 +42,31 @@ __global__ __launch_bounds__(kThreads) void csr_init(const double* __restrict__ 
   idx[j] = static_cast<uint32_t>(j);
 }
 
-__global__ __launch_bounds__(kThreads) void csr_node_keys(const int64_t* __restrict__ from,
+// entry j of the input: its node, neighbour, time index and event index
+// (pairs: entry 2k = from[k] -> to[k], 2k + 1 = to[k] -> from[k], of event k)
+struct Entries {
+  const int64_t* from;
+  const int64_t* to;
+  const int64_t* event;
+  int pairs;
+  __device__ __forceinline__ int64_t node(int64_t j) const {
+    return pairs ? ((j & 1) ? to[j >> 1] : from[j >> 1]) : from[j];
+  }
+  __device__ __forceinline__ int64_t nbr(int64_t j) const {
+    return pairs ? ((j & 1) ? from[j >> 1] : to[j >> 1]) : to[j];
+  }
+  __device__ __forceinline__ int64_t row(int64_t j) const { return pairs ? j >> 1 : j; }
+  __device__ __forceinline__ int64_t ev(int64_t j) const {
+    return event != nullptr ? event[row(j)] : (pairs ? j >> 1 : -1);
+  }
+};
+
+__global__ __launch_bounds__(kThreads) void csr_identity(int64_t n, uint32_t* __restrict__ idx) {
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (j < n) idx[j] = static_cast<uint32_t>(j);
+}
+
+__global__ __launch_bounds__(kThreads) void csr_node_keys(Entries E,
                                                           const uint32_t* __restrict__ idx,
                                                           int64_t n, int64_t N,
                                                           uint32_t* __restrict__ nkey,
@@ -45,7 +74,7 @@ __global__ __launch_bounds__(kThreads) void csr_node_keys(const int64_t* __restr
   const int64_t p = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   bool bad = false;
   if (p < n) {
-    const int64_t u = from[idx[p]];
+    const int64_t u = E.node(idx[p]);
     bad = u < 0 || u >= N;
     nkey[p] = bad ? 0xffffffffu : static_cast<uint32_t>(u);
   }
@@ -73,8 +102,8 @@ __global__ __launch_bounds__(kThreads) void csr_offsets(const uint32_t* __restri
 // out[p] = entry perm[p]: id, time, edge id, feature row (tpe lanes per row)
 template <int VEC>
 __global__ __launch_bounds__(kThreads) void csr_gather(
-    const uint32_t* __restrict__ perm, int64_t n, const int64_t* __restrict__ to,
-    const double* __restrict__ time, const int64_t* __restrict__ event, int64_t num_events,
+    const uint32_t* __restrict__ perm, int64_t n, Entries E,
+    const double* __restrict__ time, int64_t num_events,
     const uint8_t* __restrict__ feats, int64_t row_bytes, int tpe_log2,
     int32_t* __restrict__ out_ids, double* __restrict__ out_times, int64_t* __restrict__ out_eids,
     uint8_t* __restrict__ out_feats, int32_t* __restrict__ status) {
@@ -85,10 +114,10 @@ __global__ __launch_bounds__(kThreads) void csr_gather(
   bool bad = false;
   if (p < n) {
     const int64_t j = perm[p];
-    const int64_t ev = event != nullptr ? event[j] : -1;
+    const int64_t ev = E.ev(j);
     if (l == 0) {
-      out_ids[p] = static_cast<int32_t>(to[j]);
-      out_times[p] = time[j];
+      out_ids[p] = static_cast<int32_t>(E.nbr(j));
+      out_times[p] = time[E.row(j)];
       if (out_eids != nullptr) out_eids[p] = ev;
     }
     if (out_feats != nullptr && row_bytes > 0) {
@@ -146,13 +175,18 @@ extern "C" int tgx_csr_build(const tgx_csr_build_args* a, void* stream_) {
   if (esz == 0) return fail(TGX_ERR_DTYPE, "tgx_csr_build: unsupported feat dtype %d", a->feat_dtype);
   if (a->out_offsets == nullptr) return fail(TGX_ERR_ARG, "tgx_csr_build: out_offsets is NULL");
   const int64_t row_bytes = static_cast<int64_t>(a->feat_dim) * esz;
+  if ((a->flags & ~TGX_CSR_EVENT_PAIRS) != 0)
+    return fail(TGX_ERR_ARG, "tgx_csr_build: unknown flags 0x%x", a->flags);
+  const int pairs = (a->flags & TGX_CSR_EVENT_PAIRS) != 0;
+  if (pairs && n % 2 != 0)
+    return fail(TGX_ERR_ARG, "tgx_csr_build: event pairs need an even entry count, got %lld", (long long)n);
   if (n > 0) {
     if (a->from == nullptr || a->to == nullptr || a->time == nullptr || a->out_ids == nullptr ||
         a->out_times == nullptr)
       return fail(TGX_ERR_ARG, "tgx_csr_build: from/to/time/out_ids/out_times must not be NULL");
     if (row_bytes > 0 && a->out_feats == nullptr)
       return fail(TGX_ERR_ARG, "tgx_csr_build: out_feats is NULL with feat_dim > 0");
-    if ((a->feats != nullptr || a->out_eids != nullptr) && a->event == nullptr)
+    if ((a->feats != nullptr || a->out_eids != nullptr) && a->event == nullptr && !pairs)
       return fail(TGX_ERR_ARG, "tgx_csr_build: feats / out_eids need the event index array");
     if (a->feats != nullptr && a->num_events < 0)
       return fail(TGX_ERR_ARG, "tgx_csr_build: negative num_events");
@@ -176,15 +210,22 @@ extern "C" int tgx_csr_build(const tgx_csr_build_args* a, void* stream_) {
                      reinterpret_cast<uint32_t*>(ws + w.idx + align256(un * 4))};
   uint32_t* nk[2] = {reinterpret_cast<uint32_t*>(ws + w.nkey),
                      reinterpret_cast<uint32_t*>(ws + w.nkey + align256(un * 4))};
-  hipLaunchKernelGGL(csr_init, dim3(g1), dim3(kThreads), 0, stream, a->time, n, tk[0], ix[0]);
-  if ((rc = check_launch("csr_init"))) return rc;
   uint32_t* count = reinterpret_cast<uint32_t*>(ws + w.count);
   uint32_t* sums = reinterpret_cast<uint32_t*>(ws + w.sums);
-  // stable by time: 8 passes, ping-pong ending in buffer 0
+  const Entries E{a->from, a->to, a->event, pairs};
   int cur = 0;
-  if ((rc = radix_sort<uint64_t>(tk, ix, cur, n, 64, w.r, count, sums, stream))) return rc;
+  if (pairs) {
+    // already in stable time order
+    hipLaunchKernelGGL(csr_identity, dim3(g1), dim3(kThreads), 0, stream, n, ix[0]);
+    if ((rc = check_launch("csr_identity"))) return rc;
+  } else {
+    hipLaunchKernelGGL(csr_init, dim3(g1), dim3(kThreads), 0, stream, a->time, n, tk[0], ix[0]);
+    if ((rc = check_launch("csr_init"))) return rc;
+    // stable by time: 8 passes, ping-pong ending in buffer 0
+    if ((rc = radix_sort<uint64_t>(tk, ix, cur, n, 64, w.r, count, sums, stream))) return rc;
+  }
   // then stable by node over ceil(log2 N) bits (out-of-range ids sort last)
-  hipLaunchKernelGGL(csr_node_keys, dim3(g1), dim3(kThreads), 0, stream, a->from,
+  hipLaunchKernelGGL(csr_node_keys, dim3(g1), dim3(kThreads), 0, stream, E,
                      static_cast<const uint32_t*>(ix[cur]), n, N, nk[0], a->status);
   if ((rc = check_launch("csr_node_keys"))) return rc;
   int bits = 1;
@@ -211,7 +252,7 @@ extern "C" int tgx_csr_build(const tgx_csr_build_args* a, void* stream_) {
   const dim3 gg(static_cast<unsigned>(cdiv(n << tpe_log2, kThreads)));
   auto gather = [&](auto kernel) {
     hipLaunchKernelGGL(kernel, gg, dim3(kThreads), 0, stream, static_cast<const uint32_t*>(perm_in), n,
-                       a->to, a->time, a->event, a->num_events,
+                       E, a->time, a->num_events,
                        static_cast<const uint8_t*>(a->feats), fe ? row_bytes : 0, tpe_log2, a->out_ids,
                        a->out_times, a->out_eids, static_cast<uint8_t*>(fe ? a->out_feats : nullptr),
                        a->status);

@@ -198,6 +198,9 @@ constexpr int64_t kSplitBytes = 8192;
 // the device's wave slots: 600 queries ran faster at 4 waves each than at 8)
 constexpr int64_t kSplitMaxWaves = 4096;
 
+// compute units of one MI355X (the LDS residency bound of the split rule)
+constexpr int64_t kDeviceCUs = 256;
+
 // row chunks each lane loads before storing them (large-row copy)
 constexpr int kCopyDepth = 4;
 
@@ -1123,12 +1126,27 @@ int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args
   // with a CSR window takes about 24 KB per wave)
   const int lds_waves = static_cast<int>((160 * 1024 - P.te_bytes) / P.wave_bytes);
   const int wave_cap = lds_waves < kMaxWaves ? lds_waves : kMaxWaves;
+  // A launch whose workgroups all fit on the device at once at one wave per
+  // query, with the LDS bounding the workgroups per CU (a large K), splits only
+  // while they still do: a split that leaves workgroups for a second round is
+  // slower than fewer waves per query (LastFM's shape, 600 queries at K = 512:
+  // 4 waves each made one 91 KB workgroup per CU and three rounds)
+  auto fits = [&](int sp) {
+    const int64_t wg_bytes = static_cast<int64_t>(P.te_bytes) + static_cast<int64_t>(qwant) * sp * P.wave_bytes;
+    const int64_t per_cu = (160 * 1024) / wg_bytes;
+    const int64_t groups = mode == TGX_PLAN_TILES ? a->num_queries : (a->num_queries + qwant - 1) / qwant;
+    return per_cu >= kMaxWaves || groups <= kDeviceCUs * per_cu;
+  };
+  const bool one_round = fits(1);
+  auto resident = [&](int sp) { return !one_round || fits(sp); };
   int split = 1;
   if (P.m == 1) {
-    while (split < 8 && a->num_queries * (split * 2) <= kSplitMaxWaves && qwant * split * 2 <= wave_cap)
+    while (split < 8 && a->num_queries * (split * 2) <= kSplitMaxWaves && qwant * split * 2 <= wave_cap &&
+           resident(split * 2))
       split *= 2;
     const int64_t qbytes = static_cast<int64_t>(K) * (P.row_bytes + 4 * a->d_t + 13);
-    while (split < 8 && qbytes / (split * 2) >= kSplitBytes && qwant * split * 2 <= wave_cap)
+    while (split < 8 && qbytes / (split * 2) >= kSplitBytes && qwant * split * 2 <= wave_cap &&
+           resident(split * 2))
       split *= 2;
   }
   const int lg_split = split == 1 ? 0 : split == 2 ? 1 : split == 4 ? 2 : 3;  // split is 1, 2, 4 or 8

@@ -25,7 +25,7 @@ from typing import Optional
 
 import numpy as np
 
-__all__ = ["StreamConfig", "CONFIGS", "gen_batch", "num_batches", "f32_to_bf16_bits",
+__all__ = ["StreamConfig", "CONFIGS", "ENGINE_SHAPES", "gen_batch", "num_batches", "f32_to_bf16_bits",
            "bf16_bits_to_f32", "make_graph", "make_pipeline", "to_raw"]
 
 
@@ -90,6 +90,22 @@ CONFIGS = {
                        "zipf", src_a=1.3, dst_a=1.3, feat_dim=172, feat_dtype="f32",
                        buffer_size=32, batch=8192, k=32, co_occurrence=True, time_law="bursty",
                        seed=1005),
+}
+
+
+# The shapes of the reference's published pipeline timings (Engine on a frozen CSR,
+# batch 200, docs/performance_report.md:29-31): node and event counts, bipartite
+# id ranges, K and edge-feature width of Wikipedia, Reddit and LastFM, as
+# synthetic streams (the datasets themselves are not available here)
+ENGINE_SHAPES = {
+    "wikipedia": StreamConfig("wikipedia", 9228, 157_474, (0, 8228), (8228, 9228), "uniform", "zipf",
+                              dst_a=1.1, feat_dim=172, feat_dtype="f32", batch=200, k=32, seed=2001),
+    "reddit": StreamConfig("reddit", 10985, 672_447, (0, 10000), (10000, 10985), "zipf", "zipf",
+                           src_a=1.1, dst_a=1.1, feat_dim=172, feat_dtype="f32", batch=200, k=64,
+                           seed=2002),
+    "lastfm": StreamConfig("lastfm", 1981, 1_293_103, (0, 980), (980, 1981), "zipf", "zipf",
+                           src_a=0.8, dst_a=1.0, feat_dim=2, feat_dtype="f32", batch=200, k=512,
+                           seed=2003),
 }
 
 
