@@ -330,6 +330,26 @@ int tgx_negpool_sample(const int32_t* pool, const int64_t* count, int64_t num_no
                        int32_t pool_size, const int64_t* src, int64_t n, uint64_t seed,
                        uint64_t call, int64_t* out, int32_t* status, void* stream);
 
+/* The same two operations with the caller's random draws, indexed as the
+ * reference indexes its torch.rand / torch.randint draws
+ * (pipeline/negatives.py:78-86, :116-124), so that draws taken from torch's
+ * generator in the reference's call order give the reference's pool and
+ * samples.  update: u_accept[p] (float32 in [0, 1)) and slot_draw[p] (in
+ * [0, pool_size); other values skip the edge) of the edge at position p of
+ * the batch's stable sort by source; sample: u_slot[q] (float32 in [0, 1)) of
+ * query q, and out[q] = -1 for a node without history (the reference then
+ * draws those nodes with torch.randint(0, num_nodes, (#such queries,)) in
+ * query order; the caller does that).  The later edge of a batch still wins a
+ * slot two accepted edges take, where the reference leaves it to the last
+ * index_put_ write. */
+int tgx_negpool_update_draws(int32_t* pool, int64_t* count, int64_t num_nodes, int32_t pool_size,
+                             const int64_t* src, const int64_t* dst, int64_t n,
+                             const float* u_accept, const int64_t* slot_draw, void* workspace,
+                             size_t workspace_bytes, int32_t* status, void* stream);
+int tgx_negpool_sample_draws(const int32_t* pool, const int64_t* count, int64_t num_nodes,
+                             int32_t pool_size, const int64_t* src, int64_t n, const float* u_slot,
+                             int64_t* out, int32_t* status, void* stream);
+
 /* Fused most-recent-K gather (+ time encoding, + co-occurrence) (kernels b, c).
  * ring and/or csr may be NULL (no candidates from that store); with both NULL
  * every query is padding and out_feats must be NULL (the row width comes from

@@ -534,3 +534,48 @@ def negpool_sample(pool: np.ndarray, count: np.ndarray, src, seed: int, call: in
         else:
             out[q] = rand64(seed, call, q, 3) % N
     return out
+
+
+def negpool_update_draws(pool: np.ndarray, count: np.ndarray, src, dst, u_accept, slot_draw) -> None:
+    """negatives.py:45-103 with the draws given as the reference takes them:
+    ``u_accept`` (torch.rand(n)) and ``slot_draw`` (torch.randint(0, P, (n,)))
+    indexed by the edge's position in the stable argsort of src.  Position p,
+    the r-th edge of its source u, is u's e-th edge, e = count[u] + r + 1: e <= P
+    fills slot e - 1; otherwise u_accept[p] < f32(P) / f32(e) replaces slot
+    slot_draw[p].  The accepted edges are written in sorted order (a later write
+    of one (u, slot) wins), and count[u] grows by u's edges."""
+    N, P = pool.shape
+    src = np.asarray(src, np.int64)
+    dst = np.asarray(dst, np.int64)
+    n = len(src)
+    if n == 0:
+        return
+    order = np.argsort(src, kind="stable")
+    su, sd = src[order], dst[order]
+    start = np.searchsorted(su, su, side="left")
+    r = np.arange(n) - start
+    e = count[su] + r + 1
+    fill = e <= P
+    ua = np.asarray(u_accept, np.float32)
+    replace = ~fill & (ua < np.float32(P) / e.astype(np.float32))
+    slot = np.where(fill, np.minimum(e - 1, P - 1), np.asarray(slot_draw, np.int64))
+    acc = fill | replace
+    for p in np.nonzero(acc)[0]:  # in sorted order: the later write stays
+        pool[su[p], slot[p]] = np.int32(sd[p])
+    np.add.at(count, su, 1)
+
+
+def negpool_sample_draws(pool: np.ndarray, count: np.ndarray, src, u_slot) -> np.ndarray:
+    """negatives.py:105-126 with torch.rand(B) given as ``u_slot``: among the
+    valid (non-padding) slots of the source's pool row, slot int(f32(U) *
+    f32(valid)) clamped to P - 1; -1 where the row holds no valid slot (the
+    reference fills those with torch.randint(0, N, (k,)) in query order)."""
+    N, P = pool.shape
+    src = np.asarray(src, np.int64)
+    rows = pool[src]
+    valid = (rows != -1).sum(1)
+    idx = (np.asarray(u_slot, np.float32) * valid.astype(np.float32)).astype(np.int64)
+    idx = np.minimum(idx, P - 1)
+    out = rows[np.arange(len(src)), idx].astype(np.int64)
+    out[valid == 0] = -1
+    return out

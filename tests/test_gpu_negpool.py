@@ -101,3 +101,45 @@ def test_historical_negative_strategy():
     strat.update(src, src + 50)
     neg = strat.sample(src, src + 50, None, None)
     assert torch.equal(neg, src + 50)  # one edge each: the only pool entry
+
+
+@pytest.mark.parametrize("P,n", [(16, 300), (4, 5000), (8, 9000)])
+def test_torch_rng_mode_reproduces_the_reference_draws(P, n):
+    """rng="torch": the pool draws from torch's generator in the reference's call
+    order and shapes (negatives.py:78-86, 116-124), so replaying the generator
+    state into the oracle's draw-given restatement gives the same pool, counts
+    and samples, and leaves the generator where the pool left it.  Batches on
+    both sides of the single-workgroup update sizes; hot sources go past the
+    fill phase."""
+    rng = np.random.default_rng(40 + P)
+    N = 500
+    torch.manual_seed(1234)
+    pool = HistoricalNegPool(N, P, device="cuda", rng="torch")
+    cp = np.full((N, P), -1, np.int32)
+    cc = np.zeros(N, np.int64)
+    for step in range(6):
+        src = rng.integers(0, N, n)
+        src[: n // 4] = 7
+        dst = rng.integers(0, N, n)
+        state = torch.cuda.get_rng_state()
+        pool.update(torch.from_numpy(src).cuda(), torch.from_numpy(dst).cuda())
+        after = torch.cuda.get_rng_state()
+        torch.cuda.set_rng_state(state)
+        ua = torch.rand(n, device="cuda").cpu().numpy()
+        sd = torch.randint(0, P, (n,), device="cuda").cpu().numpy()
+        assert torch.equal(torch.cuda.get_rng_state(), after)
+        O.negpool_update_draws(cp, cc, src, dst, ua, sd)
+        assert np.array_equal(pool._pool.cpu().numpy(), cp), step
+        assert np.array_equal(pool._count.cpu().numpy(), cc), step
+        q = np.concatenate([rng.integers(0, N, 200), [N - 1, N - 2]])  # and nodes without history
+        state = torch.cuda.get_rng_state()
+        got = pool.sample(torch.from_numpy(q).cuda()).cpu().numpy()
+        after = torch.cuda.get_rng_state()
+        torch.cuda.set_rng_state(state)
+        want = O.negpool_sample_draws(cp, cc, q, torch.rand(len(q), device="cuda").cpu().numpy())
+        none = want < 0
+        if none.any():
+            want[none] = torch.randint(0, N, (int(none.sum()),), device="cuda").cpu().numpy()
+        assert torch.equal(torch.cuda.get_rng_state(), after)
+        assert np.array_equal(got, want), step
+    assert cc[7] > P

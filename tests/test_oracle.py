@@ -415,3 +415,49 @@ def test_negpool_sample_is_uniform_over_valid_slots_and_falls_back():
     assert np.abs(freq / 5000 - 0.2).max() < 0.03
     fb = O.negpool_sample(pool, cnt, np.array([7, 7, 60, -1]), 9, 1)  # no history / out of range
     assert ((fb >= 0) & (fb < N)).all()
+
+
+def test_negpool_draws_restatement_matches_the_counter_update():
+    """negpool_update_draws (the reference's tensor formulation with its draws
+    indexed by sorted position) equals the edge-by-edge update when handed the
+    same draws, moved from batch order to sorted order; hot sources cross the
+    fill/replace boundary and collide on slots."""
+    rng = np.random.default_rng(5)
+    N, P = 30, 4
+    a = np.full((N, P), -1, np.int32)
+    b = a.copy()
+    ca = np.zeros(N, np.int64)
+    cb = ca.copy()
+    for call in range(15):
+        n = int(rng.integers(1, 80))
+        src = rng.integers(0, N, n)
+        src[: n // 3] = 2
+        dst = rng.integers(0, 1000, n)
+        order = np.argsort(src, kind="stable")
+        ua = np.array([O.uniform01(O.rand64(77, call, int(j), 0)) for j in order], np.float32)
+        sd = np.array([O.rand64(77, call, int(j), 1) % P for j in order], np.int64)
+        O.negpool_update(a, ca, src, dst, 77, call)
+        O.negpool_update_draws(b, cb, src, dst, ua, sd)
+        assert np.array_equal(a, b) and np.array_equal(ca, cb), call
+        q = rng.integers(0, N, 50)
+        us = np.array([O.uniform01(O.rand64(77, call, i, 2)) for i in range(50)], np.float32)
+        want = O.negpool_sample(a, ca, q, 77, call)
+        got = O.negpool_sample_draws(b, cb, q, us)
+        hist = cb[q] > 0
+        assert np.array_equal(got[hist], want[hist]) and (got[~hist] == -1).all()
+    assert ca[2] > P
+
+
+def test_negpool_draws_known_answers():
+    """P = 2, one source, three edges in one batch: fill slots 0 and 1, then the
+    third (e = 3) replaces slot_draw when u < f32(2) / f32(3) = 0.6666667."""
+    for u, want in ((np.float32(0.66666657), [10, 12]), (np.float32(0.6666667), [10, 11]),
+                    (np.float32(0.9), [10, 11])):
+        pool = np.full((1, 2), -1, np.int32)
+        cnt = np.zeros(1, np.int64)
+        O.negpool_update_draws(pool, cnt, [0, 0, 0], [10, 11, 12], np.float32([0.0, 0.0, u]), [0, 0, 1])
+        assert list(pool[0]) == want and cnt[0] == 3
+    # sample: the 2 valid slots, int(u * 2); a row without history gives -1
+    pool = np.array([[10, 11], [-1, -1]], np.int32)
+    got = O.negpool_sample_draws(pool, np.array([2, 0]), [0, 0, 1], np.float32([0.49, 0.5, 0.3]))
+    assert list(got) == [10, 11, -1]

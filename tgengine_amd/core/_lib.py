@@ -113,6 +113,10 @@ SIGNATURES = {
                                    ctypes.c_uint64, c_vp, ctypes.c_size_t, c_vp, c_vp]),
     "tgx_negpool_sample": (c_i32, [c_vp, c_vp, c_i64, c_i32, c_vp, c_i64, ctypes.c_uint64,
                                    ctypes.c_uint64, c_vp, c_vp, c_vp]),
+    "tgx_negpool_update_draws": (c_i32, [c_vp, c_vp, c_i64, c_i32, c_vp, c_vp, c_i64, c_vp, c_vp,
+                                         c_vp, ctypes.c_size_t, c_vp, c_vp]),
+    "tgx_negpool_sample_draws": (c_i32, [c_vp, c_vp, c_i64, c_i32, c_vp, c_i64, c_vp, c_vp, c_vp,
+                                         c_vp]),
     "tgx_last_error": (ctypes.c_char_p, []),
     "tgx_abi_version": (c_i32, []),
 }

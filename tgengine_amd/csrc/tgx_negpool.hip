@@ -27,6 +27,16 @@
 // ^ (4 i + stream)) with mix the splitmix64 finalizer and G its golden-ratio
 // increment; U = (rand64 >> 40) * 2^-24.  Streams: 0 accept, 1 replacement
 // slot (update); 2 slot, 3 fallback node (sample).
+//
+// Caller draws (tgx_negpool_update_draws / tgx_negpool_sample_draws): the
+// uniforms and replacement slots come from the caller, indexed as the
+// reference indexes its torch.rand / torch.randint draws -- by the edge's
+// position in the stable sort of the batch by source (update), by query
+// (sample) -- so a caller drawing them from torch's generator in the
+// reference's order reproduces its pool and samples.  The update then takes
+// the sort-based path (positions by node id); a sample of a source without
+// history is left to the caller (-1), which draws its node afterwards as the
+// reference does.
 #include "tgx_radix.h"
 
 #include <mutex>
@@ -86,6 +96,8 @@ __global__ __launch_bounds__(kThreads) void np_decide(const uint32_t* __restrict
                                                       const uint32_t* __restrict__ sidx, int64_t n,
                                                       const int64_t* __restrict__ count, int P,
                                                       uint64_t seed, uint64_t call,
+                                                      const float* __restrict__ u_accept,
+                                                      const int64_t* __restrict__ slot_draw,
                                                       uint64_t* __restrict__ ckey,
                                                       uint32_t* __restrict__ cval) {
   const int64_t p = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
@@ -99,6 +111,12 @@ __global__ __launch_bounds__(kThreads) void np_decide(const uint32_t* __restrict
     int64_t slot = -1;
     if (e <= P) {
       slot = e - 1;
+    } else if (u_accept != nullptr) {
+      // the caller's draws of sorted position p; a slot outside [0, P) is skipped
+      if (u_accept[p] < static_cast<float>(P) / static_cast<float>(e)) {
+        slot = slot_draw[p];
+        if (slot < 0 || slot >= P) slot = -1;
+      }
     } else if (uniform01(rand64(seed, call, j, 0)) < static_cast<float>(P) / static_cast<float>(e)) {
       slot = static_cast<int64_t>(rand64(seed, call, j, 1) % static_cast<uint64_t>(P));
     }
@@ -133,6 +151,7 @@ __global__ __launch_bounds__(kThreads) void np_sample(const int32_t* __restrict_
                                                       const int64_t* __restrict__ count, int64_t N, int P,
                                                       const int64_t* __restrict__ src, int64_t n,
                                                       uint64_t seed, uint64_t call,
+                                                      const float* __restrict__ u_slot,
                                                       int64_t* __restrict__ out,
                                                       int32_t* __restrict__ status) {
   const int64_t q = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
@@ -143,11 +162,12 @@ __global__ __launch_bounds__(kThreads) void np_sample(const int32_t* __restrict_
     const int64_t c = bad ? 0 : count[u];
     const int64_t v = c < P ? c : P;
     if (v > 0) {
-      int64_t s = static_cast<int64_t>(uniform01(rand64(seed, call, q, 2)) * static_cast<float>(v));
+      const float U = u_slot != nullptr ? u_slot[q] : uniform01(rand64(seed, call, q, 2));
+      int64_t s = static_cast<int64_t>(U * static_cast<float>(v));
       if (s > P - 1) s = P - 1;
       out[q] = pool[u * P + s];
     } else {
-      out[q] = static_cast<int64_t>(rand64(seed, call, q, 3) % static_cast<uint64_t>(N));
+      out[q] = u_slot != nullptr ? -1 : static_cast<int64_t>(rand64(seed, call, q, 3) % static_cast<uint64_t>(N));
     }
   }
   const uint64_t bm = __ballot(bad);
@@ -484,22 +504,26 @@ extern "C" size_t tgx_negpool_update_workspace_size(int64_t n) {
   return np_layout(n).total;
 }
 
-extern "C" int tgx_negpool_update(int32_t* pool, int64_t* count, int64_t num_nodes, int32_t pool_size,
-                                  const int64_t* src, const int64_t* dst, int64_t n, uint64_t seed,
-                                  uint64_t call, void* workspace, size_t workspace_bytes,
-                                  int32_t* status, void* stream_) {
-  hipStream_t stream = static_cast<hipStream_t>(stream_);
-  int rc = check_pool("tgx_negpool_update", pool, count, num_nodes, pool_size);
+namespace tgx {
+namespace {
+
+int negpool_update(const char* who, int32_t* pool, int64_t* count, int64_t num_nodes, int32_t pool_size,
+                   const int64_t* src, const int64_t* dst, int64_t n, uint64_t seed, uint64_t call,
+                   const float* u_accept, const int64_t* slot_draw, void* workspace,
+                   size_t workspace_bytes, int32_t* status, hipStream_t stream) {
+  int rc = check_pool(who, pool, count, num_nodes, pool_size);
   if (rc) return rc;
   if (n < 0 || n >= (int64_t(1) << 31))
-    return fail(TGX_ERR_LIMIT, "tgx_negpool_update: %lld edges outside [0, 2^31)", (long long)n);
+    return fail(TGX_ERR_LIMIT, "%s: %lld edges outside [0, 2^31)", who, (long long)n);
   if (n == 0) return TGX_OK;
-  if (src == nullptr || dst == nullptr) return fail(TGX_ERR_ARG, "tgx_negpool_update: src/dst must not be NULL");
+  if (src == nullptr || dst == nullptr) return fail(TGX_ERR_ARG, "%s: src/dst must not be NULL", who);
+  const bool draws = u_accept != nullptr || slot_draw != nullptr;
+  if (draws && (u_accept == nullptr || slot_draw == nullptr))
+    return fail(TGX_ERR_ARG, "%s: u_accept and slot_draw come together", who);
   const NpLayout w = np_layout(n);
   if (workspace == nullptr || workspace_bytes < w.total)
-    return fail(TGX_ERR_ARG, "tgx_negpool_update: workspace of %zu bytes needed, got %zu", w.total,
-                workspace_bytes);
-  if (n <= 8192) {
+    return fail(TGX_ERR_ARG, "%s: workspace of %zu bytes needed, got %zu", who, w.total, workspace_bytes);
+  if (n <= 8192 && !draws) {
     // one workgroup: the 4,096-edge shape, or the 8,192-edge one (three digit passes)
     static std::once_flag attr_once;
     std::call_once(attr_once, [] {
@@ -536,7 +560,7 @@ extern "C" int tgx_negpool_update(int32_t* pool, int64_t* count, int64_t num_nod
     return rc;
   hipLaunchKernelGGL(np_decide, g1, dim3(kThreads), 0, stream, static_cast<const uint32_t*>(key[cur]),
                      static_cast<const uint32_t*>(idx[cur]), n, static_cast<const int64_t*>(count),
-                     static_cast<int>(pool_size), seed, call, ck[0], cv[0]);
+                     static_cast<int>(pool_size), seed, call, u_accept, slot_draw, ck[0], cv[0]);
   if ((rc = check_launch("np_decide"))) return rc;
   int ccur = 0;
   const uint64_t cells = static_cast<uint64_t>(num_nodes) * static_cast<uint64_t>(pool_size);
@@ -549,16 +573,53 @@ extern "C" int tgx_negpool_update(int32_t* pool, int64_t* count, int64_t num_nod
   return check_launch("np_count");
 }
 
+int negpool_sample(const char* who, const int32_t* pool, const int64_t* count, int64_t num_nodes,
+                   int32_t pool_size, const int64_t* src, int64_t n, uint64_t seed, uint64_t call,
+                   const float* u_slot, int64_t* out, int32_t* status, hipStream_t stream) {
+  int rc = check_pool(who, pool, count, num_nodes, pool_size);
+  if (rc) return rc;
+  if (n < 0) return fail(TGX_ERR_ARG, "%s: negative size", who);
+  if (n == 0) return TGX_OK;
+  if (src == nullptr || out == nullptr) return fail(TGX_ERR_ARG, "%s: src/out must not be NULL", who);
+  hipLaunchKernelGGL(np_sample, dim3(static_cast<unsigned>(cdiv(n, kThreads))), dim3(kThreads), 0, stream,
+                     pool, count, num_nodes, static_cast<int>(pool_size), src, n, seed, call, u_slot, out,
+                     status);
+  return check_launch("np_sample");
+}
+
+}  // namespace
+}  // namespace tgx
+
+extern "C" int tgx_negpool_update(int32_t* pool, int64_t* count, int64_t num_nodes, int32_t pool_size,
+                                  const int64_t* src, const int64_t* dst, int64_t n, uint64_t seed,
+                                  uint64_t call, void* workspace, size_t workspace_bytes,
+                                  int32_t* status, void* stream) {
+  return negpool_update("tgx_negpool_update", pool, count, num_nodes, pool_size, src, dst, n, seed, call,
+                        nullptr, nullptr, workspace, workspace_bytes, status, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int tgx_negpool_update_draws(int32_t* pool, int64_t* count, int64_t num_nodes, int32_t pool_size,
+                                        const int64_t* src, const int64_t* dst, int64_t n,
+                                        const float* u_accept, const int64_t* slot_draw, void* workspace,
+                                        size_t workspace_bytes, int32_t* status, void* stream) {
+  if (n > 0 && (u_accept == nullptr || slot_draw == nullptr))
+    return fail(TGX_ERR_ARG, "tgx_negpool_update_draws: u_accept/slot_draw must not be NULL");
+  return negpool_update("tgx_negpool_update_draws", pool, count, num_nodes, pool_size, src, dst, n, 0, 0,
+                        u_accept, slot_draw, workspace, workspace_bytes, status,
+                        static_cast<hipStream_t>(stream));
+}
+
 extern "C" int tgx_negpool_sample(const int32_t* pool, const int64_t* count, int64_t num_nodes,
                                   int32_t pool_size, const int64_t* src, int64_t n, uint64_t seed,
-                                  uint64_t call, int64_t* out, int32_t* status, void* stream_) {
-  int rc = check_pool("tgx_negpool_sample", pool, count, num_nodes, pool_size);
-  if (rc) return rc;
-  if (n < 0) return fail(TGX_ERR_ARG, "tgx_negpool_sample: negative size");
-  if (n == 0) return TGX_OK;
-  if (src == nullptr || out == nullptr) return fail(TGX_ERR_ARG, "tgx_negpool_sample: src/out must not be NULL");
-  hipLaunchKernelGGL(np_sample, dim3(static_cast<unsigned>(cdiv(n, kThreads))), dim3(kThreads), 0,
-                     static_cast<hipStream_t>(stream_), pool, count, num_nodes, static_cast<int>(pool_size),
-                     src, n, seed, call, out, status);
-  return check_launch("np_sample");
+                                  uint64_t call, int64_t* out, int32_t* status, void* stream) {
+  return negpool_sample("tgx_negpool_sample", pool, count, num_nodes, pool_size, src, n, seed, call, nullptr,
+                        out, status, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int tgx_negpool_sample_draws(const int32_t* pool, const int64_t* count, int64_t num_nodes,
+                                        int32_t pool_size, const int64_t* src, int64_t n, const float* u_slot,
+                                        int64_t* out, int32_t* status, void* stream) {
+  if (n > 0 && u_slot == nullptr) return fail(TGX_ERR_ARG, "tgx_negpool_sample_draws: u_slot must not be NULL");
+  return negpool_sample("tgx_negpool_sample_draws", pool, count, num_nodes, pool_size, src, n, 0, 0, u_slot,
+                        out, status, static_cast<hipStream_t>(stream));
 }
