@@ -474,7 +474,11 @@ constexpr int kWavesPerEu = NREG > 0 ? 1 : 8;
 // TILES: the launch's plan mode is TGX_PLAN_TILES (no event or list plan, so no
 // co-occurrence); that copy of the kernel carries none of their code, which
 // shortens its start-up
-template <int VEC, int NREG, bool TILES>
+// NORING: a tiled launch without a ring (a frozen CSR before any post-freeze
+// advance, as the Engine prepares): the ring code is compiled out, and the CSR
+// window, which is then the answer in order, is emitted straight from memory
+// without staging its candidates in LDS (a large K's waves stay small)
+template <int VEC, int NREG, bool TILES, bool NORING = false>
 __global__ __launch_bounds__(kMaxWaves * kWave) __attribute__((amdgpu_waves_per_eu(kWavesPerEu<NREG>)))
 void recent_fused(Params P) {
   using VT = typename Vec<VEC>::T;
@@ -488,7 +492,7 @@ void recent_fused(Params P) {
   }
   const int64_t g = static_cast<int64_t>(blockIdx.x) - P.plan_blocks;
   const int K = P.K;
-  const int B = P.B;
+  const int B = NORING ? 0 : P.B;
   const int C = P.cand_cap;
   const int m = P.m;
   const int lg = P.lg_bp;
@@ -584,10 +588,14 @@ void recent_fused(Params P) {
         }
       }
     }
-    for (int j = sl; j < ncsr; j += Bp) {
-      ct[h * C + j] = P.c_times[cbase + j];
-      cid[h * C + j] = P.c_ids[cbase + j];
-      ccode[h * C + j] = B + j;
+    // with a ring the candidates are ranked from LDS; without one (B == 0) the
+    // CSR window is the answer in order and is emitted from memory below
+    if (!NORING) {
+      for (int j = sl; j < ncsr; j += Bp) {
+        ct[h * C + j] = P.c_times[cbase + j];
+        cid[h * C + j] = P.c_ids[cbase + j];
+        ccode[h * C + j] = B + j;
+      }
     }
   }
   const bool v = live && sl < B && rid != -1 && rt < qt;
@@ -641,7 +649,10 @@ void recent_fused(Params P) {
   }
   wave_sync();
   if (q >= 0) {
-    if (!fast) {
+    if (NORING) {
+      // no ring: the ncsr <= K CSR entries, time-ascending, are the last positions
+      for (int j = sl; j < ncsr; j += Bp) emit(K - ncsr + j, P.c_ids[cbase + j], P.c_times[cbase + j], j);
+    } else if (!fast) {
       // counting rank by (time, CSR-before-ring, candidate index).  The CSR
       // window is time-ascending with ties in CSR order, so CSR entry c has
       // exactly c such predecessors among the CSR entries and only the ring
@@ -890,6 +901,7 @@ struct Launch {
   int qslots = 0;
   int vec = 2;
   int nreg = 0;
+  bool noring = false;
 };
 
 // |dt| below which every encoding argument fl32(fl32(dt w) + b) stays below
@@ -1086,9 +1098,13 @@ int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args
   P.status = a->status;
 
   const int K = a->k;
-  P.cand_cap = (P.has_csr ? K : 0) + P.B;
+  // LDS candidates: the CSR window and the ring slots; a tiled launch without a
+  // ring (the NORING copies) emits the window straight from memory instead
+  L.noring = ring == nullptr && mode == TGX_PLAN_TILES;
+  P.cand_cap = L.noring ? 0 : (P.has_csr ? K : 0) + P.B;
   auto wave_lds = [&](int m) {
-    return round16(m * P.cand_cap * 16) + round16(m * K * 4) * 3 + round16(m * K * 8) * 2 + round16(m * 24);
+    return round16(m * P.cand_cap * 16) + round16(m * K * 4) * 3 + round16(m * K * 8) *
+           (a->out_eids != nullptr ? 2 : 1) + round16(m * 24);
   };
   // Queries per wave.  Packing m = 64 / Bp queries into sub-groups of Bp >= B
   // lanes (Bp at least 16, the wave's LDS within 12 KB) pays off only when the
@@ -1113,7 +1129,7 @@ int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args
   P.off_pid = P.off_pdt + round16(P.m * K * 4);
   P.off_pt = P.off_pid + round16(P.m * K * 4);
   P.off_pe = P.off_pt + round16(P.m * K * 8);
-  P.off_tab = P.off_pe + round16(P.m * K * 8);
+  P.off_tab = P.off_pe + (a->out_eids != nullptr ? round16(P.m * K * 8) : 0);  // edge ids only when asked
   P.wave_bytes = P.off_tab + round16(P.m * 24);
   // split: with one query per wave, up to 8 waves share each query's outputs while
   // the launch stays within kSplitMaxWaves waves; and up to 8 while each wave's share of a
@@ -1231,7 +1247,10 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
                          reinterpret_cast<const void*>(recent_fused<16, 2, true>),
                          reinterpret_cast<const void*>(recent_fused<16, 4, true>),
                          reinterpret_cast<const void*>(recent_fused<4, 0, true>),
-                         reinterpret_cast<const void*>(recent_fused<2, 0, true>)};
+                         reinterpret_cast<const void*>(recent_fused<2, 0, true>),
+                         reinterpret_cast<const void*>(recent_fused<16, 0, true, true>),
+                         reinterpret_cast<const void*>(recent_fused<4, 0, true, true>),
+                         reinterpret_cast<const void*>(recent_fused<2, 0, true, true>)};
     for (const void* f : fns)
       (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     (void)hipGetLastError();
@@ -1252,7 +1271,14 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
     else
       launch(k_other);
   };
-  if (L.vec == 16) {
+  if (L.noring) {
+    if (L.vec == 16)
+      launch(recent_fused<16, 0, true, true>);
+    else if (L.vec == 4)
+      launch(recent_fused<4, 0, true, true>);
+    else
+      launch(recent_fused<2, 0, true, true>);
+  } else if (L.vec == 16) {
     if (L.nreg == 2)
       pick(recent_fused<16, 2, true>, recent_fused<16, 2, false>);
     else if (L.nreg == 4)
