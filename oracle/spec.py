@@ -209,6 +209,9 @@ def recent(nodes, qtimes, K: int, csr: Optional[CSR], ring: Optional[Ring], d: i
 
     CSR window: count = #{t < q} by lower bound, take = min(count, K), right
     aligned (:241-305); padding queries (id < 0) get an empty window (:233-235).
+    A NaN query time counts no entry (the reference's searchsorted over rows
+    padded with +inf returns the padded row length there, so its window would
+    run past the node's own entries: no defined answer to restate).
     Ring merge (:307-349): ring rows of max(node, 0) -- a padding query reads
     node 0's ring -- valid = id != -1 and t < q; candidates = K CSR slots ++ B
     ring slots, keyed by time (-inf when invalid), ascending, last K kept.
@@ -235,7 +238,9 @@ def recent(nodes, qtimes, K: int, csr: Optional[CSR], ring: Optional[Ring], d: i
         en[pad] = 0
         for q in range(Q):
             seg = csr.times[st[q]:en[q]]
-            cnt = int(np.searchsorted(seg, qtimes[q], side="left"))
+            # #{t < q}: NaN entries sort last and never count; a NaN query time
+            # counts none (searchsorted would place it after every entry)
+            cnt = 0 if np.isnan(qtimes[q]) else int(np.searchsorted(seg, qtimes[q], side="left"))
             take = min(cnt, K)
             lo = st[q] + cnt - take
             out_ids[q, K - take:] = csr.ids[lo:lo + take]

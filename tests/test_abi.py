@@ -195,6 +195,33 @@ def test_launch_shapes_stay_within_the_kernel_bounds():
     assert rc == 0 and sh[1] == 512 and sh[4] == 8 and sh[0] == 1  # one query over 8 waves
 
 
+def test_ring_less_launches_pack_queries_in_csr_window():
+    """A CSR-only tiled launch of more than 2,048 queries at K <= 64 with rows of at
+    most 64 bytes runs csr_window: 64 / Bp queries per wavefront (Bp = the power of
+    two >= max(K, 16)), `group` wavefronts per workgroup, no split; a larger K,
+    wider rows or a small launch take recent_fused's ring-less copy, one query per
+    wavefront."""
+    csr = _lib.TgxCsr(num_nodes=10, num_entries=5, feat_dim=8, feat_dtype=_lib.TGX_BF16, offsets=8,
+                      ids=8, times=8, feats=16)
+    for k, m in ((1, 4), (16, 4), (17, 2), (20, 2), (32, 2), (33, 1), (64, 1)):
+        a = _lib.TgxRecentArgs(k=k, group=4, num_queries=12000, nodes=8, times=8, out_ids=8,
+                               out_times=8, out_mask=8, out_feats=16)
+        rc, sh = _shape(None, ctypes.byref(csr), a)
+        assert rc == 0, _err()
+        assert sh[3] == m and sh[4] == 1 and sh[1] == 256
+        assert sh[0] == -(-12000 // (4 * m))
+        if m > 1:  # few queries: one per wave, split
+            a.num_queries = 2000
+            assert _shape(None, ctypes.byref(csr), a)[1][3] == 1
+    a = _lib.TgxRecentArgs(k=65, group=4, num_queries=12000, nodes=8, times=8, out_ids=8,
+                           out_times=8, out_mask=8, out_feats=16)
+    assert _shape(None, ctypes.byref(csr), a)[1][3] == 1
+    wide = _lib.TgxCsr(num_nodes=10, num_entries=5, feat_dim=40, feat_dtype=_lib.TGX_BF16, offsets=8,
+                       ids=8, times=8, feats=16)  # 80-byte rows
+    a.k = 20
+    assert _shape(None, ctypes.byref(wide), a)[1][3] == 1
+
+
 def test_fastdiv_range_is_checked():
     """Feature chunks are divided by the row's chunk count with a multiply-high
     that is exact for dividends below 2^32 / chunks: wider rows are refused."""

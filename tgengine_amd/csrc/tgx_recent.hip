@@ -820,6 +820,144 @@ void recent_fused(Params P) {
   }
 }
 
+// Ring-less tiled gather over a frozen CSR for K <= 64 with rows of at most NREG
+// 16-byte chunks (NREG = 0: no feature rows asked for).  Sub-group h of Bp =
+// 2^lg_bp >= K lanes takes query h of the wave's m = 64 / Bp consecutive
+// queries, and lane sl < K owns output position sl.  With the query's CSR
+// offsets in, each lane loads the entry that the window's last K would put at
+// its position (time, id, row, edge id).  When the query comes after the whole
+// window (its last time is below the query time; NaN times sort last, so the
+// window then holds none), those entries are the answer, as the search would
+// find: three dependent round trips (query, offsets, entries) before the
+// stores, against five for recent_fused's search, staging and row copy.
+// Otherwise the wave searches that query's window (wave_lower_bound, as
+// recent_fused) and reloads the answer's entries.
+template <int NREG>
+__global__ __launch_bounds__(kMaxWaves * kWave) void csr_window(Params P) {
+  using VT = u32x4;
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+  const int K = P.K;
+  const int m = P.m;
+  const int lg = P.lg_bp;
+  const int h = lane >> lg;
+  const int sl = lane & ((1 << lg) - 1);
+  const bool dyg = P.dt_mode == TGX_DT_DYGFORMER;
+
+  float* s_w = reinterpret_cast<float*>(smem);
+  float* s_b = s_w + (P.te_bytes / 8);
+  if (P.d_t > 0) {  // launch-uniform
+    for (int i = threadIdx.x; i < P.d_t; i += blockDim.x) {
+      s_w[i] = P.te_w[i];
+      s_b[i] = P.te_b != nullptr ? P.te_b[i] : 0.0f;
+    }
+    __syncthreads();
+  }
+  uint8_t* wb = smem + P.te_bytes + static_cast<size_t>(wv) * P.wave_bytes;
+  int32_t* pcode = reinterpret_cast<int32_t*>(wb);        // [m][K] 0 entry, -1 pad
+  float* pdt = reinterpret_cast<float*>(wb + P.off_pdt);  // [m][K] dt
+
+  const int64_t q0 = (static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + wv) * m;
+  int64_t q = q0 + h;
+  if (q >= P.Q) q = -1;
+  int64_t node = -1;
+  double qt = 0.0;
+  bool qvalid = true;
+  if (q >= 0) query_load(P, q, node, qt, qvalid);
+  const bool bad = q >= 0 && qvalid && node >= P.N;
+  if (bad && sl == 0 && P.status != nullptr) atomicAdd(&P.status[TGX_ST_BAD_QUERY_NODE], 1);
+  // a padding node (< 0) has an empty window
+  const bool live = q >= 0 && qvalid && !bad && node >= 0 && P.has_csr;
+  int64_t s0 = 0, s1 = 0;
+  if (live) {
+    s0 = P.c_off[node];
+    s1 = P.c_off[node + 1];
+  }
+
+  // ---- the entry at this lane's position if the answer is the window's last K ----
+  double t = 0.0;
+  int32_t id = -1;
+  int64_t eid = -1;
+  VT rows[NREG > 0 ? NREG : 1];
+#pragma unroll
+  for (int k = 0; k < (NREG > 0 ? NREG : 1); ++k) rows[k] = VT{};
+  auto load_entry = [&](int64_t x) {
+    t = P.c_times[x];
+    id = P.c_ids[x];
+    if (P.o_eids != nullptr) eid = P.c_eids != nullptr ? P.c_eids[x] : -1;
+    if constexpr (NREG > 0) {
+      const VT* src = reinterpret_cast<const VT*>(P.c_feats + x * P.row_bytes);
+#pragma unroll
+      for (int k = 0; k < NREG; ++k)
+        if (k < P.nch) rows[k] = src[k];
+    }
+  };
+  bool have = live && sl < K && s1 - K + sl >= s0;
+  if (have) load_entry(s1 - K + sl);
+  // sub-group uniform: lane K - 1 holds entry s1 - 1 whenever the window is not empty
+  const double tl = __shfl(t, (h << lg) + K - 1);
+  const bool after = !live || s1 == s0 || tl < qt;
+
+  // ---- otherwise: search the window, then load the answer's entries ----
+  const uint64_t slow = __ballot(!after);
+  if (slow != 0) {  // wave-uniform
+    int64_t cnt = 0;
+    for (int hh = 0; hh < m; ++hh) {
+      if (((slow >> (hh << lg)) & 1u) == 0) continue;  // wave-uniform
+      const int src = hh << lg;
+      const int64_t a0 = __shfl(s0, src);
+      const int64_t a1 = __shfl(s1, src);
+      const double th = __shfl(qt, src);
+      const int64_t c = wave_lower_bound<true>(P.c_times, a0, a1, th, lane) - a0;
+      if (h == hh) cnt = c;
+    }
+    if (!after) {
+      const int take = static_cast<int>(cnt < K ? cnt : K);
+      have = sl < K && sl >= K - take;
+      if (have) load_entry(s0 + cnt - K + sl);
+    }
+  }
+
+  // ---- outputs: position sl of query q ----
+  const bool out = q >= 0 && sl < K;
+  if (P.d_t > 0) {  // launch-uniform
+    float dt = 0.0f;
+    bool big = false;
+    if (out) {
+      const double tt = have ? t : 0.0;
+      dt = dyg ? static_cast<float>(qt) - static_cast<float>(tt) : static_cast<float>(qt - tt);
+      big = (!dyg || have) && !(fabsf(dt) < P.te_dt_small);
+      pcode[h * K + sl] = have ? 0 : -1;
+      pdt[h * K + sl] = dt;
+    }
+    const bool te_big = __ballot(big) != 0;
+    wave_sync();
+    // the wave's valid queries are consecutive from q0
+    const int64_t nv = q0 < P.Q ? (P.Q - q0 < m ? P.Q - q0 : m) : 0;
+    const int np = static_cast<int>(nv) * K;
+    if (np > 0) {
+      if (te_big)
+        encode_rows<true, false>(P, q0 * K, np, pcode, pdt, s_w, s_b, lane, kWave);
+      else
+        encode_rows<false, false>(P, q0 * K, np, pcode, pdt, s_w, s_b, lane, kWave);
+    }
+  }
+  if (out) {
+    const int64_t o = q * K + sl;
+    if constexpr (NREG > 0) {
+      VT* dst = reinterpret_cast<VT*>(P.o_feats + o * P.row_bytes);
+#pragma unroll
+      for (int k = 0; k < NREG; ++k)
+        if (k < P.nch) put<false>(dst + k, have ? rows[k] : VT{});
+    }
+    P.o_ids[o] = have ? id : -1;
+    P.o_times[o] = have ? t : 0.0;
+    P.o_mask[o] = have ? 1 : 0;
+    if (P.o_eids != nullptr) P.o_eids[o] = have ? eid : -1;
+  }
+}
+
 // stand-alone co-occurrence (FREQ) over id rows: one wavefront per pair.  A
 // position is valid by its mask byte, or without masks when its id is not -1;
 // counts cover valid positions only (an id of -2^31 marks an invalid one in LDS:
@@ -902,6 +1040,7 @@ struct Launch {
   int vec = 2;
   int nreg = 0;
   bool noring = false;
+  bool window = false;  // csr_window runs the launch
 };
 
 // |dt| below which every encoding argument fl32(fl32(dt w) + b) stays below
@@ -1173,7 +1312,7 @@ int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args
   int qslots = a->group;
   if (mode == TGX_PLAN_TILES && split > 1) qslots = 1;
   if (mode == TGX_PLAN_TILES && qslots * split > wave_cap) qslots = wave_cap > split ? wave_cap / split : 1;
-  const int waves = qslots * split;
+  int waves = qslots * split;
   if (waves < 1 || waves > kMaxWaves)
     return fail(TGX_ERR_LIMIT, "tgx_recent: %d wavefronts per workgroup outside [1, %d]", waves, kMaxWaves);
   int64_t nblocks = a->num_groups;
@@ -1182,7 +1321,7 @@ int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args
     const int64_t ntiles = (a->num_queries + P.m - 1) / P.m;
     nblocks = (ntiles + qslots - 1) / qslots;
   }
-  const size_t lds = static_cast<size_t>(P.te_bytes) + static_cast<size_t>(waves) * P.wave_bytes;
+  size_t lds = static_cast<size_t>(P.te_bytes) + static_cast<size_t>(waves) * P.wave_bytes;
   if (lds > 160 * 1024) return fail(TGX_ERR_LIMIT, "tgx_recent: %zu bytes of LDS needed", lds);
 
   int vec = 2;
@@ -1207,6 +1346,25 @@ int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args
   // rows of at most 4 16-byte chunks ride in registers with the ring slot
   int nreg = 0;
   if (vec == 16 && fe && P.B > 0) nreg = P.nch <= 2 ? 2 : (P.nch <= 4 ? 4 : 0);
+  // A ring-less tiled launch at K <= 64 whose queries take one wave each, with
+  // rows of at most 4 16-byte chunks (or none), runs csr_window instead: m =
+  // 64 / Bp queries per wave in sub-groups of Bp >= max(K, 16) lanes, `group`
+  // waves per workgroup
+  L.window = L.noring && K <= kWave && split == 1 && (!fe || (vec == 16 && P.nch <= 4));
+  if (L.window) {
+    int lgw = 4;
+    while ((1 << lgw) < K) ++lgw;
+    P.lg_bp = lgw;
+    P.m = kWave >> lgw;
+    P.off_pdt = round16(P.m * K * 4);
+    P.wave_bytes = 2 * round16(P.m * K * 4);
+    qslots = a->group;
+    waves = qslots;
+    const int64_t nwaves = (a->num_queries + P.m - 1) / P.m;
+    nblocks = (nwaves + qslots - 1) / qslots;
+    lds = static_cast<size_t>(P.te_bytes) + static_cast<size_t>(waves) * P.wave_bytes;
+    nreg = fe ? (P.nch <= 2 ? 2 : 4) : 0;
+  }
 
   // fused plan: one plan workgroup per blockDim entries, dispatched first
   L.fuse_plan = L.want_plan && plan_fused_ok(L.pl);
@@ -1271,7 +1429,14 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
     else
       launch(k_other);
   };
-  if (L.noring) {
+  if (L.window) {
+    if (L.nreg == 2)
+      launch(csr_window<2>);
+    else if (L.nreg == 4)
+      launch(csr_window<4>);
+    else
+      launch(csr_window<0>);
+  } else if (L.noring) {
     if (L.vec == 16)
       launch(recent_fused<16, 0, true, true>);
     else if (L.vec == 4)
@@ -1290,7 +1455,7 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
   } else {
     pick(recent_fused<2, 0, true>, recent_fused<2, 0, false>);
   }
-  rc = check_launch("recent_fused");
+  rc = check_launch(L.window ? "csr_window" : "recent_fused");
   if (rc != TGX_OK || !L.want_plan || L.fuse_plan) return rc;
   return launch_plan(L.pl, stream);  // batches beyond the fused plan's size
 }
