@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define TGX_ABI_VERSION 13
+#define TGX_ABI_VERSION 14
 
 /* status codes */
 #define TGX_OK 0
@@ -90,7 +90,10 @@ typedef struct tgx_ring {
 
 /* Frozen CSR (reference: temporal_graph.py:133-181): offsets int64 [N+1],
  * ids int32 [E], times float64 [E] (ascending within a node), feats [E,feat_dim],
- * eids int64 [E] (optional). */
+ * eids int64 [E] (optional).  max_time: the largest non-NaN time of the entries
+ * (+inf when unknown).  Results never depend on it: a query at a later time is
+ * after every window, and the gather then skips the search work it would issue
+ * ahead for a query that may fall inside one. */
 typedef struct tgx_csr {
   int64_t num_nodes;
   int64_t num_entries;
@@ -101,6 +104,7 @@ typedef struct tgx_csr {
   const double* times;
   const void* feats;
   const int64_t* eids;
+  double max_time;
 } tgx_csr;
 
 /* One group of queries read in place: query l of the group is node nodes[l]

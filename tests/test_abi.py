@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(L, n), n
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
-    assert L.tgx_abi_version() == _lib.TGX_ABI_VERSION == 13
+    assert L.tgx_abi_version() == _lib.TGX_ABI_VERSION == 14
     nm = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
                         text=True).stdout
     exported = set(re.findall(r"\bT (tgx_\w+)", nm))
@@ -43,7 +43,7 @@ LAYOUT_PROBE = r"""
 int main(void) {
   S(tgx_ring) F(tgx_ring, num_nodes) F(tgx_ring, slots) F(tgx_ring, ids) F(tgx_ring, eids)
   F(tgx_ring, scratch)
-  S(tgx_csr) F(tgx_csr, offsets) F(tgx_csr, eids)
+  S(tgx_csr) F(tgx_csr, offsets) F(tgx_csr, eids) F(tgx_csr, max_time)
   S(tgx_query_group) F(tgx_query_group, count) F(tgx_query_group, times_per)
   F(tgx_query_group, flags) F(tgx_query_group, valid)
   S(tgx_recent_args) F(tgx_recent_args, k) F(tgx_recent_args, plan) F(tgx_recent_args, group)

@@ -177,3 +177,23 @@ def test_csr_window_prepare_time_encoding(dt_mode, d_t, K):
     got = torch.cat([x.time_enc for x in groups]).cpu().numpy()
     assert got.shape == (3 * b, K, d_t)
     assert np.max(np.abs(got - exp)) <= TE_ATOL
+
+
+def test_csr_max_time_is_recorded_and_only_a_hint():
+    """freeze_csr records the largest non-NaN entry time in the CSR struct; the
+    gather only uses it to decide whether a query may fall inside a window (and
+    to issue its search's first round early), so any value gives the same
+    answers: -inf (no query probes ahead), +inf (every query over a long window
+    does) and the recorded one."""
+    N, Q, K, d = 300, 4000, 20, 16
+    rng, g, csr, tmax, fdt = _stream(44, N, d, True)
+    assert g._csr().max_time == tmax == np.nanmax(csr.times)
+    nodes, qt = _queries(rng, N, Q, tmax)
+    o = O.recent(nodes, qt, K, csr, None, d, fdt)
+    for hint in (float("-inf"), float("inf"), tmax):
+        g._csr().max_time = hint
+        r = g.recent(cu(nodes), cu(qt), K)
+        assert np.array_equal(r.neighbor_ids.cpu().numpy(), o.ids), hint
+        assert np.array_equal(r.timestamps.cpu().numpy().view(np.int64), o.times.view(np.int64)), hint
+        assert np.array_equal(r.mask.cpu().numpy(), o.mask), hint
+        assert np.array_equal(_feats_u8(r.edge_feats), o.feats.view(np.uint8)), hint

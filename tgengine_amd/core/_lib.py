@@ -24,7 +24,7 @@ TGX_CO_DYGFORMER = 2
 TGX_PLAN_TILES = 0
 TGX_PLAN_EVENTS = 1
 TGX_PLAN_LIST = 2
-TGX_ABI_VERSION = 13
+TGX_ABI_VERSION = 14
 TGX_STATUS_WORDS = 8
 TGX_ST_BAD_EVENT_NODE = 0
 TGX_ST_KEY_COLLISION = 1
@@ -46,7 +46,7 @@ class TgxRing(ctypes.Structure):
 class TgxCsr(ctypes.Structure):
     _fields_ = [("num_nodes", c_i64), ("num_entries", c_i64), ("feat_dim", c_i32),
                 ("feat_dtype", c_i32), ("offsets", c_vp), ("ids", c_vp), ("times", c_vp),
-                ("feats", c_vp), ("eids", c_vp)]
+                ("feats", c_vp), ("eids", c_vp), ("max_time", ctypes.c_double)]
 
 
 TGX_MAX_QUERY_GROUPS = 4

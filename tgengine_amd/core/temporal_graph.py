@@ -144,6 +144,7 @@ class TemporalGraph:
         self._nbr_times: Optional[Tensor] = None
         self._nbr_feats: Optional[Tensor] = None
         self._nbr_eids: Optional[Tensor] = None
+        self._csr_max_time = float("inf")  # largest non-NaN CSR time (a search hint)
 
         self._ov_ids: Optional[Tensor] = None
         self._ov_times: Optional[Tensor] = None
@@ -210,7 +211,7 @@ class TemporalGraph:
                 feat_dim=self.edge_feat_dim, feat_dtype=_DTYPES[self.feat_dtype],
                 offsets=self._offsets.data_ptr(), ids=_lib.ptr(self._nbr_ids),
                 times=_lib.ptr(self._nbr_times), feats=_lib.ptr(self._nbr_feats),
-                eids=_lib.ptr(self._nbr_eids))
+                eids=_lib.ptr(self._nbr_eids), max_time=self._csr_max_time)
         return self._csr_struct
 
     def _feat_in(self, edge_feat: Optional[Tensor], b: int) -> Optional[Tensor]:
@@ -426,9 +427,11 @@ class TemporalGraph:
             bufs = self._build
             src, dst, tt = bufs["src"][:E], bufs["dst"][:E], bufs["time"][:E]
             feats = bufs["feat"][:E] if "feat" in bufs else None
-            # one device round trip: node range, and whether the stream is time-ordered
+            # one device round trip: node range, whether the stream is time-ordered,
+            # and the largest non-NaN time
             lo = torch.minimum(src.min(), dst.min())
             hi = torch.maximum(src.max(), dst.max())
+            tmax = torch.where(torch.isnan(tt), float("-inf"), tt).max()
             if E > 1:
                 step = tt[1:] - tt[:-1]
                 first = torch.zeros(E, dtype=torch.bool, device=dev)
@@ -436,7 +439,9 @@ class TemporalGraph:
                 ordered = ((step > 0) | ((step == 0) & first[1:])).all()
             else:
                 ordered = torch.ones((), dtype=torch.bool, device=dev)
-            lo, hi, ordered = (int(x) for x in torch.stack([lo, hi, ordered.long()]).cpu())
+            host = torch.stack([lo.double(), hi.double(), ordered.double(), tmax]).cpu().tolist()
+            lo, hi, ordered = (int(x) for x in host[:3])  # node ids below 2^53: exact
+            self._csr_max_time = host[3]
             if lo < 0 or hi >= N:
                 raise IndexError("advance() got node ids outside [0, num_nodes)")
             flags = 0
@@ -649,6 +654,7 @@ class TemporalGraph:
         self._build_n = 0
         self._build_starts = []
         self._offsets = self._nbr_ids = self._nbr_times = self._nbr_feats = self._nbr_eids = None
+        self._csr_max_time = float("inf")
         self._ov_ids = self._ov_times = self._ov_feats = self._ov_write_pos = self._ov_eids = None
         self._ov_scratch = None
         self._ring_struct = None

@@ -130,6 +130,7 @@ struct Params {
   int64_t ev_tail;
   // |dt| below which no encoding argument reaches kRevArg (0: none is known)
   float te_dt_small;
+  double c_tmax;  // largest non-NaN CSR time (+inf: unknown)
 };
 
 template <int VEC>
@@ -625,9 +626,10 @@ void recent_fused(Params P) {
   // then a candidate's rank is its write-order distance from the oldest filled slot
   bool broken = true;
   int order = 0;
-  const bool try_fast = live && ncsr == 0 && B > 0 && P.r_wp != nullptr;
+  const bool try_fast = !NORING && live && ncsr == 0 && B > 0 && P.r_wp != nullptr;
   if (try_fast) {
-    const int w = P.b_pow2 ? static_cast<int>(wp & (B - 1)) : static_cast<int>(wp % B);
+    // (B > 0 here; the ring-less copies, whose B is the constant 0, compile no division)
+    const int w = P.b_pow2 || NORING ? static_cast<int>(wp & (B - 1)) : static_cast<int>(wp % B);
     order = sl - w < 0 ? sl - w + B : sl - w;
     const uint64_t filled = (__ballot(sl < B && rid != -1) >> (h << lg)) & submask;
     const int empty = B - __popcll(filled);
@@ -830,8 +832,11 @@ void recent_fused(Params P) {
 // window then holds none), those entries are the answer, as the search would
 // find: three dependent round trips (query, offsets, entries) before the
 // stores, against five for recent_fused's search, staging and row copy.
-// Otherwise the wave searches that query's window (wave_lower_bound, as
-// recent_fused) and reloads the answer's entries.
+// Otherwise the search goes on from a first Bp-ary round whose probes went out
+// with those loads (a window of more than Bp entries and a query time not after
+// the CSR's last one: max_time), the wave searching what is left of each such
+// query's window (wave_lower_bound, as recent_fused), and the answer's entries
+// are reloaded.
 template <int NREG>
 __global__ __launch_bounds__(kMaxWaves * kWave) void csr_window(Params P) {
   using VT = u32x4;
@@ -895,6 +900,18 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void csr_window(Params P) {
   };
   bool have = live && sl < K && s1 - K + sl >= s0;
   if (have) load_entry(s1 - K + sl);
+  // the search's first round over a window of more than Bp entries, when the query
+  // may be inside it (not after the CSR's last time): probe sl at s0 + (sl + 1)
+  // step - 1, clamped to the last entry
+  const int Bp = 1 << lg;
+  const int64_t wlen = s1 - s0;
+  const bool probing = live && wlen > Bp && qt <= P.c_tmax;
+  const int64_t step = probing ? (wlen + Bp - 1) >> lg : 0;
+  double tp = 0.0;
+  if (probing) {
+    const int64_t pos = s0 + (sl + 1) * step - 1;
+    tp = P.c_times[pos < s1 ? pos : s1 - 1];
+  }
   // sub-group uniform: lane K - 1 holds entry s1 - 1 whenever the window is not empty
   const double tl = __shfl(t, (h << lg) + K - 1);
   const bool after = !live || s1 == s0 || tl < qt;
@@ -902,15 +919,26 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void csr_window(Params P) {
   // ---- otherwise: search the window, then load the answer's entries ----
   const uint64_t slow = __ballot(!after);
   if (slow != 0) {  // wave-uniform
+    // the lower bound lies in [lo, hi]: after the first round, between the last
+    // probe below the query time and the next one
+    const uint64_t below = __ballot(probing && tp < qt) >> (h << lg);
+    int64_t lo = s0, hi = s1;
+    if (probing) {
+      const int64_t c = __popcll(Bp == kWave ? below : below & ((uint64_t(1) << Bp) - 1));
+      const int64_t nl = s0 + c * step;
+      const int64_t pc = s0 + (c + 1) * step - 1;
+      lo = nl < s1 ? nl : s1;
+      hi = pc < s1 ? pc : s1;
+    }
     int64_t cnt = 0;
     for (int hh = 0; hh < m; ++hh) {
       if (((slow >> (hh << lg)) & 1u) == 0) continue;  // wave-uniform
       const int src = hh << lg;
-      const int64_t a0 = __shfl(s0, src);
-      const int64_t a1 = __shfl(s1, src);
+      const int64_t a0 = __shfl(lo, src);
+      const int64_t a1 = __shfl(hi, src);
       const double th = __shfl(qt, src);
-      const int64_t c = wave_lower_bound<true>(P.c_times, a0, a1, th, lane) - a0;
-      if (h == hh) cnt = c;
+      const int64_t b = wave_lower_bound<true>(P.c_times, a0, a1, th, lane);
+      if (h == hh) cnt = b - s0;
     }
     if (!after) {
       const int take = static_cast<int>(cnt < K ? cnt : K);
@@ -1122,6 +1150,7 @@ int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args
       return fail(TGX_ERR_ARG, "tgx_recent: ring and csr disagree on nodes/feat_dim/dtype");
     P.N = csr->num_nodes;
     P.has_csr = csr->num_entries > 0 ? 1 : 0;
+    P.c_tmax = csr->max_time;
     P.c_off = csr->offsets;
     P.c_ids = csr->ids;
     P.c_times = csr->times;
