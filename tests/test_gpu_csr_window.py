@@ -1,8 +1,9 @@
-"""recent() on a frozen CSR through csr_window, the ring-less launch shape for
-K <= 64 whose queries take one wavefront each (more than 2,048 queries) and whose
-rows are at most 64 bytes (or absent): 64 / Bp queries per wavefront, each
-answered from the window's last K entries when the query comes after the whole
-window, else from a search.
+"""recent() and DataPipeline.prepare on a frozen CSR through the ring-less
+kernels at K <= 64: csr_window (more than 2,048 queries, each taking one
+wavefront, rows of at most 64 bytes or none: 64 / Bp queries per wavefront) and
+csr_split (the other launches: queries split over several wavefronts, or rows of
+any width through memory).  Both answer a query from the window's last K entries
+when it comes after the whole window, else from a search.
 
 Windows of 0 to thousands of entries with tied times; queries before, inside, at
 and after them, NaN query times, padding (-1) and out-of-range nodes, a validity
@@ -197,3 +198,58 @@ def test_csr_max_time_is_recorded_and_only_a_hint():
         assert np.array_equal(r.timestamps.cpu().numpy().view(np.int64), o.times.view(np.int64)), hint
         assert np.array_equal(r.mask.cpu().numpy(), o.mask), hint
         assert np.array_equal(_feats_u8(r.edge_feats), o.feats.view(np.uint8)), hint
+
+
+@pytest.mark.parametrize("d,bf16,K,dt_mode", [(172, False, 32, "dygformer"), (172, False, 64, "tgn"),
+                                              (16, True, 20, "dygformer")])
+def test_csr_split_prepare_engine_shape(d, bf16, K, dt_mode):
+    """DataPipeline.prepare of 200-event batches on the frozen CSR, as the Engine
+    runs it (600 queries, each split over several wavefronts): 172-d f32 rows
+    through memory, time encodings, queries after and inside their windows."""
+    N, b = 400, 200
+    rng, g, csr, tmax, fdt = _stream(45 + K, N, d, bf16)
+    spec = GatherSpec(neighbors=NeighborSpec(k=K), time_encoding=100, dt_mode=dt_mode)
+    pipe = DataPipeline(spec, g)
+    assert _shape_m(g, 3 * b, K, 100)[1] > 1  # split: the csr_split shape
+    for _ in range(2):
+        nodes, qt = _queries(rng, N, 3 * b, tmax)
+        src, dst, neg = (np.maximum(nodes[i * b:(i + 1) * b], 0) for i in range(3))
+        t = np.where(np.isnan(qt[:b]), tmax + 1.0, qt[:b])
+        pb = pipe.prepare(RawBatch(src=cu(src), dst=cu(dst), time=cu(t), neg=cu(neg)))
+        allq = np.concatenate([src, dst, neg])
+        qts = np.concatenate([t, t, t])
+        o = O.recent(allq, qts, K, csr, None, d, fdt)
+        assert o.mask.all(1).any() and not o.mask.all()
+        groups = [pb.src_neighbors, pb.dst_neighbors, pb.neg_neighbors]
+        assert np.array_equal(torch.cat([x.neighbor_ids for x in groups]).cpu().numpy(), o.ids)
+        assert np.array_equal(torch.cat([x.timestamps for x in groups]).cpu().numpy().view(np.int64),
+                              o.times.view(np.int64))
+        assert np.array_equal(torch.cat([x.mask for x in groups]).cpu().numpy(), o.mask)
+        assert np.array_equal(np.concatenate([_feats_u8(x.edge_feats) for x in groups]),
+                              o.feats.view(np.uint8))
+        dt = O.dt_dygformer(qts, o.times) if dt_mode == "dygformer" else O.dt_tgn(qts, o.times)
+        exp = O.time_encode_exact(dt, cosine_time_weights(100), o.mask if dt_mode == "dygformer" else None)
+        got = torch.cat([x.time_enc for x in groups]).cpu().numpy()
+        assert np.max(np.abs(got - exp)) <= TE_ATOL
+
+
+@pytest.mark.parametrize("d,bf16,K,Q", [(3, False, 20, 500), (7, True, 33, 500), (172, False, 64, 3000),
+                                        (16, True, 64, 100)])
+def test_csr_split_recent_matches_oracle(d, bf16, K, Q):
+    """recent() launches csr_split takes: 12- and 14-byte rows (4- and 2-byte
+    copy chunks), 688-byte rows at 3,000 queries (rows through memory, 4 waves per
+    query), a small launch (8 waves per query); edge ids, NaN query times, padding
+    and out-of-range nodes."""
+    N = 400
+    rng, g, csr, tmax, fdt = _stream(60 + K, N, d, bf16)
+    nodes, qt = _queries(rng, N, Q, tmax)
+    bad = rng.random(Q) < 0.02
+    nodes[bad] = N + 3
+    r = g.recent(cu(nodes), cu(qt), K)
+    o = O.recent(np.where(bad, -1, nodes), qt, K, csr, None, d, fdt)
+    assert np.array_equal(r.neighbor_ids.cpu().numpy(), o.ids)
+    assert np.array_equal(r.timestamps.cpu().numpy().view(np.int64), o.times.view(np.int64))
+    assert np.array_equal(r.mask.cpu().numpy(), o.mask)
+    assert np.array_equal(_feats_u8(r.edge_feats), o.feats.view(np.uint8))
+    assert np.array_equal(r.edge_ids.cpu().numpy(), o.eids)
+    assert g.status()["bad_query_nodes"] == int(bad.sum())

@@ -986,6 +986,151 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void csr_window(Params P) {
   }
 }
 
+// Ring-less tiled gather over a frozen CSR for K <= 64 whose queries may be split
+// over several waves and whose rows go through memory (any width): the launches
+// csr_window does not take (fewer queries, or rows above 64 bytes), such as
+// DataPipeline.prepare of 200-event batches on the Engine's frozen CSR.  Each of
+// the `split` waves of a query holds the query's K answer entries (lane p owns
+// position p) and writes every split-th chunk of its rows and encodings.  With
+// the offsets in, a wave loads the entries the window's last K would put at its
+// lanes' positions and the first kCopyDepth chunks per lane of its share of
+// their rows; when the query comes after its whole window those are the answer
+// (query, offsets, entries and first row chunks: three dependent round trips
+// before the first store, against five in recent_fused's ring-less copy).
+// Otherwise the wave searches the window and reloads.
+template <int VEC>
+__global__ __launch_bounds__(kMaxWaves * kWave) void csr_split(Params P) {
+  using VT = typename Vec<VEC>::T;
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+  const int K = P.K;
+  const int split = P.split;
+  const int qs = wv / split;
+  const int part = wv - qs * split;
+  const bool dyg = P.dt_mode == TGX_DT_DYGFORMER;
+
+  float* s_w = reinterpret_cast<float*>(smem);
+  float* s_b = s_w + (P.te_bytes / 8);
+  if (P.d_t > 0) {  // launch-uniform
+    for (int i = threadIdx.x; i < P.d_t; i += blockDim.x) {
+      s_w[i] = P.te_w[i];
+      s_b[i] = P.te_b != nullptr ? P.te_b[i] : 0.0f;
+    }
+    __syncthreads();
+  }
+  uint8_t* wb = smem + P.te_bytes + static_cast<size_t>(wv) * P.wave_bytes;
+  int32_t* pcode = reinterpret_cast<int32_t*>(wb);        // [K] 0 entry, -1 pad
+  float* pdt = reinterpret_cast<float*>(wb + P.off_pdt);  // [K] dt
+
+  int64_t q = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave / split) + qs;
+  if (q >= P.Q) q = -1;
+  int64_t node = -1;
+  double qt = 0.0;
+  bool qvalid = true;
+  if (q >= 0) query_load(P, q, node, qt, qvalid);
+  const bool bad = q >= 0 && qvalid && node >= P.N;
+  if (bad && lane == 0 && part == 0 && P.status != nullptr) atomicAdd(&P.status[TGX_ST_BAD_QUERY_NODE], 1);
+  // wave-uniform; a padding node (< 0) has an empty window
+  const bool live = q >= 0 && qvalid && !bad && node >= 0 && P.has_csr;
+  int64_t s0 = 0, s1 = 0;
+  if (live) {
+    s0 = P.c_off[node];
+    s1 = P.c_off[node + 1];
+  }
+
+  // ---- if the answer is the window's last K: lane p's entry, the first row chunks ----
+  double t = 0.0;
+  int32_t id = -1;
+  int64_t eid = -1;
+  auto load_entry = [&](int64_t x) {
+    t = P.c_times[x];
+    id = P.c_ids[x];
+    if (P.o_eids != nullptr) eid = P.c_eids != nullptr ? P.c_eids[x] : -1;
+  };
+  bool have = live && lane < K && s1 - K + lane >= s0;
+  if (have) load_entry(s1 - K + lane);
+  const bool fe = P.o_feats != nullptr && P.row_bytes > 0;
+  const int nch = P.nch;
+  const int total = K * nch;
+  const FastDiv dv(nch, P.fd_c);
+  const int ostride = split * kWave;
+  const VT* crow = reinterpret_cast<const VT*>(P.c_feats);
+  VT v[kCopyDepth];
+#pragma unroll
+  for (int u = 0; u < kCopyDepth; ++u) {
+    const int idx = part * kWave + u * ostride + lane;
+    v[u] = VT{};
+    if (fe && live && idx < total) {
+      const int p = static_cast<int>(dv.div(idx));
+      const int64_t x = s1 - K + p;
+      if (x >= s0) v[u] = crow[x * nch + (idx - p * nch)];
+    }
+  }
+  const double tl = __shfl(t, K - 1);  // entry s1 - 1 whenever the window is not empty
+  const bool after = !live || s1 == s0 || tl < qt;
+  // position p >= K - take holds entry base + p
+  int64_t base = s1 - K;
+  int take = live ? static_cast<int>(s1 - s0 < K ? s1 - s0 : K) : 0;
+  if (!after) {  // wave-uniform
+    const int64_t cnt = wave_lower_bound<true>(P.c_times, s0, s1, qt, lane) - s0;
+    take = static_cast<int>(cnt < K ? cnt : K);
+    base = s0 + cnt - K;
+    have = lane < K && lane >= K - take;
+    if (have) load_entry(base + lane);
+  }
+
+  if (q >= 0) {  // wave-uniform
+    // ---- feature rows: the wave's share of the K x nch chunks ----
+    if (fe) {
+      VT* of = reinterpret_cast<VT*>(P.o_feats) + q * total;
+      for (int idx0 = part * kWave; idx0 < total; idx0 += kCopyDepth * ostride) {
+        if (idx0 != part * kWave || !after) {
+#pragma unroll
+          for (int u = 0; u < kCopyDepth; ++u) {
+            const int idx = idx0 + u * ostride + lane;
+            v[u] = VT{};
+            if (idx < total) {
+              const int p = static_cast<int>(dv.div(idx));
+              if (p >= K - take) v[u] = crow[(base + p) * nch + (idx - p * nch)];
+            }
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kCopyDepth; ++u) {
+          const int idx = idx0 + u * ostride + lane;
+          if (idx < total) put<true>(of + idx, v[u]);
+        }
+      }
+    }
+    // ---- time encodings: the wave's share of the K x d_t ----
+    if (P.d_t > 0) {
+      bool big = false;
+      if (lane < K) {
+        const double tt = have ? t : 0.0;
+        const float dt = dyg ? static_cast<float>(qt) - static_cast<float>(tt) : static_cast<float>(qt - tt);
+        big = (!dyg || have) && !(fabsf(dt) < P.te_dt_small);
+        pcode[lane] = have ? 0 : -1;
+        pdt[lane] = dt;
+      }
+      const bool te_big = __ballot(big) != 0;
+      wave_sync();
+      if (te_big)
+        encode_rows<true, true>(P, q * K, K, pcode, pdt, s_w, s_b, part * kWave + lane, ostride);
+      else
+        encode_rows<false, true>(P, q * K, K, pcode, pdt, s_w, s_b, part * kWave + lane, ostride);
+    }
+    // ---- ids / times / mask / edge ids (the query's first wave) ----
+    if (part == 0 && lane < K) {
+      const int64_t o = q * K + lane;
+      P.o_ids[o] = have ? id : -1;
+      P.o_times[o] = have ? t : 0.0;
+      P.o_mask[o] = have ? 1 : 0;
+      if (P.o_eids != nullptr) P.o_eids[o] = have ? eid : -1;
+    }
+  }
+}
+
 // stand-alone co-occurrence (FREQ) over id rows: one wavefront per pair.  A
 // position is valid by its mask byte, or without masks when its id is not -1;
 // counts cover valid positions only (an id of -2^31 marks an invalid one in LDS:
@@ -1069,6 +1214,7 @@ struct Launch {
   int nreg = 0;
   bool noring = false;
   bool window = false;  // csr_window runs the launch
+  bool csr_split = false;  // csr_split runs it
 };
 
 // |dt| below which every encoding argument fl32(fl32(dt w) + b) stays below
@@ -1394,6 +1540,14 @@ int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args
     lds = static_cast<size_t>(P.te_bytes) + static_cast<size_t>(waves) * P.wave_bytes;
     nreg = fe ? (P.nch <= 2 ? 2 : 4) : 0;
   }
+  // the other ring-less tiled launches at K <= 64 (split queries, or rows through
+  // memory) run csr_split, with recent_fused's split and query slots
+  L.csr_split = L.noring && !L.window && K <= kWave;
+  if (L.csr_split) {
+    P.off_pdt = round16(K * 4);
+    P.wave_bytes = 2 * round16(K * 4);
+    lds = static_cast<size_t>(P.te_bytes) + static_cast<size_t>(waves) * P.wave_bytes;
+  }
 
   // fused plan: one plan workgroup per blockDim entries, dispatched first
   L.fuse_plan = L.want_plan && plan_fused_ok(L.pl);
@@ -1465,6 +1619,13 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
       launch(csr_window<4>);
     else
       launch(csr_window<0>);
+  } else if (L.csr_split) {
+    if (L.vec == 16)
+      launch(csr_split<16>);
+    else if (L.vec == 4)
+      launch(csr_split<4>);
+    else
+      launch(csr_split<2>);
   } else if (L.noring) {
     if (L.vec == 16)
       launch(recent_fused<16, 0, true, true>);
@@ -1484,7 +1645,7 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
   } else {
     pick(recent_fused<2, 0, true>, recent_fused<2, 0, false>);
   }
-  rc = check_launch(L.window ? "csr_window" : "recent_fused");
+  rc = check_launch(L.window ? "csr_window" : L.csr_split ? "csr_split" : "recent_fused");
   if (rc != TGX_OK || !L.want_plan || L.fuse_plan) return rc;
   return launch_plan(L.pl, stream);  // batches beyond the fused plan's size
 }
