@@ -201,11 +201,13 @@ def test_csr_max_time_is_recorded_and_only_a_hint():
 
 
 @pytest.mark.parametrize("d,bf16,K,dt_mode", [(172, False, 32, "dygformer"), (172, False, 64, "tgn"),
-                                              (16, True, 20, "dygformer")])
+                                              (16, True, 20, "dygformer"), (2, False, 512, "dygformer"),
+                                              (2, False, 100, "tgn")])
 def test_csr_split_prepare_engine_shape(d, bf16, K, dt_mode):
     """DataPipeline.prepare of 200-event batches on the frozen CSR, as the Engine
-    runs it (600 queries, each split over several wavefronts): 172-d f32 rows
-    through memory, time encodings, queries after and inside their windows."""
+    runs it (600 queries, each split over several wavefronts, at most 64 output
+    positions per wavefront): 172-d f32 rows through memory, LastFM's K = 512 with
+    2-d rows, time encodings, queries after and inside their windows."""
     N, b = 400, 200
     rng, g, csr, tmax, fdt = _stream(45 + K, N, d, bf16)
     spec = GatherSpec(neighbors=NeighborSpec(k=K), time_encoding=100, dt_mode=dt_mode)
@@ -234,12 +236,13 @@ def test_csr_split_prepare_engine_shape(d, bf16, K, dt_mode):
 
 
 @pytest.mark.parametrize("d,bf16,K,Q", [(3, False, 20, 500), (7, True, 33, 500), (172, False, 64, 3000),
-                                        (16, True, 64, 100)])
+                                        (16, True, 64, 100), (4, False, 300, 3000), (16, True, 512, 700)])
 def test_csr_split_recent_matches_oracle(d, bf16, K, Q):
     """recent() launches csr_split takes: 12- and 14-byte rows (4- and 2-byte
     copy chunks), 688-byte rows at 3,000 queries (rows through memory, 4 waves per
-    query), a small launch (8 waves per query); edge ids, NaN query times, padding
-    and out-of-range nodes."""
+    query), a small launch (8 waves per query), K = 300 and 512 (8 waves of at
+    most 64 positions); edge ids, NaN query times, padding and out-of-range
+    nodes."""
     N = 400
     rng, g, csr, tmax, fdt = _stream(60 + K, N, d, bf16)
     nodes, qt = _queries(rng, N, Q, tmax)

@@ -986,19 +986,24 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void csr_window(Params P) {
   }
 }
 
-// Ring-less tiled gather over a frozen CSR for K <= 64 whose queries may be split
-// over several waves and whose rows go through memory (any width): the launches
-// csr_window does not take (fewer queries, or rows above 64 bytes), such as
-// DataPipeline.prepare of 200-event batches on the Engine's frozen CSR.  Each of
-// the `split` waves of a query holds the query's K answer entries (lane p owns
-// position p) and writes every split-th chunk of its rows and encodings.  With
-// the offsets in, a wave loads the entries the window's last K would put at its
-// lanes' positions and the first kCopyDepth chunks per lane of its share of
+// Ring-less tiled gather over a frozen CSR whose queries may be split over
+// several waves and whose rows go through memory (any width): the launches
+// csr_window does not take (fewer queries, rows above 64 bytes, K above 64),
+// such as DataPipeline.prepare of 200-event batches on the Engine's frozen CSR.
+// Two layouts of a query's `split` waves: at K <= 64 each wave holds all K
+// answer entries (lane p: position p) and writes every split-th 64-chunk run of
+// the query's rows and encodings; with RANGES (K above 64) the waves own
+// consecutive ranges of per = ceil(K / split) <= 64 positions (lane l of wave
+// part: position part * per + l) and write those positions' outputs.  (At the
+// Engine's K = 32 and 64 the interleaved runs measured 14% faster than ranges;
+// at K = 512 only ranges keep one entry per lane.)  With the offsets in, a wave
+// loads the entries the window's last K would put at its lanes' positions, the
+// window's last time and the first kCopyDepth chunks per lane of its share of
 // their rows; when the query comes after its whole window those are the answer
 // (query, offsets, entries and first row chunks: three dependent round trips
 // before the first store, against five in recent_fused's ring-less copy).
 // Otherwise the wave searches the window and reloads.
-template <int VEC>
+template <int VEC, bool RANGES>
 __global__ __launch_bounds__(kMaxWaves * kWave) void csr_split(Params P) {
   using VT = typename Vec<VEC>::T;
   extern __shared__ __align__(16) uint8_t smem[];
@@ -1008,6 +1013,14 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void csr_split(Params P) {
   const int split = P.split;
   const int qs = wv / split;
   const int part = wv - qs * split;
+  const int per = RANGES ? (K + split - 1) / split : K;
+  const int p0 = RANGES ? part * per : 0;
+  const int np = K - p0 < per ? (K - p0 > 0 ? K - p0 : 0) : per;  // the wave's positions
+  const int pos = p0 + lane;                                      // lane < np
+  // the wave's share of the chunks of its positions' rows (and of their
+  // encodings): 64-chunk runs from off, every cstride chunks
+  const int off = RANGES ? 0 : part * kWave;
+  const int cstride = RANGES ? kWave : split * kWave;
   const bool dyg = P.dt_mode == TGX_DT_DYGFORMER;
 
   float* s_w = reinterpret_cast<float*>(smem);
@@ -1020,8 +1033,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void csr_split(Params P) {
     __syncthreads();
   }
   uint8_t* wb = smem + P.te_bytes + static_cast<size_t>(wv) * P.wave_bytes;
-  int32_t* pcode = reinterpret_cast<int32_t*>(wb);        // [K] 0 entry, -1 pad
-  float* pdt = reinterpret_cast<float*>(wb + P.off_pdt);  // [K] dt
+  int32_t* pcode = reinterpret_cast<int32_t*>(wb);        // [per] 0 entry, -1 pad
+  float* pdt = reinterpret_cast<float*>(wb + P.off_pdt);  // [per] dt
 
   int64_t q = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave / split) + qs;
   if (q >= P.Q) q = -1;
@@ -1039,8 +1052,9 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void csr_split(Params P) {
     s1 = P.c_off[node + 1];
   }
 
-  // ---- if the answer is the window's last K: lane p's entry, the first row chunks ----
-  double t = 0.0;
+  // ---- if the answer is the window's last K: this lane's entry, the window's last
+  // time and the first row chunks of the wave's positions ----
+  double t = 0.0, tl = 0.0;
   int32_t id = -1;
   int64_t eid = -1;
   auto load_entry = [&](int64_t x) {
@@ -1048,26 +1062,27 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void csr_split(Params P) {
     id = P.c_ids[x];
     if (P.o_eids != nullptr) eid = P.c_eids != nullptr ? P.c_eids[x] : -1;
   };
-  bool have = live && lane < K && s1 - K + lane >= s0;
-  if (have) load_entry(s1 - K + lane);
+  bool have = live && lane < np && s1 - K + pos >= s0;
+  if (have) load_entry(s1 - K + pos);
+  // with ranges only the last wave holds position K - 1
+  if (RANGES && live && s1 > s0) tl = P.c_times[s1 - 1];
   const bool fe = P.o_feats != nullptr && P.row_bytes > 0;
   const int nch = P.nch;
-  const int total = K * nch;
+  const int total = np * nch;  // chunks of the wave's positions
   const FastDiv dv(nch, P.fd_c);
-  const int ostride = split * kWave;
   const VT* crow = reinterpret_cast<const VT*>(P.c_feats);
   VT v[kCopyDepth];
 #pragma unroll
   for (int u = 0; u < kCopyDepth; ++u) {
-    const int idx = part * kWave + u * ostride + lane;
+    const int idx = off + u * cstride + lane;
     v[u] = VT{};
     if (fe && live && idx < total) {
-      const int p = static_cast<int>(dv.div(idx));
-      const int64_t x = s1 - K + p;
-      if (x >= s0) v[u] = crow[x * nch + (idx - p * nch)];
+      const int pl = static_cast<int>(dv.div(idx));
+      const int64_t x = s1 - K + p0 + pl;
+      if (x >= s0) v[u] = crow[x * nch + (idx - pl * nch)];
     }
   }
-  const double tl = __shfl(t, K - 1);  // entry s1 - 1 whenever the window is not empty
+  if (!RANGES) tl = __shfl(t, K - 1);  // entry s1 - 1 whenever the window is not empty
   const bool after = !live || s1 == s0 || tl < qt;
   // position p >= K - take holds entry base + p
   int64_t base = s1 - K;
@@ -1076,37 +1091,37 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void csr_split(Params P) {
     const int64_t cnt = wave_lower_bound<true>(P.c_times, s0, s1, qt, lane) - s0;
     take = static_cast<int>(cnt < K ? cnt : K);
     base = s0 + cnt - K;
-    have = lane < K && lane >= K - take;
-    if (have) load_entry(base + lane);
+    have = lane < np && pos >= K - take;
+    if (have) load_entry(base + pos);
   }
 
-  if (q >= 0) {  // wave-uniform
-    // ---- feature rows: the wave's share of the K x nch chunks ----
+  if (q >= 0 && np > 0) {  // wave-uniform
+    // ---- feature rows of the wave's positions ----
     if (fe) {
-      VT* of = reinterpret_cast<VT*>(P.o_feats) + q * total;
-      for (int idx0 = part * kWave; idx0 < total; idx0 += kCopyDepth * ostride) {
-        if (idx0 != part * kWave || !after) {
+      VT* of = reinterpret_cast<VT*>(P.o_feats) + (q * K + p0) * nch;
+      for (int idx0 = off; idx0 < total; idx0 += kCopyDepth * cstride) {
+        if (idx0 != off || !after) {
 #pragma unroll
           for (int u = 0; u < kCopyDepth; ++u) {
-            const int idx = idx0 + u * ostride + lane;
+            const int idx = idx0 + u * cstride + lane;
             v[u] = VT{};
             if (idx < total) {
-              const int p = static_cast<int>(dv.div(idx));
-              if (p >= K - take) v[u] = crow[(base + p) * nch + (idx - p * nch)];
+              const int pl = static_cast<int>(dv.div(idx));
+              if (p0 + pl >= K - take) v[u] = crow[(base + p0 + pl) * nch + (idx - pl * nch)];
             }
           }
         }
 #pragma unroll
         for (int u = 0; u < kCopyDepth; ++u) {
-          const int idx = idx0 + u * ostride + lane;
+          const int idx = idx0 + u * cstride + lane;
           if (idx < total) put<true>(of + idx, v[u]);
         }
       }
     }
-    // ---- time encodings: the wave's share of the K x d_t ----
+    // ---- time encodings of the wave's positions ----
     if (P.d_t > 0) {
       bool big = false;
-      if (lane < K) {
+      if (lane < np) {
         const double tt = have ? t : 0.0;
         const float dt = dyg ? static_cast<float>(qt) - static_cast<float>(tt) : static_cast<float>(qt - tt);
         big = (!dyg || have) && !(fabsf(dt) < P.te_dt_small);
@@ -1116,13 +1131,13 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void csr_split(Params P) {
       const bool te_big = __ballot(big) != 0;
       wave_sync();
       if (te_big)
-        encode_rows<true, true>(P, q * K, K, pcode, pdt, s_w, s_b, part * kWave + lane, ostride);
+        encode_rows<true, true>(P, q * K + p0, np, pcode, pdt, s_w, s_b, off + lane, cstride);
       else
-        encode_rows<false, true>(P, q * K, K, pcode, pdt, s_w, s_b, part * kWave + lane, ostride);
+        encode_rows<false, true>(P, q * K + p0, np, pcode, pdt, s_w, s_b, off + lane, cstride);
     }
-    // ---- ids / times / mask / edge ids (the query's first wave) ----
-    if (part == 0 && lane < K) {
-      const int64_t o = q * K + lane;
+    // ---- ids / times / mask / edge ids (without ranges: the query's first wave) ----
+    if (lane < np && (RANGES || part == 0)) {
+      const int64_t o = q * K + pos;
       P.o_ids[o] = have ? id : -1;
       P.o_times[o] = have ? t : 0.0;
       P.o_mask[o] = have ? 1 : 0;
@@ -1215,6 +1230,7 @@ struct Launch {
   bool noring = false;
   bool window = false;  // csr_window runs the launch
   bool csr_split = false;  // csr_split runs it
+  bool csr_ranges = false;  // in position ranges (K above 64)
 };
 
 // |dt| below which every encoding argument fl32(fl32(dt w) + b) stays below
@@ -1540,12 +1556,27 @@ int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args
     lds = static_cast<size_t>(P.te_bytes) + static_cast<size_t>(waves) * P.wave_bytes;
     nreg = fe ? (P.nch <= 2 ? 2 : 4) : 0;
   }
-  // the other ring-less tiled launches at K <= 64 (split queries, or rows through
-  // memory) run csr_split, with recent_fused's split and query slots
-  L.csr_split = L.noring && !L.window && K <= kWave;
+  // the other ring-less tiled launches (split queries, rows through memory, K
+  // above 64) run csr_split: recent_fused's split; above K = 64 in position
+  // ranges, the split raised to a power of two >= K / 64 (each wave owns at most 64
+  // positions; its LDS is two words per position, so the split never leaves
+  // workgroups for a second round)
+  L.csr_split = L.noring && !L.window;
+  L.csr_ranges = K > kWave;
   if (L.csr_split) {
-    P.off_pdt = round16(K * 4);
-    P.wave_bytes = 2 * round16(K * 4);
+    int sp = split;
+    while (sp * kWave < K) sp *= 2;  // K <= TGX_MAX_K = 8 x 64
+    if (sp != split) {
+      split = sp;
+      P.split = split;
+      qslots = 1;
+      waves = split;
+      nblocks = a->num_queries;
+    }
+    // LDS: pcode and dt of the wave's positions (all K without ranges)
+    const int per = L.csr_ranges ? (K + split - 1) / split : K;
+    P.off_pdt = round16(per * 4);
+    P.wave_bytes = 2 * round16(per * 4);
     lds = static_cast<size_t>(P.te_bytes) + static_cast<size_t>(waves) * P.wave_bytes;
   }
 
@@ -1620,12 +1651,21 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
     else
       launch(csr_window<0>);
   } else if (L.csr_split) {
-    if (L.vec == 16)
-      launch(csr_split<16>);
-    else if (L.vec == 4)
-      launch(csr_split<4>);
-    else
-      launch(csr_split<2>);
+    if (L.csr_ranges) {
+      if (L.vec == 16)
+        launch(csr_split<16, true>);
+      else if (L.vec == 4)
+        launch(csr_split<4, true>);
+      else
+        launch(csr_split<2, true>);
+    } else {
+      if (L.vec == 16)
+        launch(csr_split<16, false>);
+      else if (L.vec == 4)
+        launch(csr_split<4, false>);
+      else
+        launch(csr_split<2, false>);
+    }
   } else if (L.noring) {
     if (L.vec == 16)
       launch(recent_fused<16, 0, true, true>);
