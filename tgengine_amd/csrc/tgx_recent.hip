@@ -475,11 +475,7 @@ constexpr int kWavesPerEu = NREG > 0 ? 1 : 8;
 // TILES: the launch's plan mode is TGX_PLAN_TILES (no event or list plan, so no
 // co-occurrence); that copy of the kernel carries none of their code, which
 // shortens its start-up
-// NORING: a tiled launch without a ring (a frozen CSR before any post-freeze
-// advance, as the Engine prepares): the ring code is compiled out, and the CSR
-// window, which is then the answer in order, is emitted straight from memory
-// without staging its candidates in LDS (a large K's waves stay small)
-template <int VEC, int NREG, bool TILES, bool NORING = false>
+template <int VEC, int NREG, bool TILES>
 __global__ __launch_bounds__(kMaxWaves * kWave) __attribute__((amdgpu_waves_per_eu(kWavesPerEu<NREG>)))
 void recent_fused(Params P) {
   using VT = typename Vec<VEC>::T;
@@ -493,7 +489,7 @@ void recent_fused(Params P) {
   }
   const int64_t g = static_cast<int64_t>(blockIdx.x) - P.plan_blocks;
   const int K = P.K;
-  const int B = NORING ? 0 : P.B;
+  const int B = P.B;
   const int C = P.cand_cap;
   const int m = P.m;
   const int lg = P.lg_bp;
@@ -589,14 +585,10 @@ void recent_fused(Params P) {
         }
       }
     }
-    // with a ring the candidates are ranked from LDS; without one (B == 0) the
-    // CSR window is the answer in order and is emitted from memory below
-    if (!NORING) {
-      for (int j = sl; j < ncsr; j += Bp) {
-        ct[h * C + j] = P.c_times[cbase + j];
-        cid[h * C + j] = P.c_ids[cbase + j];
-        ccode[h * C + j] = B + j;
-      }
+    for (int j = sl; j < ncsr; j += Bp) {
+      ct[h * C + j] = P.c_times[cbase + j];
+      cid[h * C + j] = P.c_ids[cbase + j];
+      ccode[h * C + j] = B + j;
     }
   }
   const bool v = live && sl < B && rid != -1 && rt < qt;
@@ -626,10 +618,9 @@ void recent_fused(Params P) {
   // then a candidate's rank is its write-order distance from the oldest filled slot
   bool broken = true;
   int order = 0;
-  const bool try_fast = !NORING && live && ncsr == 0 && B > 0 && P.r_wp != nullptr;
+  const bool try_fast = live && ncsr == 0 && B > 0 && P.r_wp != nullptr;
   if (try_fast) {
-    // (B > 0 here; the ring-less copies, whose B is the constant 0, compile no division)
-    const int w = P.b_pow2 || NORING ? static_cast<int>(wp & (B - 1)) : static_cast<int>(wp % B);
+    const int w = P.b_pow2 ? static_cast<int>(wp & (B - 1)) : static_cast<int>(wp % B);
     order = sl - w < 0 ? sl - w + B : sl - w;
     const uint64_t filled = (__ballot(sl < B && rid != -1) >> (h << lg)) & submask;
     const int empty = B - __popcll(filled);
@@ -651,10 +642,7 @@ void recent_fused(Params P) {
   }
   wave_sync();
   if (q >= 0) {
-    if (NORING) {
-      // no ring: the ncsr <= K CSR entries, time-ascending, are the last positions
-      for (int j = sl; j < ncsr; j += Bp) emit(K - ncsr + j, P.c_ids[cbase + j], P.c_times[cbase + j], j);
-    } else if (!fast) {
+    if (!fast) {
       // counting rank by (time, CSR-before-ring, candidate index).  The CSR
       // window is time-ascending with ties in CSR order, so CSR entry c has
       // exactly c such predecessors among the CSR entries and only the ring
@@ -1428,8 +1416,9 @@ int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args
   P.status = a->status;
 
   const int K = a->k;
-  // LDS candidates: the CSR window and the ring slots; a tiled launch without a
-  // ring (the NORING copies) emits the window straight from memory instead
+  // LDS candidates: the CSR window and the ring slots.  A tiled launch without a
+  // ring runs csr_window or csr_split (below), which stage no candidates; the
+  // split rule sizes it as a recent_fused launch without them
   L.noring = ring == nullptr && mode == TGX_PLAN_TILES;
   P.cand_cap = L.noring ? 0 : (P.has_csr ? K : 0) + P.B;
   auto wave_lds = [&](int m) {
@@ -1619,10 +1608,7 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
                          reinterpret_cast<const void*>(recent_fused<16, 2, true>),
                          reinterpret_cast<const void*>(recent_fused<16, 4, true>),
                          reinterpret_cast<const void*>(recent_fused<4, 0, true>),
-                         reinterpret_cast<const void*>(recent_fused<2, 0, true>),
-                         reinterpret_cast<const void*>(recent_fused<16, 0, true, true>),
-                         reinterpret_cast<const void*>(recent_fused<4, 0, true, true>),
-                         reinterpret_cast<const void*>(recent_fused<2, 0, true, true>)};
+                         reinterpret_cast<const void*>(recent_fused<2, 0, true>)};
     for (const void* f : fns)
       (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     (void)hipGetLastError();
@@ -1666,13 +1652,6 @@ extern "C" int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_re
       else
         launch(csr_split<2, false>);
     }
-  } else if (L.noring) {
-    if (L.vec == 16)
-      launch(recent_fused<16, 0, true, true>);
-    else if (L.vec == 4)
-      launch(recent_fused<4, 0, true, true>);
-    else
-      launch(recent_fused<2, 0, true, true>);
   } else if (L.vec == 16) {
     if (L.nreg == 2)
       pick(recent_fused<16, 2, true>, recent_fused<16, 2, false>);
