@@ -18,6 +18,7 @@ outputs must equal the GPU's).
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import sys
@@ -31,6 +32,23 @@ sys.path.insert(0, str(ROOT))
 
 PEAK_HBM_GBS = 8000.0
 METRIC = "prepared queries/sec (K-nbr gather+time-enc); achieved HBM GB/s % of peak"
+
+
+class _no_gc:
+    """Python's cyclic garbage collector off inside a host-timed region (as timeit
+    does): a collection triggered by the steps' allocations lands at a random step
+    and measured as 1-2 us per step of spread over a 20-step window.  No collection
+    is forced before (a full one leaves the host's caches cold for the first
+    steps: 27 -> 34 us per step over 20); the collector is back on afterwards."""
+
+    def __enter__(self):
+        self.was = gc.isenabled()
+        gc.disable()
+
+    def __exit__(self, *exc):
+        if self.was:
+            gc.enable()
+        return False
 
 
 def bytes_per_batch(cfg, Q: int, V: int, pairs: int, d_t: int = 100) -> int:
@@ -513,11 +531,12 @@ def run_csr_prepare(a, log) -> None:
         for i in range(W):
             pb = pipe.prepare(raws[i])
         torch.cuda.synchronize()
-        h0 = time.perf_counter()
-        for i in range(W, W + S):
-            pb = pipe.prepare(raws[i])
-        torch.cuda.synchronize()
-        step_us = (time.perf_counter() - h0) / S * 1e6
+        with _no_gc():
+            h0 = time.perf_counter()
+            for i in range(W, W + S):
+                pb = pipe.prepare(raws[i])
+            torch.cuda.synchronize()
+            step_us = (time.perf_counter() - h0) / S * 1e6
         del pb
         # kernel time per launch: the first R prepare launches, graph-replayed
         args = pipe.launch_args(raws[0])
@@ -690,18 +709,19 @@ def main():
     host_prep = host_adv = 0.0
     total_q = 0
     torch.cuda.synchronize()
-    t_start = time.perf_counter()
-    for i in range(W, W + K):
-        h0 = time.perf_counter()
-        pb = pipe.prepare(raws[i])
-        h1 = time.perf_counter()
-        g.advance(raws[i].src, raws[i].dst, raws[i].time, raws[i].edge_feat)
-        host_adv += time.perf_counter() - h1
-        host_prep += h1 - h0
-        total_q += lens[i] * cfg.queries_per_event
-    del pb
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t_start
+    with _no_gc():
+        t_start = time.perf_counter()
+        for i in range(W, W + K):
+            h0 = time.perf_counter()
+            pb = pipe.prepare(raws[i])
+            h1 = time.perf_counter()
+            g.advance(raws[i].src, raws[i].dst, raws[i].time, raws[i].edge_feat)
+            host_adv += time.perf_counter() - h1
+            host_prep += h1 - h0
+            total_q += lens[i] * cfg.queries_per_event
+        del pb
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t_start
 
     # roofline window: the prepare kernels of the next R batches of the stream on the
     # ring state the timed region left, captured once in a HIP graph and replayed
@@ -800,6 +820,8 @@ def main():
                                + (", co-occurrence" if cfg.co_occurrence else ""),
                    "batches_timed": f"{W}..{W + K - 1}", "events_per_batch": cfg.batch},
         "host_us_per_step": {"prepare": host_prep / K * 1e6, "advance": host_adv / K * 1e6},
+        "timed_region": "prepare + advance of every batch, inputs resident in HBM, Python's "
+                        "cyclic GC off, synchronised on both sides",
         "prepare_kernel": {"us_per_launch": avg_launch_s * 1e6, "launches": n_launch,
                            "batches": f"{W + K}..{total - 1}",
                            "queries_per_s": sum(rQs) / (kern_ms / 1e3) if kern_ms else None,
