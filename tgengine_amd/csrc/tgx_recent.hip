@@ -744,10 +744,15 @@ void recent_fused(Params P) {
         }
       }
     } else {
-      for (int idx0 = part * kWave; idx0 < total; idx0 += kCopyDepth * ostride) {
-        VT v4[kCopyDepth];
+      // the event- and list-plan copies (co-occurrence launches: C2's 200-event
+      // batches) load 8 chunks per lane before storing them, the tiled ones 4 (8 made
+      // C2's gather 12.95 -> 12.22 us and C5's 1% faster, C1's 8.3 -> 8.9 and C4's
+      // 367 -> 381 us slower)
+      constexpr int kDepth = TILES ? kCopyDepth : 2 * kCopyDepth;
+      for (int idx0 = part * kWave; idx0 < total; idx0 += kDepth * ostride) {
+        VT v4[kDepth];
 #pragma unroll
-        for (int u = 0; u < kCopyDepth; ++u) {
+        for (int u = 0; u < kDepth; ++u) {
           const int idx = idx0 + u * ostride + lane;
           v4[u] = VT{};
           if (idx < total) {
@@ -763,7 +768,7 @@ void recent_fused(Params P) {
           }
         }
 #pragma unroll
-        for (int u = 0; u < kCopyDepth; ++u) {
+        for (int u = 0; u < kDepth; ++u) {
           const int idx = idx0 + u * ostride + lane;
           if (idx < total) put<true>(of + idx, v4[u]);
         }
