@@ -256,3 +256,64 @@ def test_csr_split_recent_matches_oracle(d, bf16, K, Q):
     assert np.array_equal(_feats_u8(r.edge_feats), o.feats.view(np.uint8))
     assert np.array_equal(r.edge_ids.cpu().numpy(), o.eids)
     assert g.status()["bad_query_nodes"] == int(bad.sum())
+
+
+def _special_graph(seed, N, d, E=6000):
+    """A frozen CSR whose times include -0.0 / +0.0 ties, ±inf and NaN (NaN sorts
+    after every time, -0.0 ties +0.0 in build order), built from events that are
+    not time-ordered (the general build)."""
+    rng = np.random.default_rng(seed)
+    src = np.minimum(rng.zipf(1.5, E) - 1, N - 1).astype(np.int64)
+    dst = rng.integers(0, N, E)
+    time = rng.choice(np.array([-0.0, 0.0, -np.inf, np.inf, np.nan, -2.5, 1.0, 3.0, 7.5]), E)
+    time = np.where(rng.random(E) < 0.5, np.floor(rng.uniform(-10, 10, E)), time)
+    f = rng.standard_normal((E, d)).astype(np.float32)
+    g = TemporalGraph(N, edge_feat_dim=d, device="cuda", buffer_size=8, track_edge_ids=True)
+    events = []
+    for lo in range(0, E, 1500):
+        hi = min(E, lo + 1500)
+        g.advance(cu(src[lo:hi]), cu(dst[lo:hi]), cu(time[lo:hi]), cu(f[lo:hi]))
+        events.append((src[lo:hi], dst[lo:hi], time[lo:hi], f[lo:hi], lo))
+    g.freeze_csr()
+    assert not g._csr_time_sorted  # the general build ran
+    return rng, g, O.csr_freeze(N, d, events)
+
+
+@pytest.mark.parametrize("K,Q", [(20, 3000), (20, 300), (64, 3000), (512, 200)])
+def test_ring_less_special_times(K, Q):
+    """csr_window (K <= 64, more than 2,048 queries) and csr_split (the rest) on
+    windows holding ±0, ±inf and NaN times, queried at ±0, ±inf, NaN and grid times:
+    ids, times, rows, masks and edge ids equal to the oracle's."""
+    N, d = 60, 4
+    rng, g, csr = _special_graph(70 + K, N, d)
+    nodes = rng.integers(-1, N, Q)
+    qt = rng.choice(np.array([-0.0, 0.0, -np.inf, np.inf, np.nan, 1.0, 3.0, 100.0]), Q)
+    qt = np.where(rng.random(Q) < 0.5, np.floor(rng.uniform(-12, 12, Q)), qt)
+    r = g.recent(cu(nodes), cu(qt), K)
+    o = O.recent(nodes, qt, K, csr, None, d)
+    assert o.mask.any() and not o.mask.all()
+    assert np.array_equal(r.neighbor_ids.cpu().numpy(), o.ids)
+    assert np.array_equal(r.timestamps.cpu().numpy().view(np.int64), o.times.view(np.int64))
+    assert np.array_equal(r.mask.cpu().numpy(), o.mask)
+    assert np.array_equal(r.edge_feats.cpu().numpy(), o.feats)
+    assert np.array_equal(r.edge_ids.cpu().numpy(), o.eids)
+
+
+def test_ring_less_routing_boundaries():
+    """Every side of the host's routing of ring-less launches: K = 1, 15, 16, 17, 31,
+    32, 33, 63, 64, 65, 128, 129 at 2,048 and 2,049 queries (csr_split with a split,
+    csr_window with none) and rows of 16, 48, 64 and 80 bytes (80: csr_split even
+    without a split), each against the oracle."""
+    N = 300
+    for d in (4, 12, 16, 20):
+        rng, g, csr, tmax, fdt = _stream(80 + d, N, d, False, E=12000)
+        for K in (1, 15, 16, 17, 31, 32, 33, 63, 64, 65, 128, 129):
+            for Q in (2048, 2049):
+                nodes, qt = _queries(rng, N, Q, tmax)
+                r = g.recent(cu(nodes), cu(qt), K)
+                o = O.recent(nodes, qt, K, csr, None, d, fdt)
+                case = (d, K, Q)
+                assert np.array_equal(r.neighbor_ids.cpu().numpy(), o.ids), case
+                assert np.array_equal(r.timestamps.cpu().numpy().view(np.int64), o.times.view(np.int64)), case
+                assert np.array_equal(r.mask.cpu().numpy(), o.mask), case
+                assert np.array_equal(r.edge_feats.cpu().numpy(), o.feats), case
