@@ -483,8 +483,9 @@ void recent_fused(Params P) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
   if (static_cast<int>(blockIdx.x) < P.plan_blocks) {
-    // the plan touches only the ring's scratch, never the arrays gathered here
-    plan_block(P.pl, blockIdx.x, *reinterpret_cast<PlanLds*>(smem));
+    // the plan reads the ring's write positions and writes only its scratch and
+    // the workspace, never the arrays gathered here
+    plan_block_ordered(P.pl, blockIdx.x, smem);
     return;
   }
   const int64_t g = static_cast<int64_t>(blockIdx.x) - P.plan_blocks;
@@ -1578,7 +1579,7 @@ int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args
   L.fuse_plan = L.want_plan && plan_fused_ok(L.pl);
   P.pl = L.pl;
   P.plan_blocks = L.fuse_plan ? static_cast<int>((L.pl.n + kWave * waves - 1) / (kWave * waves)) : 0;
-  L.lds = L.fuse_plan ? std::max(lds, sizeof(PlanLds)) : lds;
+  L.lds = L.fuse_plan ? std::max(lds, plan_lds_bytes(kWave * waves)) : lds;
   L.blocks = nblocks + P.plan_blocks;
   if (L.blocks >= (int64_t(1) << 31)) return fail(TGX_ERR_LIMIT, "tgx_recent: grid too large");
   L.threads = kWave * waves;

@@ -9,38 +9,30 @@
 // entry with e later same-node entries is kept iff e < kept = min(c, B) and
 // lands in slot (write_pos + kept - 1 - e) % B.
 //
-// Both designs below take per-node tickets from node-indexed counters owned by
-// the ring (zero between calls); equal nodes of a workgroup are first
-// aggregated in an LDS hash table, so a node costs one global atomic per
-// workgroup however hot it is.  Tickets number a node's entries in no
-// particular order; ranking by entry index happens when the node is written.
-//
 // Batches of up to kFastMaxEntries entries: two launches.
-//   plan   : tickets; ticket t < kListCap stores the entry in the node's list
-//            lst[u][t] (ring scratch); the ticket-1 entry appends the node to
-//            the group list, the ticket-kListCap entry to the large-group
-//            list.  The two cursors share one 64-bit word: one atomic per
-//            workgroup.
-//   commit : singletons (c == 1) are written directly; a group of
-//            c <= kListCap is ranked by one wavefront from its node list; a
-//            larger group by a workgroup that reads the plan's int32 node of
-//            every entry from the top of the batch down, kTopChunk entries at a
-//            time, and ranks the node's entries until the kept ones are found.  Every role
-//            starts its loads before it knows whether it has work, so a role
-//            costs two or three memory round trips.  The first small-group workgroup reports the
-//            diagnostics and clears the other cursor set for the next plan
-//            (two sets alternate).
-// Larger batches: four launches, whose lists are sized after counting.
-//   count  : tickets.
+//   plan   : every entry's rank among its node's entries in entry order, from
+//            its workgroup's scan of the batch's node ids (entries of its nodes
+//            before and after its range) and wavefront ballots over its own
+//            range (tgx_ring_plan.h); the entry's record holds its ring slot if
+//            it is kept (rank >= c - kept) and, on the node's last entry, the
+//            node's new write position.  No workgroup waits for another.
+//   commit : one copy per entry: the record, node, neighbour, time and row in
+//            one round trip, then the kept entries' stores.
+// Larger batches: four launches, with per-node tickets from node-indexed
+// counters owned by the ring (zero between calls; equal nodes of a workgroup
+// are first aggregated in an LDS hash table, so a node costs one global atomic
+// per workgroup however hot it is) and lists sized after counting.
+//   count  : tickets, in no particular order.
 //   groups : the ticket-0 entry of every node seen more than once reserves
 //            a contiguous list of c slots and a group id, small (c <= 64)
 //            or large (one atomic per wave, offsets by a wave scan).
 //   fill   : list[base[u] + ticket] = entry index.
-//   commit : singletons as above; a small group is ranked by one wavefront in
-//            registers, a large group by a whole workgroup over bitmap
-//            windows walked down from the top of the batch.
-// Every path writes the kept entries, restores count[u] to zero and advances
-// write_pos.  Feature rows move as 16-byte vectors when the row allows it.
+//   commit : singletons (c == 1) are written directly; a small group is ranked
+//            by one wavefront in registers, a large group by a whole workgroup
+//            over bitmap windows walked down from the top of the batch; the
+//            counters are restored to zero.
+// Every path writes the kept entries and advances write_pos.  Feature rows move
+// as 16-byte vectors when the row allows it.
 #include "tgx_ring_plan.h"
 
 #include <algorithm>
@@ -58,14 +50,6 @@ constexpr int kWinWords = kWinBits / 32;       // 256 words = 1 KB
 static_assert(kWinWords == kThreads, "one bitmap word per thread");
 constexpr int64_t kSmallGroupBlocks = 256;  // commit blocks for small groups (4 waves each)
 constexpr int64_t kLargeGroupBlocks = 64;   // four-launch commit blocks for large groups
-// the two-launch commit runs 512-thread workgroups, so that the large-group
-// role's step of kTopChunk entries is kTopRows 16-byte loads per thread
-constexpr int kFastThreads = 512;
-constexpr int kFastWaves = kFastThreads / kWave;
-constexpr int kTopRows = 4;                 // 16-byte loads (4 entry nodes each) in flight per thread
-constexpr int kTopChunk = 4 * kTopRows * kFastThreads;  // entries per top-down step
-constexpr int64_t kFastLargeBlocks = 128;   // two-launch commit blocks for large groups
-constexpr int64_t kFastSmallBlocks = 128;   // two-launch commit blocks for small groups (8 waves each)
 
 // (write_pos + off) % B for write_pos >= 0, 0 <= off < B
 __device__ __forceinline__ int64_t ring_slot(int64_t w, int off, int B) {
@@ -144,8 +128,8 @@ __global__ __launch_bounds__(kThreads) void append_count(PlanParams P) {
 
 // ---- two-launch 1. plan -------------------------------------------------------
 __global__ __launch_bounds__(kThreads) void fast_plan(PlanParams P) {
-  __shared__ PlanLds L;
-  plan_block(P, blockIdx.x, L);
+  __shared__ __align__(16) uint8_t smem[plan_lds_bytes(kThreads)];
+  plan_block_ordered(P, blockIdx.x, smem);
 }
 
 // ---- four-launch 2. groups --------------------------------------------------------------
@@ -390,57 +374,9 @@ __device__ __forceinline__ void commit_singletons(const AppendParams& P, int blk
   }
 }
 
-// copy the kept rows R[0..kept) (kept <= kListCap) of node u (row r -> slot
-// (w + kept - 1 - r) % B) by one wavefront: lanes 8r .. 8r + 7 take row r, lane
-// 8r + j its chunks j, j + 8, ..., kSmallDepth of them per round, so a row of up
-// to 8 kSmallDepth chunks costs one round trip
-constexpr int kSmallDepth = 8;
-static_assert(kListCap * 8 == kWave, "eight lanes per listed row");
-template <int VEC>
-__device__ __forceinline__ void write_listed(const AppendParams& P, const int32_t* R, int64_t u,
-                                             int kept, int64_t w) {
-  using V = typename VecT<VEC>::T;
-  const int lane = threadIdx.x & (kWave - 1);
-  const int r = lane >> 3;
-  const int j = lane & 7;
-  if (r >= kept) return;
-  const int nv = static_cast<int>(P.row_bytes / VEC);
-  const int64_t i = R[r];
-  const int64_t e = i < P.b ? i : i - P.b;
-  const int64_t slot = u * P.B + ring_slot(w, kept - 1 - r, P.B);
-  const V* srow = reinterpret_cast<const V*>(P.feat + e * P.row_bytes);
-  V* drow = reinterpret_cast<V*>(P.feats + slot * P.row_bytes);
-  int32_t id = 0;
-  double tm = 0.0;
-  if (j == 0) {
-    id = static_cast<int32_t>(i < P.b ? P.dst[e] : P.src[e]);
-    tm = P.time[e];
-  }
-  for (int c0 = j; c0 < nv || j == 0; c0 += 8 * kSmallDepth) {
-    V v[kSmallDepth];
-#pragma unroll
-    for (int k = 0; k < kSmallDepth; ++k) {
-      const int c = c0 + 8 * k;
-      v[k] = (P.feat != nullptr && c < nv) ? srow[c] : V{};
-    }
-    if (j == 0 && c0 == 0) {
-      P.ids[slot] = id;
-      P.times[slot] = tm;
-      if (P.eids != nullptr) P.eids[slot] = P.eid_base + e;
-    }
-#pragma unroll
-    for (int k = 0; k < kSmallDepth; ++k) {
-      const int c = c0 + 8 * k;
-      if (c < nv) drow[c] = v[k];
-    }
-    if (c0 + 8 * kSmallDepth >= nv) break;
-  }
-}
-
 // one group of c <= kWave entries listed in idx (lane j < c holds one entry
-// index), ranked in registers by one wavefront, then written (LISTED: c <=
-// kListCap, copied by write_listed)
-template <int VEC, bool LISTED = false>
+// index), ranked in registers by one wavefront, then written
+template <int VEC>
 __device__ __forceinline__ void commit_small(const AppendParams& P, int64_t u, int c, int32_t idx,
                                              int64_t w, int32_t* R) {
   const int lane = threadIdx.x & (kWave - 1);
@@ -449,10 +385,7 @@ __device__ __forceinline__ void commit_small(const AppendParams& P, int64_t u, i
   for (int j = 0; j < c; ++j) e += __shfl(idx, j, kWave) > idx;
   if (lane < c && e < kept) R[e] = idx;
   wave_sync_lds();
-  if constexpr (LISTED)
-    write_listed<VEC>(P, R, u, kept, w);
-  else
-    write_kept<VEC>(P, R, u, kept, w, lane, kWave);
+  write_kept<VEC>(P, R, u, kept, w, lane, kWave);
   if (lane == 0) {
     P.wp[u] = w + kept;
     P.cnt[u] = 0;
@@ -499,218 +432,77 @@ __global__ __launch_bounds__(kThreads) void append_commit(AppendParams P) {
 }
 
 // ---- two-launch 2. commit -------------------------------------------------------
-// The plan's node of every entry, four per 16-byte load, top-down: row r of
-// thread t holds entries 4q .. 4q + 3 of q = hi4 / 4 - 1 - (r kFastThreads + t)
-// (hi4 a multiple of 4; the node array is padded to whole 256-byte lines, and
-// indices >= n are masked by the caller), so each row covers 4 kFastThreads
-// consecutive entries in descending order.
-__device__ __forceinline__ void load_top(const AppendParams& P, int64_t hi4,
-                                         int4 (&nd)[kTopRows]) {
-#pragma unroll
-  for (int r = 0; r < kTopRows; ++r) {
-    const int64_t q = hi4 / 4 - 1 - (static_cast<int64_t>(r) * kFastThreads + threadIdx.x);
-    nd[r] = q >= 0 ? reinterpret_cast<const int4*>(P.ticket)[q] : make_int4(-1, -1, -1, -1);
-  }
-}
-
-// LDS of the top-down ranking: the match count of every (row, wavefront)
-struct TopLds {
-  int32_t tot[kTopRows][kFastWaves];
-};
-static_assert(kTopRows * kFastWaves <= kWave, "one lane per (row, wavefront) count");
-
-// set bits of the wave mask b below this lane
-__device__ __forceinline__ int lanes_below(uint64_t b) {
-  return static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(b >> 32),
-                                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(b), 0u)));
-}
-
-// One large group (c > kListCap) by the whole workgroup.  Its kept entries are
-// its last kept = min(c, B) in the batch: the plan's node array is read from the
-// top down, kTopChunk entries per step, and the entry with e later entries of
-// node u is ranked from the match counts (matches in earlier steps, earlier
-// rows, lower wavefronts, lower lanes, and this lane's higher entries).  Within
-// a wavefront, three ballots of the bits of every lane's count give the
-// matches of the lower lanes (mbcnt) and the wavefront's total, so only the
-// (row, wavefront) totals pass through LDS.  The first step (nd) is loaded by
-// the caller before u is known.  Steps end once B entries are found (kept = B)
-// or the batch is exhausted (kept = c), so the node's counter is not read.
+// One entry per tpe lanes (one 16-byte chunk of its row each, as the four-launch
+// singletons): the plan's record of the entry (its ring slot or -1, and the
+// node's new write position on the node's last entry), the entry's node,
+// neighbour, time and feature row arrive in one round trip; a kept entry is
+// written to its slot.  Rows longer than kKeptDepth chunks per lane continue in
+// rounds of kKeptDepth loads, then stores.  Workgroup 0 reports and clears the
+// plan's diagnostics.
 template <int VEC>
-__device__ __forceinline__ void fast_large(const AppendParams& P, int64_t u, int4 (&nd)[kTopRows],
-                                           int32_t* R, TopLds& T) {
-  const int wv = threadIdx.x / kWave;
-  const int lane = threadIdx.x & (kWave - 1);
-  const int t = threadIdx.x;
-  const int32_t u32 = static_cast<int32_t>(u);
-  const int n32 = static_cast<int>(P.n);  // < 2^30 entries, so entry indices fit in int
-  int carry = 0;
-  for (int hi4 = (n32 + 3) & ~3;;) {  // workgroup-uniform
-    // m4[r] bit s: entry 4q + 3 - s of row r is node u (s = 0 is the highest);
-    // below[r]: matches of the lower lanes of this wavefront in row r
-    uint32_t m4[kTopRows];
-    int below[kTopRows];
+__global__ __launch_bounds__(kThreads) void kept_commit(AppendParams P) {
+  using V = typename VecT<VEC>::T;
+  if (blockIdx.x == 0 && threadIdx.x == 0) commit_diagnostics(P, kCtlKTime, kCtlKBad);
+  const int nv = static_cast<int>(P.row_bytes / VEC);
+  const int tpe = 1 << P.tpe_log2;
+  const int epb = kThreads >> P.tpe_log2;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * epb + (threadIdx.x >> P.tpe_log2);
+  const int l = threadIdx.x & (tpe - 1);
+  if (i >= P.n) return;
+  const longlong2 kr = reinterpret_cast<const longlong2*>(P.krec)[i];
+  const int64_t e = i < P.b ? i : i - P.b;
+  const int64_t u = entry_node(P.src, P.dst, i, P.b);
+  const V* srow = reinterpret_cast<const V*>(P.feat + e * P.row_bytes);
+  V v[kKeptDepth];
 #pragma unroll
-    for (int r = 0; r < kTopRows; ++r) {
-      const int top = hi4 - 4 * (r * kFastThreads + t) - 1;  // 4q + 3
-      uint32_t m = static_cast<uint32_t>(nd[r].w == u32) | static_cast<uint32_t>(nd[r].z == u32) << 1 |
-                   static_cast<uint32_t>(nd[r].y == u32) << 2 | static_cast<uint32_t>(nd[r].x == u32) << 3;
-      // entries n .. hi4 - 1 (at most 3, in the topmost load of the first step)
-      // hold stale nodes: entry top - s is valid iff s >= top - n + 1
-      if (top >= n32) m &= (0xfu << (top - n32 + 1)) & 0xfu;
-      m4[r] = m;
-      const int cnt = __popc(m);
-      int bl = 0, tot = 0;
+  for (int k = 0; k < kKeptDepth; ++k) {
+    const int c = l + k * tpe;
+    v[k] = (P.feat != nullptr && c < nv) ? srow[c] : V{};
+  }
+  int32_t other = 0;
+  double tm = 0.0;
+  if (l == 0) {
+    other = static_cast<int32_t>(i < P.b ? P.dst[e] : P.src[e]);
+    tm = P.time[e];
+  }
+  if (kr.x >= 0) {
+    const int64_t slot = u * P.B + kr.x;
+    V* drow = reinterpret_cast<V*>(P.feats + slot * P.row_bytes);
 #pragma unroll
-      for (int k = 0; k < 3; ++k) {
-        const uint64_t b = __ballot((cnt >> k) & 1);
-        bl += lanes_below(b) << k;
-        tot += __popcll(b) << k;
+    for (int k = 0; k < kKeptDepth; ++k) {
+      const int c = l + k * tpe;
+      if (c < nv) drow[c] = v[k];
+    }
+    for (int c0 = l + kKeptDepth * tpe; c0 < nv; c0 += kKeptDepth * tpe) {
+#pragma unroll
+      for (int k = 0; k < kKeptDepth; ++k) {
+        const int c = c0 + k * tpe;
+        v[k] = (P.feat != nullptr && c < nv) ? srow[c] : V{};
       }
-      below[r] = bl;
-      if (lane == 0) T.tot[r][wv] = tot;
-    }
-    __syncthreads();
-    // lane l < kTopRows kFastWaves: the count of (row l / kFastWaves,
-    // wavefront l % kFastWaves); an exclusive scan in that order gives bases
-    const int x = lane < kTopRows * kFastWaves ? T.tot[lane / kFastWaves][lane % kFastWaves] : 0;
-    // inclusive scan over lanes [0, 32) in registers (DPP): shifts by 1, 2, 4
-    // and 8 lanes within each 16-lane row, then row 0's last lane into row 1
-    static_assert(kTopRows * kFastWaves == 32, "the scan covers two DPP rows");
-    int incl = x;
-    incl += __builtin_amdgcn_update_dpp(0, incl, 0x111, 0xf, 0xf, false);  // row_shr:1
-    incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xf, 0xf, false);  // row_shr:2
-    incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xf, 0xf, false);  // row_shr:4
-    incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xf, 0xf, false);  // row_shr:8
-    incl += __builtin_amdgcn_update_dpp(0, incl, 0x142, 0xa, 0xf, false);  // row_bcast:15, rows 1, 3
-    // the lane index is wavefront-uniform: read the bases with readlane
-    const int step_total = __builtin_amdgcn_readlane(incl, kTopRows * kFastWaves - 1);
-    const int exc = incl - x;
-    const int wvu = __builtin_amdgcn_readfirstlane(wv);
 #pragma unroll
-    for (int r = 0; r < kTopRows; ++r) {
-      int e = carry + __builtin_amdgcn_readlane(exc, r * kFastWaves + wvu) + below[r];
-      uint32_t m = m4[r];
-      const int top = hi4 - 4 * (r * kFastThreads + t) - 1;
-      // only ranks below B are kept
-      for (; m != 0u && e < P.B; m &= m - 1, ++e) R[e] = top - __builtin_ctz(m);
-    }
-    carry += step_total;
-    hi4 -= kTopChunk;
-    __syncthreads();  // T is rewritten by the next step; R is complete at the end
-    if (carry >= P.B || hi4 <= 0) break;
-    load_top(P, hi4, nd);
-  }
-  const int kept = carry < P.B ? carry : P.B;
-  // the write position is loaded here, not with the node: the step loop's
-  // first wait would otherwise wait for it too (one round trip more); here it
-  // shares the round trip of the kept rows' loads
-  const int64_t w = P.wp[u];
-  write_kept<VEC>(P, R, u, kept, w, t, kFastThreads);
-  if (t == 0) {
-    P.wp[u] = w + kept;
-    P.cnt[u] = 0;
-  }
-  __syncthreads();  // the next group rewrites R
-}
-
-// the plan's cursor word (groups | large counts) of ctl words 8-15 (c0, c1:
-// both cursor sets, phase_next, phase_cur)
-static_assert(kCtlPhaseCur - kCtlFCursor - 4 == 1, "phase_cur is word 1 of c1");
-__device__ __forceinline__ uint64_t plan_cursor(u32x4 c0, u32x4 c1) {
-  const uint32_t ph = c1.y & 1u;
-  return ph == 0 ? (static_cast<uint64_t>(c0.y) << 32 | c0.x) : (static_cast<uint64_t>(c0.w) << 32 | c0.z);
-}
-
-// the first small-group workgroup of a commit (gb >= 1 always), once the
-// cursor words are in: report the plan's diagnostics, clear them, clear the
-// other cursor set (its plan is committed) and hand it to the next plan
-__device__ __forceinline__ void fast_diagnostics(const AppendParams& P, uint32_t phase_cur) {
-  const int ph = static_cast<int>(phase_cur & 1u);
-  const u32x4 dg = *reinterpret_cast<const u32x4*>(P.ctl + kCtlFDiag);
-  const int time_flag = static_cast<int>(ph == 0 ? dg[0] : dg[2]);
-  const int bad = static_cast<int>(ph == 0 ? dg[1] : dg[3]);
-  *reinterpret_cast<uint64_t*>(P.ctl + kCtlFCursor + 2 * (1 - ph)) = 0;
-  P.ctl[kCtlPhaseNext] = 1 - ph;
-  if (P.status != nullptr) {
-    if (bad != 0) atomicAdd(&P.status[TGX_ST_BAD_EVENT_NODE], bad);
-    if (time_flag == 0) atomicAdd(&P.status[TGX_ST_KEY_COLLISION], 1);
-  }
-  P.ctl[kCtlFDiag + 2 * ph] = 0;
-  P.ctl[kCtlFDiag + 2 * ph + 1] = 0;
-}
-
-// blocks [0, ga): singletons; [ga, ga+gb): groups of c <= kListCap, one per
-// wavefront; [ga+gb, ...): larger groups, one per workgroup.  The ctl words
-// (cursors, phase) are loaded first, and every role issues its own first loads
-// before it uses them, so they cost one round trip together: loads and their
-// wait counter are in order, and a wait for a younger load is a wait for all.
-template <int VEC>
-__global__ __launch_bounds__(kFastThreads) void fast_commit(AppendParams P) {
-  __shared__ int32_t rows[kFastWaves][TGX_MAX_SLOTS];
-  __shared__ TopLds top;
-  const int blk = static_cast<int>(blockIdx.x);
-  const int wv = threadIdx.x / kWave;
-  const int lane = threadIdx.x & (kWave - 1);
-  // ctl words 8-15 in one round trip: both cursor sets, phase_next, phase_cur
-  // (this launch writes only the other set and phase_next, which it does not use)
-  const u32x4 c0 = *reinterpret_cast<const u32x4*>(P.ctl + kCtlFCursor);
-  const u32x4 c1 = *reinterpret_cast<const u32x4*>(P.ctl + kCtlFCursor + 4);
-  if (blk < P.ga) {
-    commit_singletons<VEC>(P, blk);
-  } else if (blk < P.ga + P.gb) {
-    // the first group id of this wavefront is read with the cursor (in bounds of
-    // the n/2 + 1 list), so a group costs three round trips
-    const int gstride = P.gb * kFastWaves;
-    int gid = (blk - P.ga) * kFastWaves + wv;
-    int64_t u = gid <= P.n / 2 ? P.groups[gid] : 0;
-    const int ngroups = field(plan_cursor(c0, c1), kFGroups);
-    if (blk == P.ga && threadIdx.x == 0) fast_diagnostics(P, c1.y);
-    for (; gid < ngroups; gid += gstride) {  // wave-uniform
-      const int c = P.cnt[u];
-      const int64_t w = P.wp[u];
-      const int32_t idx = lane < kListCap ? P.lst[u * kListCap + lane] : -1;
-      const int64_t u_next = gid + gstride < ngroups ? P.groups[gid + gstride] : 0;
-      // a larger group has its own role; its counter reads c > kListCap, or 0
-      // once that role restored it
-      if (c >= 2 && c <= kListCap) commit_small<VEC, true>(P, u, c, lane < c ? idx : -1, w, rows[wv]);
-      u = u_next;
-    }
-  } else {
-    // the group's node and the top of the batch are read with the cursor
-    // (gid < n / (kListCap + 1) + 1, the large list's length)
-    const int gstride = static_cast<int>(gridDim.x) - P.ga - P.gb;
-    const int64_t hi4 = (P.n + 3) & ~int64_t(3);
-    int gid = blk - P.ga - P.gb;
-    int64_t u = P.large[gid];
-    int4 nd[kTopRows];
-    load_top(P, hi4, nd);
-    const int nlarge = field(plan_cursor(c0, c1), kFLarge);
-    for (; gid < nlarge; gid += gstride) {  // workgroup-uniform
-      fast_large<VEC>(P, u, nd, rows[0], top);
-      if (gid + gstride < nlarge) {
-        u = P.large[gid + gstride];
-        load_top(P, hi4, nd);
+      for (int k = 0; k < kKeptDepth; ++k) {
+        const int c = c0 + k * tpe;
+        if (c < nv) drow[c] = v[k];
       }
     }
+    if (l == 0) {
+      P.ids[slot] = other;
+      P.times[slot] = tm;
+      if (P.eids != nullptr) P.eids[slot] = P.eid_base + e;
+    }
   }
+  if (l == 0 && kr.y >= 0) P.wp[u] = kr.y;
 }
 
 // ---- discard: restore the scratch of a planned batch without committing it ----
 __global__ __launch_bounds__(kThreads) void append_discard(PlanParams P, int two_launch) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   if (i == 0) {
-    if (two_launch) {
-      // the replacement plan takes the same set again (phase_next is unchanged)
-      const int ph = P.ctl[kCtlPhaseCur] & 1;
-      *reinterpret_cast<uint64_t*>(P.ctl + kCtlFCursor + 2 * ph) = 0;
-      P.ctl[kCtlFDiag + 2 * ph] = 0;
-      P.ctl[kCtlFDiag + 2 * ph + 1] = 0;
-    } else {
-      P.ctl[kCtlTimeOk] = 0;
-      P.ctl[kCtlBad] = 0;
-    }
+    P.ctl[two_launch ? kCtlKTime : kCtlTimeOk] = 0;
+    P.ctl[two_launch ? kCtlKBad : kCtlBad] = 0;
   }
-  if (i >= P.n) return;
+  // a two-launch plan leaves no per-node state
+  if (two_launch || i >= P.n) return;
   const int64_t u = entry_node(P.src, P.dst, i, P.b);
   if (u >= 0 && u < P.N) P.cnt[u] = 0;
 }
@@ -725,9 +517,11 @@ using namespace tgx;
 extern "C" size_t tgx_ring_append_workspace_size(int64_t b) {
   if (b <= 0) return 256;
   const size_t n = static_cast<size_t>(2 * b);
-  // ticket | four-launch lists | groups | large
+  // four-launch: ticket | lists | groups | large; two-launch (n <= kFastMaxEntries):
+  // and the plan's entry records
   return align256(n * 4) + align256(n * 4) + align256((n / 2 + 1) * 4) +
-         align256((n / (kListCap + 1) + 1) * 4);
+         align256((n / (kListCap + 1) + 1) * 4) +
+         (n <= static_cast<size_t>(kFastMaxEntries) ? align256(n * 16) : 0);
 }
 
 extern "C" size_t tgx_ring_scratch_size(int64_t num_nodes) {
@@ -771,7 +565,13 @@ int plan_setup(const char* who, const tgx_ring* ring, const int64_t* src, const 
   P.ticket = reinterpret_cast<int32_t*>(ws);
   P.list = reinterpret_cast<int32_t*>(ws + o_list);
   P.groups = reinterpret_cast<int32_t*>(ws + o_groups);
-  P.large = reinterpret_cast<int32_t*>(ws + o_groups + align256(static_cast<size_t>(n / 2 + 1) * 4));
+  const size_t o_large = o_groups + align256(static_cast<size_t>(n / 2 + 1) * 4);
+  P.large = reinterpret_cast<int32_t*>(ws + o_large);
+  P.krec = n <= kFastMaxEntries
+               ? reinterpret_cast<int64_t*>(ws + o_large + align256(static_cast<size_t>(n / (kListCap + 1) + 1) * 4))
+               : nullptr;
+  P.wpos = ring->write_pos;
+  P.B = ring->slots;
   return TGX_OK;
 }
 
@@ -846,14 +646,9 @@ int setup_append(const char* who, const tgx_ring* ring, const int64_t* src, cons
 template <int VEC>
 void launch_commit_vec(const AppendParams& P, hipStream_t stream) {
   if (plan_fused_ok(P)) {
-    // 512-thread workgroups: the roles' block counts for that size
-    AppendParams Q = P;
-    const int64_t epb = kFastThreads >> Q.tpe_log2;
-    Q.ga = static_cast<int>((Q.n + epb - 1) / epb);
-    Q.gb = static_cast<int>(std::min<int64_t>((Q.n / 2 + kFastWaves) / kFastWaves, kFastSmallBlocks));
-    const int64_t gc = std::min<int64_t>(Q.n / (kListCap + 1) + 1, kFastLargeBlocks);
-    hipLaunchKernelGGL(fast_commit<VEC>, dim3(static_cast<unsigned>(Q.ga + Q.gb + gc)),
-                       dim3(kFastThreads), 0, stream, Q);
+    const int64_t epb = kThreads >> P.tpe_log2;
+    hipLaunchKernelGGL(kept_commit<VEC>, dim3(static_cast<unsigned>((P.n + epb - 1) / epb)),
+                       dim3(kThreads), 0, stream, P);
   } else {
     const int64_t gc = std::min<int64_t>(P.n / (kWave + 1) + 1, kLargeGroupBlocks);
     hipLaunchKernelGGL(append_commit<VEC>, dim3(static_cast<unsigned>(P.ga + P.gb + gc)),
@@ -873,7 +668,7 @@ int launch_commit(const AppendParams& P, int vec, hipStream_t stream) {
       launch_commit_vec<2>(P, stream);
       break;
   }
-  return check_launch(plan_fused_ok(P) ? "fast_commit" : "append_commit");
+  return check_launch(plan_fused_ok(P) ? "kept_commit" : "append_commit");
 }
 
 }  // namespace

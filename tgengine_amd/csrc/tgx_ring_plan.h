@@ -2,11 +2,20 @@
 // kernels (tgx_ring.hip) and the plan role fused into the gather launch
 // (tgx_recent.hip).
 //
-// A plan reads the batch's src/dst/time and writes only the ring's scratch
-// (per-node counters, node lists, control words) and the caller's workspace,
-// never the ring arrays, so it can run in the same launch as a gather over the
-// ring.  Tickets number the entries of a node in no particular order; the
-// commit ranks them by entry index.
+// A plan reads the batch's src/dst/time and the ring's write positions, and
+// writes only the ring's scratch and the caller's workspace, never the ring
+// arrays, so it can run in the same launch as a gather over the ring.
+//
+// Batches of up to kFastMaxEntries entries (the two-launch update): the plan
+// gives every entry its rank among its node's entries in entry order, so it can
+// tell the kept ones and their final slots, and the commit is one copy per
+// entry.  Each plan workgroup takes blockDim consecutive entries; it learns how
+// many entries of each of its nodes come before and after its range by scanning
+// the batch's node ids (inputs, immutable during the launch: no workgroup
+// waits for another, and nothing passes between workgroups), and ranks its own
+// entries in index order by wavefront ballots.  Larger batches: tickets from
+// node-indexed counters, in no particular order, ranked when the node is
+// written (four launches).
 #pragma once
 
 #include "tgx_internal.h"
@@ -22,26 +31,13 @@ constexpr int kPlanHash = 1 << kPlanHashBits;
 static_assert(kPlanHash >= 2 * kPlanMaxThreads, "hash table at most half full");
 
 // ctl words (ring scratch).  Four-launch: cursors and diagnostics (words 0-4).
-// Two-launch: two cursor sets (uint64 at words 8 and 10: groups | large counts)
-// and two diagnostics pairs (time flag, bad count at 16 + 2p), used by alternate
-// plans.  A plan takes set p = phase_next and records it in
-// phase_cur; its commit reads set phase_cur, and its workgroup 0 clears the other
-// set (its plan is committed), reports and clears this plan's diagnostics and
-// sets phase_next to the other set, so nothing waits for the last workgroup.
+// Two-launch: the plan's diagnostics (words 16, 17: time flag, bad count), which
+// its commit reports and clears (a discard clears them).
 enum {
   kCtlCursor = 0, kCtlGroups = 1, kCtlTimeOk = 2, kCtlLarge = 3, kCtlBad = 4,
-  kCtlFCursor = 8,  // + 2p
-  kCtlPhaseNext = 12, kCtlPhaseCur = 13,
-  kCtlFDiag = 16    // + 2p: time flag, + 2p + 1: bad count
+  kCtlKTime = 16, kCtlKBad = 17
 };
 constexpr int kCtlWords = 32;
-// fields of the two-launch cursor word (every count is at most n <= 2^15)
-constexpr int kFieldBits = 21;
-constexpr uint64_t kFieldMask = (uint64_t(1) << kFieldBits) - 1;
-enum { kFGroups = 0, kFLarge = 1 };
-__host__ __device__ constexpr int field(uint64_t x, int f) {
-  return static_cast<int>((x >> (f * kFieldBits)) & kFieldMask);
-}
 
 // ring scratch: counters [N] | node lists [N, kListCap] | ctl (16-byte aligned)
 inline int64_t ctl_offset(int64_t num_nodes) {
@@ -55,13 +51,17 @@ struct PlanParams {
   int64_t b;
   int64_t n;       // 2b entries
   int64_t N;
-  int32_t* cnt;    // [N] per-node counters (zero between calls)
-  int32_t* lst;    // [N, kListCap] node lists
+  int32_t* cnt;    // [N] four-launch per-node counters (zero between calls)
+  int32_t* lst;    // [N, kListCap] four-launch node lists
   int32_t* ctl;    // [kCtlWords]
-  int32_t* ticket; // [n] four-launch tickets; two-launch: node of every entry (-1: bad)
+  int32_t* ticket; // [n] four-launch tickets
   int32_t* list;   // [n] four-launch lists
-  int32_t* groups; // [n/2 + 1] groups
-  int32_t* large;  // [n/(kListCap+1) + 1] large groups
+  int32_t* groups; // [n/2 + 1] four-launch groups
+  int32_t* large;  // [n/(kListCap+1) + 1] four-launch large groups
+  // two-launch
+  const int64_t* wpos;  // ring write positions (read)
+  int B;              // ring slots
+  int64_t* krec;      // [n, 2] per entry: ring slot (-1: not kept), new write position (-1: none)
 };
 
 struct PlanLds {
@@ -131,53 +131,144 @@ __device__ __forceinline__ void report_diagnostics(const PlanParams& P, int bad,
   }
 }
 
-// Two-launch plan of entries [block * blockDim.x, +blockDim.x) (blockDim.x a
-// multiple of kWave, at most kPlanMaxThreads; every thread of the workgroup
-// calls it), into cursor set phase_next.  Ticket t < kListCap stores the entry
-// in lst[u][t]; the ticket-1 entry appends u to the group list, the
-// ticket-kListCap entry to the large-group list.  Every entry's node goes to
-// ticket[i] as int32, where the commit of a large group finds the node's
-// entries.  The two wave counts are packed in one word: a workgroup prefix in
-// LDS, then one cursor atomic per workgroup.
-__device__ __forceinline__ void plan_block(const PlanParams& P, int64_t block, PlanLds& L) {
-  const int64_t i = block * blockDim.x + threadIdx.x;
-  const int wv = threadIdx.x / kWave;
-  const int lane = threadIdx.x & (kWave - 1);
-  // nobody writes phase_next while a plan runs; every workgroup records the
-  // same phase for the commit
-  const int ph = P.ctl[kCtlPhaseNext] & 1;
-  if (threadIdx.x == 0) P.ctl[kCtlPhaseCur] = ph;
+// Two-launch plan of entries [block * T, +T), T = blockDim.x (a multiple of
+// kWave, at most kPlanMaxThreads; every thread of the workgroup calls it).
+// krec[i] = (slot, wp') for entry i: the entry with rank r among the c entries
+// of its node u (in entry order) is kept iff r >= c - kept, kept = min(c, B),
+// and lands in slot (wp[u] + r - (c - kept)) % B; the node's last entry also
+// carries wp' = wp[u] + kept.  LDS (plan_lds_bytes(T), sized so that a gather
+// launch carrying the plan keeps its occupancy): a hash table of the
+// workgroup's nodes (hkey, H = 512 slots up to 256 threads, else 1024: at most
+// half full), per node and counter set the entries of the batch before and
+// after the range that the scan met (hba: before in the low, after in the high
+// 16 bits, both < 2^15; wavefront w counts into set w % 4, so a hub node does
+// not serialise one counter), and per node and wavefront its entries in the
+// wavefront's part of the range (wcnt).
+constexpr int kPlanScan = 4;  // node ids each thread loads per step of the batch scan
+constexpr int kPlanSets = 4;  // counter sets of the scan
+__host__ __device__ constexpr int plan_hash_bits(int T) { return T > 256 ? 10 : 9; }
+__host__ __device__ constexpr size_t plan_lds_bytes(int T) {
+  return static_cast<size_t>(1 << plan_hash_bits(T)) *
+         (4 + 4 * static_cast<size_t>(T / kWave < kPlanSets ? T / kWave : kPlanSets) +
+          static_cast<size_t>(T / kWave));
+}
+
+__device__ __forceinline__ int plan_hash(int32_t u, int bits) {
+  return static_cast<int>((static_cast<uint32_t>(u) * 2654435761u) >> (32 - bits));
+}
+
+__device__ __forceinline__ void plan_block_ordered(const PlanParams& P, int64_t block, uint8_t* smem) {
+  const int T = static_cast<int>(blockDim.x);
+  const int t = threadIdx.x;
+  const int wv = t / kWave;
+  const int lane = t & (kWave - 1);
+  const int nw = T / kWave;
+  const int hbits = plan_hash_bits(T);
+  const int H = 1 << hbits;
+  const int nsets = nw < kPlanSets ? nw : kPlanSets;
+  int32_t* hkey = reinterpret_cast<int32_t*>(smem);                 // [H]
+  uint32_t* hba = reinterpret_cast<uint32_t*>(smem + 4 * H);         // [nsets][H]
+  uint8_t* wcnt = smem + 4 * H + 4 * static_cast<size_t>(nsets) * H;  // [nw][H]
+  uint32_t* mine_ba = hba + static_cast<size_t>(wv % kPlanSets) * H;
+  const int64_t lo = block * T;
+  const int64_t hi = lo + T < P.n ? lo + T : P.n;
+  const int64_t i = lo + t;
   int bad;
   bool time_ok;
   const int32_t u = entry_prologue(P, i, bad, time_ok);
-  const int32_t t = node_ticket(P, u, L);
-  if (i < P.n) P.ticket[i] = u;
-  if (t >= 0 && t < kListCap) P.lst[static_cast<int64_t>(u) * kListCap + t] = static_cast<int32_t>(i);
-  const uint64_t gm = __ballot(t == 1);
-  const uint64_t lm = __ballot(t == kListCap);
-  if (lane == 0)
-    L.wofs[wv] = (static_cast<uint64_t>(__popcll(gm)) << (kFGroups * kFieldBits)) |
-                 (static_cast<uint64_t>(__popcll(lm)) << (kFLarge * kFieldBits));
+  // the write position is needed last: its load goes out first
+  const int64_t w = u >= 0 ? P.wpos[u] : 0;
+  for (int s = t; s < H; s += T) hkey[s] = -1;
+  for (int s = t; s < nsets * H; s += T) hba[s] = 0u;
+  for (int s = t; s < nw * H / 4; s += T) reinterpret_cast<uint32_t*>(wcnt)[s] = 0u;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const int nw = static_cast<int>(blockDim.x) / kWave;
-    uint64_t tot = 0;
-    for (int w = 0; w < nw; ++w) {
-      const uint64_t c = L.wofs[w];
-      L.wofs[w] = tot;
-      tot += c;
+  int hs = -1;
+  if (u >= 0) {
+    hs = plan_hash(u, hbits);
+    while (true) {  // terminates: fewer keys than slots
+      const int32_t old = atomicCAS(&hkey[hs], -1, u);
+      if (old == -1 || old == u) break;
+      hs = (hs + 1) & (H - 1);
     }
-    L.wofs[kPlanMaxWaves] =
-        tot != 0 ? atomicAdd(reinterpret_cast<unsigned long long*>(P.ctl + kCtlFCursor + 2 * ph),
-                             static_cast<unsigned long long>(tot))
-                 : 0;
+  }
+  // rank in the wavefront (entry order) and the wavefront's count per node
+  int wrank = 0;
+  {
+    uint64_t todo = __ballot(u >= 0);
+    while (todo != 0u) {  // wave-uniform
+      const int leader = __builtin_ctzll(todo);
+      const int sl = __shfl(hs, leader);
+      const uint64_t same = __ballot(u >= 0 && hs == sl);
+      if (u >= 0 && hs == sl)
+        wrank = static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(same >> 32),
+                                                           __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(same), 0u)));
+      if (lane == leader) wcnt[static_cast<size_t>(wv) * H + sl] = static_cast<uint8_t>(__popcll(same));
+      todo &= ~same;
+    }
   }
   __syncthreads();
-  const uint64_t below = (uint64_t(1) << lane) - 1;
-  const uint64_t at = L.wofs[kPlanMaxWaves] + L.wofs[wv];
-  if (t == 1) P.groups[field(at, kFGroups) + __popcll(gm & below)] = u;
-  if (t == kListCap) P.large[field(at, kFLarge) + __popcll(lm & below)] = u;
-  report_diagnostics(P, bad, time_ok, kCtlFDiag + 2 * ph, kCtlFDiag + 2 * ph + 1);
+  // the batch outside [lo, hi): entries of this workgroup's nodes before and
+  // after it, counted per wavefront (hub nodes would serialise one counter);
+  // each step's node ids are loaded one step ahead
+  const int64_t step = static_cast<int64_t>(T) * kPlanScan;
+  int64_t nx[kPlanScan];
+  auto fetch = [&](int64_t j0) {
+#pragma unroll
+    for (int k = 0; k < kPlanScan; ++k) {
+      const int64_t j = j0 + static_cast<int64_t>(k) * T + t;
+      nx[k] = (j < P.n && (j < lo || j >= hi)) ? entry_node(P.src, P.dst, j, P.b) : -1;
+    }
+  };
+  fetch(0);
+  for (int64_t j0 = 0; j0 < P.n; j0 += step) {  // workgroup-uniform
+    int64_t cur[kPlanScan];
+#pragma unroll
+    for (int k = 0; k < kPlanScan; ++k) cur[k] = nx[k];
+    if (j0 + step < P.n) fetch(j0 + step);
+#pragma unroll
+    for (int k = 0; k < kPlanScan; ++k) {
+      if (cur[k] < 0 || cur[k] >= P.N) continue;
+      const int32_t x = static_cast<int32_t>(cur[k]);
+      int s = plan_hash(x, hbits);
+      int32_t key = hkey[s];
+      while (key != x && key != -1) {
+        s = (s + 1) & (H - 1);
+        key = hkey[s];
+      }
+      if (key == x) {
+        const int64_t j = j0 + static_cast<int64_t>(k) * T + t;
+        atomicAdd(&mine_ba[s], j < lo ? 1u : 0x10000u);
+      }
+    }
+  }
+  __syncthreads();
+  if (i < P.n) {
+    int64_t slot = -1, wnew = -1;
+    if (u >= 0) {
+      int below = 0, mine = 0, before = 0, after = 0;
+      for (int w2 = 0; w2 < nw; ++w2) {
+        const int c2 = wcnt[static_cast<size_t>(w2) * H + hs];
+        mine += c2;
+        if (w2 < wv) below += c2;
+      }
+      for (int s2 = 0; s2 < nsets; ++s2) {
+        const uint32_t ba = hba[static_cast<size_t>(s2) * H + hs];
+        before += static_cast<int>(ba & 0xffffu);
+        after += static_cast<int>(ba >> 16);
+      }
+      const int c = before + mine + after;
+      const int r = before + below + wrank;
+      const int kept = c < P.B ? c : P.B;
+      const int m = r - (c - kept);
+      if (m >= 0) {
+        const uint64_t x = static_cast<uint64_t>(w) + static_cast<uint64_t>(m);
+        slot = static_cast<int64_t>(x % static_cast<uint64_t>(P.B));
+      }
+      if (r == c - 1) wnew = w + kept;
+    }
+    reinterpret_cast<longlong2*>(P.krec)[i] = make_longlong2(slot, wnew);
+  }
+  report_diagnostics(P, bad, time_ok, kCtlKTime, kCtlKBad);
 }
 
 // Host side (tgx_ring.hip).  plan_setup checks the arguments of a plan and fills
