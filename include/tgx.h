@@ -184,9 +184,9 @@ typedef struct tgx_recent_args {
    * the batch append_src/dst/time (append_b events, append_workspace of
    * tgx_ring_append_workspace_size(append_b) bytes) that the caller appends
    * next, through tgx_ring_commit (or drops through tgx_ring_discard).  The plan
-   * writes only the ring's scratch and the workspace, so it runs beside the
-   * gather; batches above 16384 events are planned by launches of their own
-   * after the gather.  append_b == 0: no plan. */
+   * reads the batch and the ring's write positions and writes only the
+   * workspace, so it runs beside the gather; batches above 16384 events are
+   * planned by launches of their own after the gather.  append_b == 0: no plan. */
   const int64_t* append_src;
   const int64_t* append_dst;
   const double* append_time;
@@ -245,16 +245,21 @@ size_t tgx_ring_append_static_max_bytes(void);
 
 /* tgx_ring_append in two halves, so the first can run while other work still
  * reads the ring (the same split of _append_overflow, temporal_graph.py:351-387):
- *   tgx_ring_plan   : per-node counts and the entry lists of the batch, in the
- *                     workspace and the ring's scratch; reads src/dst/time, never
- *                     the ring arrays.  Needs the scratch counters at zero (as
- *                     every commit or discard leaves them).
+ *   tgx_ring_plan   : up to 16384 events, every entry's slot (or none) and every
+ *                     node's new write position, in the workspace; reads
+ *                     src/dst/time and write_pos, writes no ring array and no
+ *                     scratch but two diagnostic words.  Above 16384 events,
+ *                     per-node counts and entry lists in the workspace and the
+ *                     ring's scratch, reading src/dst/time only; needs the
+ *                     scratch counters at zero (as every commit or discard
+ *                     leaves them).
  *   tgx_ring_commit : the ring writes of a planned batch (same arguments and
  *                     workspace as its plan); restores the counters; reports the
  *                     plan's diagnostics into `status`.
  *   tgx_ring_discard: drops a planned batch without touching the ring arrays and
  *                     restores the counters.
- * Plan, then exactly one of commit / discard, ordered on streams by the caller. */
+ * Plan, then exactly one of commit / discard, ordered on streams by the caller,
+ * with no other write to the ring between them (the plan reads write_pos). */
 int tgx_ring_plan(const tgx_ring* ring, const int64_t* src, const int64_t* dst,
                   const double* time, int64_t b, void* workspace, size_t workspace_bytes,
                   void* stream);
