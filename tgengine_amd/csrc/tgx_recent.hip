@@ -204,6 +204,9 @@ constexpr int64_t kDeviceCUs = 256;
 
 // row chunks each lane loads before storing them (large-row copy)
 constexpr int kCopyDepth = 4;
+// node ids per thread and step of the ring plan's batch scan when the plan runs
+// in a gather launch (its registers stay within the gather's)
+constexpr int kFusedPlanScan = 4;
 
 // x / n for x * n < 2^32 (n >= 1): one multiply-high by ceil(2^32 / n)
 struct FastDiv {
@@ -485,7 +488,7 @@ void recent_fused(Params P) {
   if (static_cast<int>(blockIdx.x) < P.plan_blocks) {
     // the plan reads the ring's write positions and writes only its scratch and
     // the workspace, never the arrays gathered here
-    plan_block_ordered(P.pl, blockIdx.x, smem);
+    plan_block_ordered<kFusedPlanScan>(P.pl, blockIdx.x, smem);
     return;
   }
   const int64_t g = static_cast<int64_t>(blockIdx.x) - P.plan_blocks;

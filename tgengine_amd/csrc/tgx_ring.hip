@@ -127,9 +127,14 @@ __global__ __launch_bounds__(kThreads) void append_count(PlanParams P) {
 }
 
 // ---- two-launch 1. plan -------------------------------------------------------
-__global__ __launch_bounds__(kThreads) void fast_plan(PlanParams P) {
-  __shared__ __align__(16) uint8_t smem[plan_lds_bytes(kThreads)];
-  plan_block_ordered(P, blockIdx.x, smem);
+// Alone, the plan's workgroups are as large as they go: each scans the whole
+// batch, so T threads take n/T node ids each, all loaded in one or two steps.
+constexpr int kPlanAloneThreads = 1024;
+constexpr int kPlanAloneScan = 8;
+template <int T>
+__global__ __launch_bounds__(T) void fast_plan(PlanParams P) {
+  __shared__ __align__(16) uint8_t smem[plan_lds_bytes(T)];
+  plan_block_ordered<T == kPlanAloneThreads ? kPlanAloneScan : 4>(P, blockIdx.x, smem);
 }
 
 // ---- four-launch 2. groups --------------------------------------------------------------
@@ -578,7 +583,12 @@ int plan_setup(const char* who, const tgx_ring* ring, const int64_t* src, const 
 int launch_plan(const PlanParams& P, hipStream_t stream) {
   const dim3 grid1(static_cast<unsigned>((P.n + kThreads - 1) / kThreads));
   if (plan_fused_ok(P)) {
-    hipLaunchKernelGGL(fast_plan, grid1, dim3(kThreads), 0, stream, P);
+    if (P.n <= kThreads) {
+      hipLaunchKernelGGL(fast_plan<kThreads>, grid1, dim3(kThreads), 0, stream, P);
+    } else {
+      const dim3 grid(static_cast<unsigned>((P.n + kPlanAloneThreads - 1) / kPlanAloneThreads));
+      hipLaunchKernelGGL(fast_plan<kPlanAloneThreads>, grid, dim3(kPlanAloneThreads), 0, stream, P);
+    }
     return check_launch("fast_plan");
   }
   // the four-launch plan: groups and fill also read the lists' aliases

@@ -132,56 +132,92 @@ __device__ __forceinline__ void report_diagnostics(const PlanParams& P, int bad,
 }
 
 // Two-launch plan of entries [block * T, +T), T = blockDim.x (a multiple of
-// kWave, at most kPlanMaxThreads; every thread of the workgroup calls it).
+// kWave, at most kOrderedMaxThreads; every thread of the workgroup calls it).
 // krec[i] = (slot, wp') for entry i: the entry with rank r among the c entries
 // of its node u (in entry order) is kept iff r >= c - kept, kept = min(c, B),
 // and lands in slot (wp[u] + r - (c - kept)) % B; the node's last entry also
-// carries wp' = wp[u] + kept.  LDS (plan_lds_bytes(T), sized so that a gather
-// launch carrying the plan keeps its occupancy): a hash table of the
-// workgroup's nodes (hkey, H = 512 slots up to 256 threads, else 1024: at most
-// half full), per node and counter set the entries of the batch before and
-// after the range that the scan met (hba: before in the low, after in the high
-// 16 bits, both < 2^15; wavefront w counts into set w % 4, so a hub node does
-// not serialise one counter), and per node and wavefront its entries in the
-// wavefront's part of the range (wcnt).
-constexpr int kPlanScan = 4;  // node ids each thread loads per step of the batch scan
+// carries wp' = wp[u] + kept.
+//
+// LDS, plan_lds_bytes(T) (sized so that a gather launch carrying the plan keeps
+// its occupancy), per slot of a hash table of the workgroup's nodes (H >= 2T
+// slots, so at most half full):
+//   hkey[H]          the node;
+//   hba[H][4]        entries of the batch before (low 16 bits) and after (high
+//                    16 bits) the range that the scan met, in four counter sets
+//                    (wavefront w counts into set w % 4; both sums < 2^15);
+//   wcnt[H][stride]  per wavefront, the node's entries in its part of the range
+//                    (bytes; stride = 4, 8 or 16 >= T / 64).
+// One 16-byte read of hba and one read of wcnt give an entry everything it
+// needs at the end.
+//
+// SCAN: node ids each thread loads per step of the batch scan (the next step's
+// loads go out before this step's lookups, the first step's before anything
+// else).  A wavefront's 64 scanned entries lie all before or all after the
+// range (both are multiples of 64), and its matches of one node (a hub) add up
+// in one atomic.
+constexpr int kOrderedMaxThreads = 1024;
 constexpr int kPlanSets = 4;  // counter sets of the scan
-__host__ __device__ constexpr int plan_hash_bits(int T) { return T > 256 ? 10 : 9; }
+__host__ __device__ constexpr int plan_hash_bits(int T) {
+  return T > 512 ? 11 : T > 256 ? 10 : T > 128 ? 9 : T > 64 ? 8 : 7;
+}
+__host__ __device__ constexpr int plan_wcnt_stride(int T) { return T > 512 ? 16 : T > 256 ? 8 : 4; }
 __host__ __device__ constexpr size_t plan_lds_bytes(int T) {
   return static_cast<size_t>(1 << plan_hash_bits(T)) *
-         (4 + 4 * static_cast<size_t>(T / kWave < kPlanSets ? T / kWave : kPlanSets) +
-          static_cast<size_t>(T / kWave));
+         static_cast<size_t>(4 + 4 * kPlanSets + plan_wcnt_stride(T));
 }
 
 __device__ __forceinline__ int plan_hash(int32_t u, int bits) {
   return static_cast<int>((static_cast<uint32_t>(u) * 2654435761u) >> (32 - bits));
 }
 
+// sum of the four bytes of x, and of those below byte `upto` (0..4)
+__device__ __forceinline__ uint32_t byte_sum(uint32_t x) { return __builtin_amdgcn_sad_u8(x, 0u, 0u); }
+__device__ __forceinline__ uint32_t byte_sum_below(uint32_t x, int upto) {
+  return upto <= 0 ? 0u : upto >= 4 ? byte_sum(x) : byte_sum(x & ((1u << (8 * upto)) - 1u));
+}
+
+template <int SCAN>
 __device__ __forceinline__ void plan_block_ordered(const PlanParams& P, int64_t block, uint8_t* smem) {
   const int T = static_cast<int>(blockDim.x);
   const int t = threadIdx.x;
   const int wv = t / kWave;
   const int lane = t & (kWave - 1);
-  const int nw = T / kWave;
   const int hbits = plan_hash_bits(T);
   const int H = 1 << hbits;
-  const int nsets = nw < kPlanSets ? nw : kPlanSets;
-  int32_t* hkey = reinterpret_cast<int32_t*>(smem);                 // [H]
-  uint32_t* hba = reinterpret_cast<uint32_t*>(smem + 4 * H);         // [nsets][H]
-  uint8_t* wcnt = smem + 4 * H + 4 * static_cast<size_t>(nsets) * H;  // [nw][H]
-  uint32_t* mine_ba = hba + static_cast<size_t>(wv % kPlanSets) * H;
+  const int stride = plan_wcnt_stride(T);
+  int32_t* hkey = reinterpret_cast<int32_t*>(smem);                               // [H]
+  uint32_t* hba = reinterpret_cast<uint32_t*>(smem + 4 * static_cast<size_t>(H));  // [H][4]
+  uint8_t* wcnt = smem + static_cast<size_t>(4 + 4 * kPlanSets) * H;              // [H][stride]
+  const int set = wv % kPlanSets;
   const int64_t lo = block * T;
   const int64_t hi = lo + T < P.n ? lo + T : P.n;
   const int64_t i = lo + t;
-  int bad;
-  bool time_ok;
-  const int32_t u = entry_prologue(P, i, bad, time_ok);
-  // the write position is needed last: its load goes out first
-  const int64_t w = u >= 0 ? P.wpos[u] : 0;
+  // the entry's node and time, then the first step of the batch scan (node ids
+  // of the entries outside [lo, hi)), all before any of them is waited for
+  int64_t uu = -1;
+  double ti = 0.0;
+  if (i < P.n) {
+    uu = entry_node(P.src, P.dst, i, P.b);
+    if (i < P.b) ti = P.time[i];
+  }
+  const int64_t step = static_cast<int64_t>(T) * SCAN;
+  int64_t nx[SCAN];
+  auto fetch = [&](int64_t j0) {
+#pragma unroll
+    for (int k = 0; k < SCAN; ++k) {
+      const int64_t j = j0 + static_cast<int64_t>(k) * T + t;
+      nx[k] = (j < P.n && (j < lo || j >= hi)) ? entry_node(P.src, P.dst, j, P.b) : -1;
+    }
+  };
+  fetch(0);
   for (int s = t; s < H; s += T) hkey[s] = -1;
-  for (int s = t; s < nsets * H; s += T) hba[s] = 0u;
-  for (int s = t; s < nw * H / 4; s += T) reinterpret_cast<uint32_t*>(wcnt)[s] = 0u;
+  for (int s = t; s < kPlanSets * H; s += T) hba[s] = 0u;
+  for (int s = t; s < stride * H / 4; s += T) reinterpret_cast<uint32_t*>(wcnt)[s] = 0u;
   __syncthreads();
+  const int bad = i < P.n && (uu < 0 || uu >= P.N) ? 1 : 0;
+  const int32_t u = i < P.n && !bad ? static_cast<int32_t>(uu) : -1;
+  // the write position is needed last
+  const int64_t w = u >= 0 ? P.wpos[u] : 0;
   int hs = -1;
   if (u >= 0) {
     hs = plan_hash(u, hbits);
@@ -191,53 +227,58 @@ __device__ __forceinline__ void plan_block_ordered(const PlanParams& P, int64_t 
       hs = (hs + 1) & (H - 1);
     }
   }
-  // rank in the wavefront (entry order) and the wavefront's count per node
+  // the wavefront's count per node (its byte of the node's wcnt row, by an
+  // atomic on the row's word; a wavefront's LDS operations complete in order, so
+  // the read after its own atomics sees them all), then the rank in entry order
+  // among the wavefront's entries of the same node, by ballots over the nodes
+  // it holds more than once
   int wrank = 0;
   {
-    uint64_t todo = __ballot(u >= 0);
+    uint32_t* wcw = reinterpret_cast<uint32_t*>(wcnt);
+    const int wi = u >= 0 ? (hs * stride + wv) >> 2 : 0;
+    const int sh = 8 * (wv & 3);
+    if (u >= 0) atomicAdd(&wcw[wi], 1u << sh);
+    const int cnt = u >= 0 ? static_cast<int>((wcw[wi] >> sh) & 0xffu) : 0;
+    uint64_t todo = __ballot(cnt > 1);
     while (todo != 0u) {  // wave-uniform
       const int leader = __builtin_ctzll(todo);
-      const int sl = __shfl(hs, leader);
+      const int sl = __builtin_amdgcn_readlane(hs, leader);
       const uint64_t same = __ballot(u >= 0 && hs == sl);
       if (u >= 0 && hs == sl)
         wrank = static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(same >> 32),
                                                            __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(same), 0u)));
-      if (lane == leader) wcnt[static_cast<size_t>(wv) * H + sl] = static_cast<uint8_t>(__popcll(same));
       todo &= ~same;
     }
   }
   __syncthreads();
   // the batch outside [lo, hi): entries of this workgroup's nodes before and
-  // after it, counted per wavefront (hub nodes would serialise one counter);
-  // each step's node ids are loaded one step ahead
-  const int64_t step = static_cast<int64_t>(T) * kPlanScan;
-  int64_t nx[kPlanScan];
-  auto fetch = [&](int64_t j0) {
-#pragma unroll
-    for (int k = 0; k < kPlanScan; ++k) {
-      const int64_t j = j0 + static_cast<int64_t>(k) * T + t;
-      nx[k] = (j < P.n && (j < lo || j >= hi)) ? entry_node(P.src, P.dst, j, P.b) : -1;
-    }
-  };
-  fetch(0);
+  // after it
   for (int64_t j0 = 0; j0 < P.n; j0 += step) {  // workgroup-uniform
-    int64_t cur[kPlanScan];
+    int64_t cur[SCAN];
 #pragma unroll
-    for (int k = 0; k < kPlanScan; ++k) cur[k] = nx[k];
+    for (int k = 0; k < SCAN; ++k) cur[k] = nx[k];
     if (j0 + step < P.n) fetch(j0 + step);
 #pragma unroll
-    for (int k = 0; k < kPlanScan; ++k) {
-      if (cur[k] < 0 || cur[k] >= P.N) continue;
-      const int32_t x = static_cast<int32_t>(cur[k]);
-      int s = plan_hash(x, hbits);
-      int32_t key = hkey[s];
-      while (key != x && key != -1) {
-        s = (s + 1) & (H - 1);
-        key = hkey[s];
+    for (int k = 0; k < SCAN; ++k) {
+      int s = -1;
+      if (cur[k] >= 0 && cur[k] < P.N) {
+        const int32_t x = static_cast<int32_t>(cur[k]);
+        s = plan_hash(x, hbits);
+        int32_t key = hkey[s];
+        while (key != x && key != -1) {
+          s = (s + 1) & (H - 1);
+          key = hkey[s];
+        }
+        if (key != x) s = -1;
       }
-      if (key == x) {
-        const int64_t j = j0 + static_cast<int64_t>(k) * T + t;
-        atomicAdd(&mine_ba[s], j < lo ? 1u : 0x10000u);
+      const uint64_t mm = __ballot(s >= 0);
+      if (mm != 0u) {  // wave-uniform
+        const uint32_t inc = j0 + static_cast<int64_t>(k) * T + t < lo ? 1u : 0x10000u;  // wave-uniform
+        const int ld = __builtin_ctzll(mm);
+        const int ls = __builtin_amdgcn_readlane(s, ld);
+        const uint64_t same = __ballot(s == ls);
+        if (lane == ld) atomicAdd(&hba[static_cast<size_t>(ls) * kPlanSets + set], inc * static_cast<uint32_t>(__popcll(same)));
+        else if (s >= 0 && s != ls) atomicAdd(&hba[static_cast<size_t>(s) * kPlanSets + set], inc);
       }
     }
   }
@@ -245,16 +286,25 @@ __device__ __forceinline__ void plan_block_ordered(const PlanParams& P, int64_t 
   if (i < P.n) {
     int64_t slot = -1, wnew = -1;
     if (u >= 0) {
-      int below = 0, mine = 0, before = 0, after = 0;
-      for (int w2 = 0; w2 < nw; ++w2) {
-        const int c2 = wcnt[static_cast<size_t>(w2) * H + hs];
-        mine += c2;
-        if (w2 < wv) below += c2;
+      const uint4 ba = *reinterpret_cast<const uint4*>(&hba[static_cast<size_t>(hs) * kPlanSets]);
+      const int before = static_cast<int>((ba.x & 0xffffu) + (ba.y & 0xffffu) + (ba.z & 0xffffu) + (ba.w & 0xffffu));
+      const int after = static_cast<int>((ba.x >> 16) + (ba.y >> 16) + (ba.z >> 16) + (ba.w >> 16));
+      const uint8_t* row = wcnt + static_cast<size_t>(hs) * stride;
+      uint32_t cw[4] = {0u, 0u, 0u, 0u};
+      if (stride == 16) {
+        const uint4 v = *reinterpret_cast<const uint4*>(row);
+        cw[0] = v.x; cw[1] = v.y; cw[2] = v.z; cw[3] = v.w;
+      } else if (stride == 8) {
+        const uint2 v = *reinterpret_cast<const uint2*>(row);
+        cw[0] = v.x; cw[1] = v.y;
+      } else {
+        cw[0] = *reinterpret_cast<const uint32_t*>(row);
       }
-      for (int s2 = 0; s2 < nsets; ++s2) {
-        const uint32_t ba = hba[static_cast<size_t>(s2) * H + hs];
-        before += static_cast<int>(ba & 0xffffu);
-        after += static_cast<int>(ba >> 16);
+      int mine = 0, below = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        mine += static_cast<int>(byte_sum(cw[q]));
+        below += static_cast<int>(byte_sum_below(cw[q], wv - 4 * q));
       }
       const int c = before + mine + after;
       const int r = before + below + wrank;
@@ -268,6 +318,7 @@ __device__ __forceinline__ void plan_block_ordered(const PlanParams& P, int64_t 
     }
     reinterpret_cast<longlong2*>(P.krec)[i] = make_longlong2(slot, wnew);
   }
+  const bool time_ok = i < P.b && trunc(ti) > static_cast<double>(P.n - 3);
   report_diagnostics(P, bad, time_ok, kCtlKTime, kCtlKBad);
 }
 
