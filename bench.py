@@ -478,6 +478,146 @@ def run_rows(a, log) -> None:
     log(f"rows: negpool {ms * 1e3:.2f} us per update + sample")
 
 
+RING_SHAPES = ("c3", "singletons", "one_node", "groups8", "pairs", "groups10", "groups40", "groups100")
+
+
+def ring_shape_batch(cfg, name: str, j: int):
+    """src, dst of batch j of a 4,000-event ring-update shape on cfg's node range:
+    the C3 stream itself, or entries built to give every node the same count (each
+    node once, all entries on one node, groups of 8, 2, 10, 40 or 100 entries); the
+    node set moves between batches."""
+    from tgengine_amd.synthetic import gen_batch
+    b = 4000
+    i = np.arange(b, dtype=np.int64)
+    base = (j * 7919) % (cfg.num_nodes - 10000)
+    if name == "c3":
+        bt = gen_batch(cfg, 3000 + j, with_feats=False)
+        return bt["src"][:b].astype(np.int64), bt["dst"][:b].astype(np.int64)
+    groups = {"groups8": 1000, "pairs": b, "groups10": 800, "groups40": 200, "groups100": 80}
+    if name == "singletons":
+        return base + 2 * i, base + 2 * i + 1
+    if name == "one_node":
+        return np.full(b, base, np.int64), np.full(b, base, np.int64)
+    g = groups[name]
+    return base + i % g, base + (i + 7) % g
+
+
+def run_ring_shapes(a, log) -> None:
+    """--ring-shapes: the ring update alone (tgx_ring_append: the plan launch, then
+    the commit launch) on the C3 ring (1M nodes, 32 slots, 16-d bf16 rows) for
+    4,000-event batches of several shapes, one JSON line each.  Per shape: the
+    first 3 batches on an empty ring are compared with the oracle's ring_advance
+    (every touched node's slots, times, rows and write position), then 100 appends
+    are captured in a HIP graph and replayed between two HIP events, then 100
+    batches run through DataPipeline.prepare -> advance (the plan in the gather
+    launch, the commit alone; untimed here, so that a kernel trace of this command
+    shows the commit of both paths)."""
+    import torch
+    from oracle import spec  # the CPU legs only
+    from tgengine_amd import RawBatch
+    from tgengine_amd.synthetic import CONFIGS, make_graph, make_pipeline
+    cfg = CONFIGS["c3"]
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    N, d, b, NB = cfg.num_nodes, cfg.feat_dim, 4000, 100
+    rng = np.random.default_rng(11)
+    shapes = [s for s in a.ring_shapes.split(",") if s]
+    for name in shapes:
+        if name not in RING_SHAPES:
+            raise SystemExit(f"--ring-shapes: unknown shape {name!r} (one of {', '.join(RING_SHAPES)})")
+    t_next = 1.0e7
+    for name in shapes:
+        host, devb = [], []
+        for j in range(3 + 2 * NB):
+            s_, d_ = ring_shape_batch(cfg, name, j)
+            tt = t_next + np.arange(b) * 1e-3
+            t_next = float(tt[-1]) + 1.0
+            f = (rng.standard_normal((b, d)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+            host.append((s_, d_, tt, f))
+            devb.append((torch.from_numpy(s_).to(device), torch.from_numpy(d_).to(device),
+                         torch.from_numpy(tt).to(device), torch.from_numpy(f).view(torch.bfloat16).to(device),
+                         torch.from_numpy(rng.integers(0, N, b)).to(device)))
+        g = make_graph(cfg)
+        g.freeze_csr()
+        # parity: the first 3 batches on an empty ring against the oracle
+        ring = spec.Ring.empty(N, cfg.buffer_size, d, np.uint16)
+        ring.times.fill(0.0)  # touch every page before the oracle is timed
+        ring.feats.fill(0)
+        c0 = time.perf_counter()
+        for j in range(3):
+            spec.ring_advance(ring, *host[j])
+        cpu_s = time.perf_counter() - c0
+        for j in range(3):
+            g.advance(*devb[j][:4])
+        torch.cuda.synchronize()
+        touched = np.unique(np.concatenate([np.concatenate(h[:2]) for h in host[:3]]))
+        tt_ = torch.from_numpy(touched).to(device)
+        same = (np.array_equal(g._ov_ids[tt_].cpu().numpy(), ring.ids[touched])
+                and np.array_equal(g._ov_times[tt_].cpu().numpy(), ring.times[touched])
+                and np.array_equal(g._ov_feats[tt_].view(torch.int16).cpu().numpy().view(np.uint16),
+                                   ring.feats[touched])
+                and np.array_equal(g._ov_write_pos[tt_].cpu().numpy(), ring.wp[touched]))
+        if not same:
+            raise RuntimeError(f"ring-shapes {name}: the ring after 3 batches differs from the oracle's")
+        del ring
+        # timed: NB appends, captured once and replayed
+        for j in range(3, 13):
+            g.advance(*devb[j][:4])
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for j in range(3, 3 + NB):
+                g.advance(*devb[j][:4])
+        graph.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / NB
+        del graph
+        # the same batches' shape through prepare -> advance (commit alone)
+        pipe = make_pipeline(cfg, g)
+        for j in range(3 + NB, 3 + 2 * NB):
+            s_, d_, t_, f_, n_ = devb[j]
+            pipe.prepare(RawBatch(src=s_, dst=d_, time=t_, edge_feat=f_, neg=n_))
+            g.advance(s_, d_, t_, f_)
+        torch.cuda.synchronize()
+        st = g.status()
+        if any(st.values()):
+            raise RuntimeError(f"ring-shapes {name}: device diagnostics {st}")
+        # algorithmic bytes: every event read (ids, time, row), every kept entry
+        # written (id, time, row) and every touched node's write position
+        kept = distinct = 0
+        for s_, d_, _, _ in host[3:3 + NB]:
+            u, c = np.unique(np.concatenate([s_, d_]), return_counts=True)
+            kept += int(np.minimum(c, cfg.buffer_size).sum())
+            distinct += len(u)
+        rb = d * cfg.feat_bytes
+        nbytes = (NB * b * (24 + rb) + kept * (12 + rb) + distinct * 8) / NB
+        gbs = nbytes / (us * 1e-6) / 1e9
+        u0, c0_ = np.unique(np.concatenate(host[3][:2]), return_counts=True)
+        print(json.dumps({
+            "row": "ring_update", "shape": name, "metric": "events/s (ring update alone)",
+            "value": b / (us * 1e-6), "unit": "events/s", "us_per_append": us,
+            "workload": f"tgx_ring_append of 4,000-event batches on the C3 ring ({N} nodes, "
+                        f"{cfg.buffer_size} slots, {d}-d bf16 rows): {len(u0)} nodes per batch, up to "
+                        f"{int(c0_.max())} entries per node",
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": gbs / PEAK_HBM_GBS, "bytes_per_call": nbytes},
+            "cpu_baseline": {"value": 3 * b / cpu_s, "unit": "events/s", "cores": 1, "kind": "port",
+                             "sample": "oracle.spec.ring_advance (numpy) of the shape's first 3 batches"},
+            "parity": "after 3 batches on an empty ring, every touched node's ids, times, rows and "
+                      "write position equal to the oracle's",
+            "timing": f"HIP event pair around a graph replay of {NB} appends"}), flush=True)
+        log(f"ring-shapes {name}: {us:.2f} us per append")
+        del g, pipe, devb
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+
+
 def run_csr_prepare(a, log) -> None:
     """--csr-prepare: DataPipeline.prepare on a frozen CSR, as the reference's Engine
     runs it (engine/__init__.py:174-195: advance the training events, freeze,
@@ -637,6 +777,9 @@ def main():
                          "reference's published Engine shapes (Wikipedia, Reddit, LastFM), one JSON line each")
     ap.add_argument("--csr-shapes", default="wikipedia,reddit,lastfm")
     ap.add_argument("--csr-steps", type=int, default=500)
+    ap.add_argument("--ring-shapes", default="", nargs="?", const=",".join(RING_SHAPES),
+                    help="instead of the streaming step, time the ring update alone for 4,000-event "
+                         "batches of these shapes (all when given without a list), one JSON line each")
     ap.add_argument("--ceilings", action="store_true",
                     help="after timing, measure the device's copy, store and row-gather ceilings "
                          "(plain torch kernels at 1 GiB and at the gather's byte count) and report them")
@@ -651,6 +794,9 @@ def main():
         return
     if a.csr_prepare:
         run_csr_prepare(a, log)
+        return
+    if a.ring_shapes:
+        run_ring_shapes(a, log)
         return
 
     import torch

@@ -468,18 +468,21 @@ __device__ __forceinline__ void co_occurrence_pair(const Params& P, int64_t g, i
 // gfx9 counts vector loads and stores in one in-order vmcnt, so a load behind
 // stores would wait for their completion.  With at most one wave per SIMD slot
 // for the whole grid the gathers all run up front and the stores then stream.
-// Waves-per-SIMD target: 8 for the large-row kernels, whose bandwidth needs every
-// resident wave (plan-group workgroups of 6 waves fit 5 per CU at 8, 4 at 7); none
-// for the small-row kernel, where forcing 8 capped the scalar registers and spilled
-// them into its own code, while the 7 the registers allow still hold its grid.
-template <int NREG>
-constexpr int kWavesPerEu = NREG > 0 ? 1 : 8;
+// Waves-per-SIMD target: 8 for the event- and list-plan kernels with rows through
+// memory, whose bandwidth needs every resident wave (plan-group workgroups of 6
+// waves fit 5 per CU at 8, 4 at 7; without the target C5's gather took 200 us
+// instead of 176); none for the small-row kernels and the tiled 16-byte-chunk
+// kernel, where forcing 8 capped the scalar registers and spilled them into their
+// own code (the tiled one: 8.56 -> 7.74 us on C1 and 367 -> 356 us on C4 without
+// it), while the 7 the registers allow still hold their grids.
+template <int VEC, int NREG, bool TILES>
+constexpr int kWavesPerEu = NREG > 0 || (TILES && VEC == 16) ? 1 : 8;
 
 // TILES: the launch's plan mode is TGX_PLAN_TILES (no event or list plan, so no
 // co-occurrence); that copy of the kernel carries none of their code, which
 // shortens its start-up
 template <int VEC, int NREG, bool TILES>
-__global__ __launch_bounds__(kMaxWaves * kWave) __attribute__((amdgpu_waves_per_eu(kWavesPerEu<NREG>)))
+__global__ __launch_bounds__(kMaxWaves * kWave) __attribute__((amdgpu_waves_per_eu(kWavesPerEu<VEC, NREG, TILES>)))
 void recent_fused(Params P) {
   using VT = typename Vec<VEC>::T;
   extern __shared__ __align__(16) uint8_t smem[];
