@@ -231,3 +231,35 @@ def test_many_batch_sizes_stay_exact_without_per_shape_state():
     assert not hasattr(pipe, "_plans")
     _check_ring(g, ring, bt, "ring after the last batch")
     _check_status(g)
+
+
+@pytest.mark.parametrize("shape", ["singletons", "one_node", "pairs", "groups10"])
+def test_fused_plan_batch_shapes(shape):
+    """The plan as the gather launch's first workgroups, on 4,000-event batches
+    whose nodes all have the same number of entries (consecutive ids), against the
+    oracle's ring after every batch."""
+    cfg = dataclasses.replace(CONFIGS["c3"], num_nodes=60_000)
+    g, pipe, ring = _setup(cfg)
+    rng = np.random.default_rng(40)
+    b = 4000
+    i = np.arange(b, dtype=np.int64)
+    for j in range(4):
+        base = 1000 + 9973 * j
+        if shape == "singletons":
+            src, dst = base + 2 * i, base + 2 * i + 1
+        elif shape == "one_node":
+            src, dst = np.full(b, base), np.full(b, base)
+        elif shape == "pairs":
+            src, dst = base + i, base + (i + 1) % b
+        else:
+            src, dst = base + i % 800, base + (i + 7) % 800
+        bt = dict(gen_batch(cfg, j))
+        bt["src"], bt["dst"] = src, dst
+        bt["neg"] = rng.integers(0, cfg.num_nodes, b)
+        rb = S.to_raw(cfg, bt)
+        pipe.prepare(rb)
+        assert (g._plan is not None) == (j > 0)
+        _advance_both(g, ring, rb, bt)
+        _check_ring(g, ring, bt, f"{shape}: ring after {j}")
+    _check_status(g)
+

@@ -2,13 +2,16 @@
 
 Bit-exact comparison of ids, times, feature rows, write positions and edge ids
 after every batch, over shapes that reach every code path of both update
-designs: the two-launch path (batches of up to 32768 entries: singletons,
-groups of up to 8 entries ranked from the node lists, larger groups from the
-lists plus the overflow array over one or several 8192-index bitmap windows)
-and the four-launch path (larger batches: small groups of 2..64 entries, large
-groups over one or several windows), plus B not a power of two, bf16 rows of
-odd width, zero-width rows, invalid node ids and the size boundary between the
-two paths.
+designs: the two-launch path (batches of up to 32768 entries: the plan ranks
+every entry among its node's entries in entry order from an LDS hash of its
+workgroup's nodes and one scan of the batch, in 1,024-thread workgroups, or
+256 for batches of at most 256 entries; the commit is one copy per entry) and
+the four-launch path (larger batches: tickets from node-indexed counters, small
+groups of 2..64 entries, large groups over one or several bitmap windows), plus
+B not a power of two, bf16 rows of odd width, zero-width rows, invalid node ids,
+the size boundary between the two paths, plan-workgroup boundaries, and batch
+shapes that give every node the same number of entries (one node holding the
+batch, consecutive ids in pairs or groups).
 """
 import numpy as np
 import pytest
@@ -365,3 +368,43 @@ def test_restore_and_reset_drop_a_pending_plan():
     g.plan_append(s2, d2, t2)
     g.reset()
     assert g._plan is None
+
+
+@pytest.mark.parametrize("b", [1, 2, 127, 128, 129, 511, 512, 513, 1537, 4096])
+def test_ring_plan_workgroup_boundaries(b):
+    """Entries of one node on both sides of plan-workgroup boundaries (256-entry
+    workgroups up to 256 entries, 1,024 above), a hub in every workgroup, and
+    wavefronts holding a node more than once."""
+    def gen(rng):
+        for _ in range(3):
+            src = rng.integers(0, 40, b)
+            dst = rng.integers(0, 40, b)
+            src[::3] = 5
+            yield src, dst
+    _run(20 + b, 40, 32, 8, True, gen)
+
+
+def _shape(name, b):
+    """src, dst of a batch whose nodes all have the same number of entries, on
+    consecutive ids from a moving base (the multiplicative hash spreads such runs
+    evenly, the case a probe scheme must not degrade on)."""
+    i = np.arange(b, dtype=np.int64)
+    groups = {"pairs": b, "groups8": b // 4, "groups10": b // 5, "groups100": b // 50}
+
+    def gen(rng):
+        for j in range(3):
+            base = 1000 + 9973 * j
+            if name == "singletons":
+                yield base + 2 * i, base + 2 * i + 1
+            elif name == "one_node":
+                yield np.full(b, base), np.full(b, base)
+            else:
+                g = groups[name]
+                yield base + i % g, base + (i + 7) % g
+    return gen
+
+
+@pytest.mark.parametrize("shape", ["singletons", "one_node", "pairs", "groups8", "groups10", "groups100"])
+def test_ring_update_shapes_match_the_oracle(shape):
+    _run(30, 50_000, 32, 16, True, _shape(shape, 4000))
+
