@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define TGX_ABI_VERSION 14
+#define TGX_ABI_VERSION 15
 
 /* status codes */
 #define TGX_OK 0
@@ -329,12 +329,19 @@ int tgx_csr_build(const tgx_csr_build_args* args, void* stream);
  * splitmix64 finalizer, U = (rand64 >> 40) * 2^-24; streams 0/1 (update accept /
  * slot), 2/3 (sample slot / fallback node).  Out-of-range ids are skipped
  * (update) or sampled as nodes without history (sample) and counted in status.
- * workspace: tgx_negpool_update_workspace_size(n) bytes. */
+ * workspace: tgx_negpool_update_workspace_size(n) bytes (no initialisation
+ * needed).  scratch: NULL, or tgx_negpool_scratch_size() bytes of device memory,
+ * 256-byte aligned, zero-filled once by the caller and otherwise left to the
+ * library (a table that every update leaves zeroed again); with it, batches of
+ * up to 32,768 edges update in two launches over the whole device, without it in
+ * one workgroup (up to 8,192 edges) or by sorting.  Same results either way.
+ * Updates that share a scratch must be ordered (one stream). */
 size_t tgx_negpool_update_workspace_size(int64_t n);
+size_t tgx_negpool_scratch_size(void);
 int tgx_negpool_update(int32_t* pool, int64_t* count, int64_t num_nodes, int32_t pool_size,
                        const int64_t* src, const int64_t* dst, int64_t n, uint64_t seed,
-                       uint64_t call, void* workspace, size_t workspace_bytes, int32_t* status,
-                       void* stream);
+                       uint64_t call, void* workspace, size_t workspace_bytes, void* scratch,
+                       size_t scratch_bytes, int32_t* status, void* stream);
 int tgx_negpool_sample(const int32_t* pool, const int64_t* count, int64_t num_nodes,
                        int32_t pool_size, const int64_t* src, int64_t n, uint64_t seed,
                        uint64_t call, int64_t* out, int32_t* status, void* stream);

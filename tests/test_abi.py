@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(L, n), n
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
-    assert L.tgx_abi_version() == _lib.TGX_ABI_VERSION == 14
+    assert L.tgx_abi_version() == _lib.TGX_ABI_VERSION == 15
     nm = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
                         text=True).stdout
     exported = set(re.findall(r"\bT (tgx_\w+)", nm))
@@ -346,14 +346,21 @@ def test_csr_build_argument_checks():
 
 def test_negpool_argument_checks():
     L = _lib.lib()
-    assert L.tgx_negpool_update(None, None, 10, 4, 8, 8, 1, 0, 0, 8, 1 << 20, None, None) == 1
-    assert L.tgx_negpool_update(8, 8, 0, 4, 8, 8, 1, 0, 0, 8, 1 << 20, None, None) == 3
-    assert L.tgx_negpool_update(8, 8, 10, 0, 8, 8, 1, 0, 0, 8, 1 << 20, None, None) == 3
+    assert L.tgx_negpool_update(None, None, 10, 4, 8, 8, 1, 0, 0, 8, 1 << 20, None, 0, None, None) == 1
+    assert L.tgx_negpool_update(8, 8, 0, 4, 8, 8, 1, 0, 0, 8, 1 << 20, None, 0, None, None) == 3
+    assert L.tgx_negpool_update(8, 8, 10, 0, 8, 8, 1, 0, 0, 8, 1 << 20, None, 0, None, None) == 3
     assert "pool_size" in _err()
-    assert L.tgx_negpool_update(8, 8, 10, 4, None, 8, 1, 0, 0, 8, 1 << 20, None, None) == 1
-    assert L.tgx_negpool_update(8, 8, 10, 4, 8, 8, 100, 0, 0, 8, 16, None, None) == 1
+    assert L.tgx_negpool_update(8, 8, 10, 4, None, 8, 1, 0, 0, 8, 1 << 20, None, 0, None, None) == 1
+    assert L.tgx_negpool_update(8, 8, 10, 4, 8, 8, 100, 0, 0, 8, 16, None, 0, None, None) == 1
     assert "workspace" in _err()
-    assert L.tgx_negpool_update(8, 8, 10, 4, 8, 8, 0, 0, 0, None, 0, None, None) == 0  # empty batch
+    # the cell table: its size, and 256-byte alignment (checked before any launch)
+    sz = L.tgx_negpool_scratch_size()
+    assert sz == 65536 * 12
+    assert L.tgx_negpool_update(8, 8, 10, 4, 8, 8, 100, 0, 0, 256, 1 << 20, 256, sz - 1, None, None) == 1
+    assert "scratch" in _err()
+    assert L.tgx_negpool_update(8, 8, 10, 4, 8, 8, 100, 0, 0, 256, 1 << 20, 264, sz, None, None) == 1
+    assert "aligned" in _err()
+    assert L.tgx_negpool_update(8, 8, 10, 4, 8, 8, 0, 0, 0, None, 0, None, 0, None, None) == 0  # empty batch
     assert L.tgx_negpool_sample(8, 8, 10, 4, None, 5, 0, 0, 8, None, None) == 1
     assert L.tgx_negpool_sample(8, 8, 10, 4, 8, -1, 0, 0, 8, None, None) == 1
     # keys, values, composite keys and values double-buffered, plus digit counts

@@ -1,7 +1,8 @@
 """HistoricalNegPool on the device (tgx_negpool_update / tgx_negpool_sample)
 against the oracle (the reference's reservoir update, edge by edge, with the
 library's counter-based random numbers): pool slots, counts and samples bit for
-bit after every call, and the reservoir property measured on the device."""
+bit after every call, on every update path (two launches with the cell table,
+one workgroup, the sort), and the reservoir property measured on the device."""
 import numpy as np
 import pytest
 import torch
@@ -17,10 +18,30 @@ def _check(pool, ref_pool, ref_cnt, where):
     assert np.array_equal(pool._count.cpu().numpy(), ref_cnt), f"{where}: count"
 
 
-@pytest.mark.parametrize("N,P,b", [(40, 4, 90), (500, 16, 3000), (7, 1, 50), (2000, 512, 20000)])
-def test_negpool_matches_the_oracle(N, P, b):
+class _NoScratch:
+    """Stands in for the pool's cell table: the update then takes the paths that
+    need none (one workgroup up to 8,192 edges, the sort above)."""
+
+    def data_ptr(self):
+        return 0
+
+    def numel(self):
+        return 0
+
+
+def _pool(N, P, seed, scratch=True):
+    pool = HistoricalNegPool(N, pool_size=P, device="cuda", seed=seed)
+    if not scratch:
+        pool._scratch = _NoScratch()
+    return pool
+
+
+@pytest.mark.parametrize("scratch", [True, False])
+@pytest.mark.parametrize("N,P,b", [(40, 4, 90), (500, 16, 3000), (7, 1, 50), (2000, 512, 20000),
+                                   (3000, 8, 40000)])
+def test_negpool_matches_the_oracle(N, P, b, scratch):
     rng = np.random.default_rng(N + P)
-    pool = HistoricalNegPool(N, pool_size=P, device="cuda", seed=1234 + N)
+    pool = _pool(N, P, 1234 + N, scratch)
     ref = np.full((N, P), -1, np.int32)
     cnt = np.zeros(N, np.int64)
     for call in range(8):
@@ -43,15 +64,19 @@ def test_negpool_matches_the_oracle(N, P, b):
     assert st[0] == 5  # the five out-of-range sources of call 3
 
 
-@pytest.mark.parametrize("n", [1, 63, 64, 65, 1000, 4095, 4096, 4097, 5000, 8191, 8192, 8193, 12000])
-def test_negpool_batch_sizes(n):
+@pytest.mark.parametrize("scratch", [True, False])
+@pytest.mark.parametrize("n", [1, 63, 64, 65, 255, 256, 257, 1000, 1023, 1024, 1025, 4095, 4096, 4097, 5000,
+                               8191, 8192, 8193, 12000, 32768, 32769])
+def test_negpool_batch_sizes(n, scratch):
     """Batch sizes on both sides of the single-workgroup updates (at most 4,096 and
-    8,192 edges, one thread per edge and round) and at a wavefront's boundary: three
-    updates of n edges each, hot sources and a two-slot pool (many edges on one
-    cell), pool and counts bit for bit after every call."""
+    8,192 edges, one thread per edge and round), of the two-launch update's
+    workgroups (256 edges for batches of at most 256, else 1,024) and its limit
+    (32,768 edges), and at a wavefront's boundary: three updates of n edges each,
+    hot sources and a two-slot pool (many edges on one cell), pool and counts bit
+    for bit after every call."""
     N, P = 64, 2
     rng = np.random.default_rng(n)
-    pool = HistoricalNegPool(N, pool_size=P, device="cuda", seed=99 + n)
+    pool = _pool(N, P, 99 + n, scratch)
     ref = np.full((N, P), -1, np.int32)
     cnt = np.zeros(N, np.int64)
     for call in range(3):

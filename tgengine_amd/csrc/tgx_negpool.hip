@@ -38,6 +38,7 @@
 // history is left to the caller (-1), which draws its node afterwards as the
 // reference does.
 #include "tgx_radix.h"
+#include "tgx_ring_plan.h"
 
 #include <mutex>
 
@@ -173,6 +174,98 @@ __global__ __launch_bounds__(kThreads) void np_sample(const int32_t* __restrict_
   const uint64_t bm = __ballot(bad);
   if ((threadIdx.x & (kWave - 1)) == 0 && bm != 0 && status != nullptr)
     atomicAdd(&status[TGX_ST_BAD_QUERY_NODE], __popcll(bm));
+}
+
+// Batches of up to kNpRankMax edges with the caller's cell table (scratch): two
+// launches over the whole device.
+//   np_rank   : each workgroup ranks its edges among their source's edges in
+//               batch order (rank_block of tgx_ring_plan.h: an LDS hash of its
+//               sources and one scan of the batch's sources), so edge j, the
+//               r-th of the c edges of u, decides as above with e = count[u] +
+//               r + 1; an accepted edge finds its cell u * P + slot in the
+//               table (open addressing on the key + 1, 0 = empty) and raises
+//               the cell's latest edge to j + 1 (atomicMax).  The record of
+//               edge j: (its cell or -1, the new count on u's last edge or -1).
+//   np_commit : the cell's latest edge writes the pool slot and empties the
+//               cell (the table is zero again after every call); u's last edge
+//               writes count[u].  An edge that reads the cell after its latest
+//               edge emptied it sees 0, which is not its own index either.
+constexpr int64_t kNpRankMax = 32768;  // rank_block's before/after counts (< 2^15)
+constexpr int kNpCellBits = 16;        // 65,536 cells: at most half full at kNpRankMax edges
+constexpr int64_t kNpCells = int64_t(1) << kNpCellBits;
+
+struct NpRankParams {
+  const int64_t* src;
+  int64_t n;
+  int64_t N;
+  int P;
+  const int64_t* count;
+  uint64_t seed;
+  uint64_t call;
+  unsigned long long* ckey;  // [kNpCells] cell + 1, 0 = empty
+  int32_t* cmax;             // [kNpCells] latest edge + 1, 0 = none
+  longlong2* rec;            // [n]
+  int32_t* status;
+};
+
+__device__ __forceinline__ uint32_t np_cell_hash(uint64_t k) {
+  return static_cast<uint32_t>((k * kGolden) >> (64 - kNpCellBits));
+}
+
+template <int T, int SCAN>
+__global__ __launch_bounds__(T) void np_rank(NpRankParams P) {
+  __shared__ __align__(16) uint8_t smem[plan_lds_bytes(T)];
+  const int bad = rank_block<SCAN>(P.src, P.src, P.n, P.n, P.N, P.count, blockIdx.x, smem,
+                                   [&](int64_t j, int32_t u, int c, int r, int64_t cnt) {
+    int64_t cell = -1, newc = -1;
+    if (u >= 0) {
+      const int64_t e = cnt + r + 1;
+      int64_t slot = -1;
+      if (e <= P.P) {
+        slot = e - 1;
+      } else if (uniform01(rand64(P.seed, P.call, j, 0)) < static_cast<float>(P.P) / static_cast<float>(e)) {
+        slot = static_cast<int64_t>(rand64(P.seed, P.call, j, 1) % static_cast<uint64_t>(P.P));
+      }
+      if (slot >= 0) {
+        const uint64_t k1 = static_cast<uint64_t>(u) * static_cast<uint64_t>(P.P) + static_cast<uint64_t>(slot) + 1u;
+        uint32_t h = np_cell_hash(k1);
+        while (true) {  // terminates: at most n < kNpCells cells are ever taken
+          const unsigned long long old = atomicCAS(&P.ckey[h], 0ull, static_cast<unsigned long long>(k1));
+          if (old == 0ull || old == k1) break;
+          h = (h + 1u) & static_cast<uint32_t>(kNpCells - 1);
+        }
+        atomicMax(&P.cmax[h], static_cast<int32_t>(j + 1));
+        cell = h;
+      }
+      if (r == c - 1) newc = cnt + c;
+    }
+    P.rec[j] = make_longlong2(cell, newc);
+  });
+  const uint64_t bm = __ballot(bad);
+  if ((threadIdx.x & (kWave - 1)) == 0 && bm != 0 && P.status != nullptr)
+    atomicAdd(&P.status[TGX_ST_BAD_EVENT_NODE], __popcll(bm));
+}
+
+__global__ __launch_bounds__(kThreads) void np_commit(const longlong2* __restrict__ rec,
+                                                      const int64_t* __restrict__ src,
+                                                      const int64_t* __restrict__ dst, int64_t n,
+                                                      unsigned long long* ckey, int32_t* cmax,
+                                                      int32_t* __restrict__ pool, int64_t* __restrict__ count) {
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (j >= n) return;
+  const longlong2 r = rec[j];
+  const int64_t v = dst[j];
+  const int64_t u = src[j];
+  if (r.x >= 0) {
+    const int32_t m = cmax[r.x];
+    const unsigned long long k1 = ckey[r.x];
+    if (m == static_cast<int32_t>(j + 1)) {
+      pool[k1 - 1u] = static_cast<int32_t>(v);
+      ckey[r.x] = 0ull;
+      cmax[r.x] = 0;
+    }
+  }
+  if (r.y >= 0) count[u] = r.y;
 }
 
 // Batches of at most 8,192 edges: the whole update in one workgroup (the
@@ -480,6 +573,9 @@ NpLayout np_layout(int64_t n) {
   return w;
 }
 
+// the caller's cell table of the two-launch update: keys, then latest edges
+size_t np_scratch_bytes() { return static_cast<size_t>(kNpCells) * (8 + 4); }
+
 int bits_for(uint64_t max_plus_one) {  // 2^bits - 1 >= max_plus_one - 1 ... and above every valid key
   int bits = 1;
   while (bits < 64 && (uint64_t(1) << bits) < max_plus_one + 1) ++bits;
@@ -510,7 +606,8 @@ namespace {
 int negpool_update(const char* who, int32_t* pool, int64_t* count, int64_t num_nodes, int32_t pool_size,
                    const int64_t* src, const int64_t* dst, int64_t n, uint64_t seed, uint64_t call,
                    const float* u_accept, const int64_t* slot_draw, void* workspace,
-                   size_t workspace_bytes, int32_t* status, hipStream_t stream) {
+                   size_t workspace_bytes, void* scratch, size_t scratch_bytes, int32_t* status,
+                   hipStream_t stream) {
   int rc = check_pool(who, pool, count, num_nodes, pool_size);
   if (rc) return rc;
   if (n < 0 || n >= (int64_t(1) << 31))
@@ -523,6 +620,36 @@ int negpool_update(const char* who, int32_t* pool, int64_t* count, int64_t num_n
   const NpLayout w = np_layout(n);
   if (workspace == nullptr || workspace_bytes < w.total)
     return fail(TGX_ERR_ARG, "%s: workspace of %zu bytes needed, got %zu", who, w.total, workspace_bytes);
+  if (scratch != nullptr) {
+    if (scratch_bytes < np_scratch_bytes())
+      return fail(TGX_ERR_ARG, "%s: scratch of %zu bytes needed, got %zu", who, np_scratch_bytes(), scratch_bytes);
+    if ((reinterpret_cast<uintptr_t>(scratch) & 255u) != 0)
+      return fail(TGX_ERR_ARG, "%s: scratch must be 256-byte aligned", who);
+  }
+  if (scratch != nullptr && !draws && n <= kNpRankMax) {
+    // two launches over the device, the cell table in the caller's scratch
+    NpRankParams R{};
+    R.src = src;
+    R.n = n;
+    R.N = num_nodes;
+    R.P = static_cast<int>(pool_size);
+    R.count = count;
+    R.seed = seed;
+    R.call = call;
+    R.ckey = static_cast<unsigned long long*>(scratch);
+    R.cmax = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(scratch) + kNpCells * 8);
+    R.rec = static_cast<longlong2*>(workspace);
+    R.status = status;
+    if (n <= kThreads)
+      hipLaunchKernelGGL((np_rank<kThreads, 4>), dim3(1), dim3(kThreads), 0, stream, R);
+    else
+      hipLaunchKernelGGL((np_rank<kOrderedMaxThreads, 8>), dim3(static_cast<unsigned>(cdiv(n, kOrderedMaxThreads))),
+                         dim3(kOrderedMaxThreads), 0, stream, R);
+    if ((rc = check_launch("np_rank"))) return rc;
+    hipLaunchKernelGGL(np_commit, dim3(static_cast<unsigned>(cdiv(n, kThreads))), dim3(kThreads), 0, stream,
+                       static_cast<const longlong2*>(R.rec), src, dst, n, R.ckey, R.cmax, pool, count);
+    return check_launch("np_commit");
+  }
   if (n <= 8192 && !draws) {
     // one workgroup: the 4,096-edge shape, or the 8,192-edge one (three digit passes)
     static std::once_flag attr_once;
@@ -592,11 +719,14 @@ int negpool_sample(const char* who, const int32_t* pool, const int64_t* count, i
 
 extern "C" int tgx_negpool_update(int32_t* pool, int64_t* count, int64_t num_nodes, int32_t pool_size,
                                   const int64_t* src, const int64_t* dst, int64_t n, uint64_t seed,
-                                  uint64_t call, void* workspace, size_t workspace_bytes,
-                                  int32_t* status, void* stream) {
+                                  uint64_t call, void* workspace, size_t workspace_bytes, void* scratch,
+                                  size_t scratch_bytes, int32_t* status, void* stream) {
   return negpool_update("tgx_negpool_update", pool, count, num_nodes, pool_size, src, dst, n, seed, call,
-                        nullptr, nullptr, workspace, workspace_bytes, status, static_cast<hipStream_t>(stream));
+                        nullptr, nullptr, workspace, workspace_bytes, scratch, scratch_bytes, status,
+                        static_cast<hipStream_t>(stream));
 }
+
+extern "C" size_t tgx_negpool_scratch_size(void) { return np_scratch_bytes(); }
 
 extern "C" int tgx_negpool_update_draws(int32_t* pool, int64_t* count, int64_t num_nodes, int32_t pool_size,
                                         const int64_t* src, const int64_t* dst, int64_t n,
@@ -605,7 +735,7 @@ extern "C" int tgx_negpool_update_draws(int32_t* pool, int64_t* count, int64_t n
   if (n > 0 && (u_accept == nullptr || slot_draw == nullptr))
     return fail(TGX_ERR_ARG, "tgx_negpool_update_draws: u_accept/slot_draw must not be NULL");
   return negpool_update("tgx_negpool_update_draws", pool, count, num_nodes, pool_size, src, dst, n, 0, 0,
-                        u_accept, slot_draw, workspace, workspace_bytes, status,
+                        u_accept, slot_draw, workspace, workspace_bytes, nullptr, 0, status,
                         static_cast<hipStream_t>(stream));
 }
 

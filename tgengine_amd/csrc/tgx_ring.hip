@@ -93,9 +93,9 @@ struct AppendParams : PlanParams {
   int64_t* eids;
   int32_t* nbase;   // [N] four-launch list base of multi-entry nodes (over lst)
   int32_t* status;
-  int tpe_log2;     // lanes per entry (singleton copy)
-  int ga;           // blocks of the singleton role in commit
-  int gb;           // blocks of the small-group role
+  int tpe_log2;     // lanes per entry (kept_commit, four-launch singletons)
+  int ga;           // four-launch commit: blocks of the singleton role
+  int gb;           // four-launch commit: blocks of the small-group role
 };
 
 // the plan's diagnostics (words time_word, bad_word) reach the status words only

@@ -131,12 +131,11 @@ __device__ __forceinline__ void report_diagnostics(const PlanParams& P, int bad,
   }
 }
 
-// Two-launch plan of entries [block * T, +T), T = blockDim.x (a multiple of
-// kWave, at most kOrderedMaxThreads; every thread of the workgroup calls it).
-// krec[i] = (slot, wp') for entry i: the entry with rank r among the c entries
-// of its node u (in entry order) is kept iff r >= c - kept, kept = min(c, B),
-// and lands in slot (wp[u] + r - (c - kept)) % B; the node's last entry also
-// carries wp' = wp[u] + kept.
+// Ordered ranking of entries [block * T, +T), T = blockDim.x (a multiple of
+// kWave, at most kOrderedMaxThreads; every thread of the workgroup calls it):
+// each entry's rank among its node's entries of the batch in entry order, and
+// the node's count (rank_block below; the two-launch ring plan and the negative
+// pool's update build on it).
 //
 // LDS, plan_lds_bytes(T) (sized so that a gather launch carrying the plan keeps
 // its occupancy), per slot of a hash table of the workgroup's nodes (H >= 2T
@@ -176,8 +175,16 @@ __device__ __forceinline__ uint32_t byte_sum_below(uint32_t x, int upto) {
   return upto <= 0 ? 0u : upto >= 4 ? byte_sum(x) : byte_sum(x & ((1u << (8 * upto)) - 1u));
 }
 
-template <int SCAN>
-__device__ __forceinline__ void plan_block_ordered(const PlanParams& P, int64_t block, uint8_t* smem) {
+// The ranking core, shared with the negative pool's update: entries i of [0, n)
+// with node entry_node(src, dst, i, b) (b = n: src only).  For each entry of
+// the workgroup's range it calls fin(i, u, c, r, w): u its node (-1 when outside
+// [0, N)), c the node's entries in the batch, r the entry's rank among them in
+// entry order, w = nval[u] (loaded early; nval may be NULL).  Returns 1 for a
+// calling thread whose entry's node is out of range.
+template <int SCAN, class Fin>
+__device__ __forceinline__ int rank_block(const int64_t* src, const int64_t* dst, int64_t b, int64_t n,
+                                          int64_t N, const int64_t* nval, int64_t block, uint8_t* smem,
+                                          Fin&& fin) {
   const int T = static_cast<int>(blockDim.x);
   const int t = threadIdx.x;
   const int wv = t / kWave;
@@ -190,23 +197,18 @@ __device__ __forceinline__ void plan_block_ordered(const PlanParams& P, int64_t 
   uint8_t* wcnt = smem + static_cast<size_t>(4 + 4 * kPlanSets) * H;              // [H][stride]
   const int set = wv % kPlanSets;
   const int64_t lo = block * T;
-  const int64_t hi = lo + T < P.n ? lo + T : P.n;
+  const int64_t hi = lo + T < n ? lo + T : n;
   const int64_t i = lo + t;
-  // the entry's node and time, then the first step of the batch scan (node ids
-  // of the entries outside [lo, hi)), all before any of them is waited for
-  int64_t uu = -1;
-  double ti = 0.0;
-  if (i < P.n) {
-    uu = entry_node(P.src, P.dst, i, P.b);
-    if (i < P.b) ti = P.time[i];
-  }
+  // the entry's node, then the first step of the batch scan (node ids of the
+  // entries outside [lo, hi)), all before any of them is waited for
+  const int64_t uu = i < n ? entry_node(src, dst, i, b) : -1;
   const int64_t step = static_cast<int64_t>(T) * SCAN;
   int64_t nx[SCAN];
   auto fetch = [&](int64_t j0) {
 #pragma unroll
     for (int k = 0; k < SCAN; ++k) {
       const int64_t j = j0 + static_cast<int64_t>(k) * T + t;
-      nx[k] = (j < P.n && (j < lo || j >= hi)) ? entry_node(P.src, P.dst, j, P.b) : -1;
+      nx[k] = (j < n && (j < lo || j >= hi)) ? entry_node(src, dst, j, b) : -1;
     }
   };
   fetch(0);
@@ -214,10 +216,10 @@ __device__ __forceinline__ void plan_block_ordered(const PlanParams& P, int64_t 
   for (int s = t; s < kPlanSets * H; s += T) hba[s] = 0u;
   for (int s = t; s < stride * H / 4; s += T) reinterpret_cast<uint32_t*>(wcnt)[s] = 0u;
   __syncthreads();
-  const int bad = i < P.n && (uu < 0 || uu >= P.N) ? 1 : 0;
-  const int32_t u = i < P.n && !bad ? static_cast<int32_t>(uu) : -1;
-  // the write position is needed last
-  const int64_t w = u >= 0 ? P.wpos[u] : 0;
+  const int bad = i < n && (uu < 0 || uu >= N) ? 1 : 0;
+  const int32_t u = i < n && !bad ? static_cast<int32_t>(uu) : -1;
+  // the node's value is needed last
+  const int64_t w = u >= 0 && nval != nullptr ? nval[u] : 0;
   int hs = -1;
   if (u >= 0) {
     hs = plan_hash(u, hbits);
@@ -253,15 +255,15 @@ __device__ __forceinline__ void plan_block_ordered(const PlanParams& P, int64_t 
   __syncthreads();
   // the batch outside [lo, hi): entries of this workgroup's nodes before and
   // after it
-  for (int64_t j0 = 0; j0 < P.n; j0 += step) {  // workgroup-uniform
+  for (int64_t j0 = 0; j0 < n; j0 += step) {  // workgroup-uniform
     int64_t cur[SCAN];
 #pragma unroll
     for (int k = 0; k < SCAN; ++k) cur[k] = nx[k];
-    if (j0 + step < P.n) fetch(j0 + step);
+    if (j0 + step < n) fetch(j0 + step);
 #pragma unroll
     for (int k = 0; k < SCAN; ++k) {
       int s = -1;
-      if (cur[k] >= 0 && cur[k] < P.N) {
+      if (cur[k] >= 0 && cur[k] < N) {
         const int32_t x = static_cast<int32_t>(cur[k]);
         s = plan_hash(x, hbits);
         int32_t key = hkey[s];
@@ -283,8 +285,8 @@ __device__ __forceinline__ void plan_block_ordered(const PlanParams& P, int64_t 
     }
   }
   __syncthreads();
-  if (i < P.n) {
-    int64_t slot = -1, wnew = -1;
+  if (i < n) {
+    int c = 0, r = 0;
     if (u >= 0) {
       const uint4 ba = *reinterpret_cast<const uint4*>(&hba[static_cast<size_t>(hs) * kPlanSets]);
       const int before = static_cast<int>((ba.x & 0xffffu) + (ba.y & 0xffffu) + (ba.z & 0xffffu) + (ba.w & 0xffffu));
@@ -306,8 +308,27 @@ __device__ __forceinline__ void plan_block_ordered(const PlanParams& P, int64_t 
         mine += static_cast<int>(byte_sum(cw[q]));
         below += static_cast<int>(byte_sum_below(cw[q], wv - 4 * q));
       }
-      const int c = before + mine + after;
-      const int r = before + below + wrank;
+      c = before + mine + after;
+      r = before + below + wrank;
+    }
+    fin(i, u, c, r, w);
+  }
+  return bad;
+}
+
+// The ring plan of entries [block * T, +T), on rank_block: the entry with rank r
+// among the c entries of its node u is kept iff m = r - (c - kept) >= 0, kept =
+// min(c, B), and lands in slot (wp[u] + m) % B; the node's last entry carries
+// wp' = wp[u] + kept.  krec[i] = (slot, wp'), -1 for none.
+template <int SCAN>
+__device__ __forceinline__ void plan_block_ordered(const PlanParams& P, int64_t block, uint8_t* smem) {
+  const int64_t i = block * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+  // the time is loaded first and used last (the reference key's check)
+  const double ti = i < P.b ? P.time[i] : 0.0;
+  const int bad = rank_block<SCAN>(P.src, P.dst, P.b, P.n, P.N, P.wpos, block, smem,
+                                   [&](int64_t e, int32_t u, int c, int r, int64_t w) {
+    int64_t slot = -1, wnew = -1;
+    if (u >= 0) {
       const int kept = c < P.B ? c : P.B;
       const int m = r - (c - kept);
       if (m >= 0) {
@@ -316,8 +337,8 @@ __device__ __forceinline__ void plan_block_ordered(const PlanParams& P, int64_t 
       }
       if (r == c - 1) wnew = w + kept;
     }
-    reinterpret_cast<longlong2*>(P.krec)[i] = make_longlong2(slot, wnew);
-  }
+    reinterpret_cast<longlong2*>(P.krec)[e] = make_longlong2(slot, wnew);
+  });
   const bool time_ok = i < P.b && trunc(ti) > static_cast<double>(P.n - 3);
   report_diagnostics(P, bad, time_ok, kCtlKTime, kCtlKBad);
 }

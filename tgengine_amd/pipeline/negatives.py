@@ -62,6 +62,9 @@ class HistoricalNegPool:
         self._call = 0
         self._status = torch.zeros(_lib.TGX_STATUS_WORDS, dtype=torch.int32, device=self.device)
         self._ws: Optional[Tensor] = None
+        # the update's cell table (zero-filled once; every update leaves it zeroed)
+        self._scratch = torch.zeros(int(_lib.lib().tgx_negpool_scratch_size()), dtype=torch.uint8,
+                                    device=self.device)
 
     def _ids(self, t: Tensor) -> Tensor:
         return t.detach().to(self.device, torch.int64).contiguous().reshape(-1)
@@ -94,7 +97,8 @@ class HistoricalNegPool:
             _lib.check(_lib.lib().tgx_negpool_update(
                 self._pool.data_ptr(), self._count.data_ptr(), self.num_nodes, self.pool_size,
                 s.data_ptr(), d.data_ptr(), n, self.seed, self._call, self._ws.data_ptr(),
-                self._ws.numel(), self._status.data_ptr(), _stream_handle(self.device)), "tgx_negpool_update")
+                self._ws.numel(), self._scratch.data_ptr(), self._scratch.numel(), self._status.data_ptr(),
+                _stream_handle(self.device)), "tgx_negpool_update")
         self._call += 1
 
     def sample(self, src: Tensor) -> Tensor:
