@@ -375,8 +375,10 @@ int tgx_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args* 
 
 /* Launch shape tgx_recent would use for these arguments, without launching:
  * shape[0] workgroups, [1] threads per workgroup, [2] dynamic LDS bytes,
- * [3] queries per wavefront, [4] wavefronts per query, [5] queries per
- * workgroup, [6] plan workgroups, [7] feature copy width in bytes.  Same
+ * [3] queries per wavefront, [4] wavefronts per query in one workgroup (a
+ * query split over more than 4 wavefronts without a ring spreads them over
+ * several workgroups), [5] queries per workgroup (1 also for those),
+ * [6] plan workgroups, [7] feature copy width in bytes.  Same
  * argument checks and return codes as tgx_recent. */
 int tgx_recent_launch_shape(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args* args,
                             int64_t shape[8]);

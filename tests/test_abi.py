@@ -192,7 +192,10 @@ def test_launch_shapes_stay_within_the_kernel_bounds():
     a = _lib.TgxRecentArgs(k=3, group=4, num_queries=1, nodes=8, times=8, out_ids=8, out_times=8,
                            out_mask=8, out_feats=16)
     rc, sh = _shape(None, ctypes.byref(csr), a)
-    assert rc == 0 and sh[1] == 512 and sh[4] == 8 and sh[0] == 1  # one query over 8 waves
+    # one query over 8 waves: without a ring, two workgroups of 4
+    assert rc == 0 and sh[1] == 256 and sh[4] == 4 and sh[0] == 2 and sh[5] == 1
+    rc, sh = _shape(ctypes.byref(ring), ctypes.byref(csr), a)
+    assert rc == 0 and sh[1] == 512 and sh[4] == 8 and sh[0] == 1  # with a ring: one workgroup
 
 
 def test_ring_less_launches_pack_queries_in_csr_window():

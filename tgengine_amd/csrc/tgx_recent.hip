@@ -131,6 +131,7 @@ struct Params {
   // |dt| below which no encoding argument reaches kRevArg (0: none is known)
   float te_dt_small;
   double c_tmax;  // largest non-NaN CSR time (+inf: unknown)
+  int wg_parts;   // csr_split: workgroups per query (1: a workgroup holds whole queries)
 };
 
 template <int VEC>
@@ -204,6 +205,10 @@ constexpr int64_t kDeviceCUs = 256;
 
 // row chunks each lane loads before storing them (large-row copy)
 constexpr int kCopyDepth = 4;
+// csr_split: a query split over more wavefronts than this spreads them over
+// workgroups of this many (Reddit's 600 queries x 8 waves: 12.3 -> 11.7 us, LastFM's
+// 31.5 -> 30.0 us; 2 or 1 wave per workgroup measured no better)
+constexpr int kSplitGroupWaves = 4;
 // node ids per thread and step of the ring plan's batch scan when the plan runs
 // in a gather launch (its registers stay within the gather's)
 constexpr int kFusedPlanScan = 4;
@@ -1011,8 +1016,11 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void csr_split(Params P) {
   const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
   const int K = P.K;
   const int split = P.split;
-  const int qs = wv / split;
-  const int part = wv - qs * split;
+  // the query's waves: `split` of one workgroup, or spread over wg_parts workgroups
+  const int wpw = static_cast<int>(blockDim.x) / kWave;
+  const int qs = P.wg_parts > 1 ? 0 : wv / split;
+  const int part = P.wg_parts > 1 ? static_cast<int>(blockIdx.x % static_cast<unsigned>(P.wg_parts)) * wpw + wv
+                                  : wv - qs * split;
   const int per = RANGES ? (K + split - 1) / split : K;
   const int p0 = RANGES ? part * per : 0;
   const int np = K - p0 < per ? (K - p0 > 0 ? K - p0 : 0) : per;  // the wave's positions
@@ -1036,7 +1044,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void csr_split(Params P) {
   int32_t* pcode = reinterpret_cast<int32_t*>(wb);        // [per] 0 entry, -1 pad
   float* pdt = reinterpret_cast<float*>(wb + P.off_pdt);  // [per] dt
 
-  int64_t q = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave / split) + qs;
+  int64_t q = P.wg_parts > 1 ? static_cast<int64_t>(blockIdx.x / static_cast<unsigned>(P.wg_parts))
+                              : static_cast<int64_t>(blockIdx.x) * (wpw / split) + qs;
   if (q >= P.Q) q = -1;
   int64_t node = -1;
   double qt = 0.0;
@@ -1578,6 +1587,14 @@ int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args
     const int per = L.csr_ranges ? (K + split - 1) / split : K;
     P.off_pdt = round16(per * 4);
     P.wave_bytes = 2 * round16(per * 4);
+    // a query's waves spread over workgroups of kSplitGroupWaves (its waves share
+    // nothing but the encoder weights, which each workgroup loads): finer
+    // workgroups even out the CUs
+    if (qslots == 1 && split > kSplitGroupWaves) {
+      P.wg_parts = split / kSplitGroupWaves;
+      waves = kSplitGroupWaves;
+      nblocks = a->num_queries * P.wg_parts;
+    }
     lds = static_cast<size_t>(P.te_bytes) + static_cast<size_t>(waves) * P.wave_bytes;
   }
 
@@ -1692,7 +1709,8 @@ extern "C" int tgx_recent_launch_shape(const tgx_ring* ring, const tgx_csr* csr,
   shape[1] = L.threads;
   shape[2] = static_cast<int64_t>(L.lds);
   shape[3] = L.P.m;
-  shape[4] = L.P.plan_mode == TGX_PLAN_TILES ? L.P.split : 1 << L.P.split;
+  shape[4] = L.P.plan_mode == TGX_PLAN_TILES ? L.P.split / (L.P.wg_parts > 1 ? L.P.wg_parts : 1)
+                                             : 1 << L.P.split;
   shape[5] = static_cast<int64_t>(L.qslots) * L.P.m;
   shape[6] = L.P.plan_blocks;
   shape[7] = L.vec;
