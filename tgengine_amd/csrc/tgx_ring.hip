@@ -444,13 +444,14 @@ __global__ __launch_bounds__(kThreads) void append_commit(AppendParams P) {
 // written to its slot.  Rows longer than kKeptDepth chunks per lane continue in
 // rounds of kKeptDepth loads, then stores.  Workgroup 0 reports and clears the
 // plan's diagnostics.
+constexpr int kKeptThreads = 256;
 template <int VEC>
-__global__ __launch_bounds__(kThreads) void kept_commit(AppendParams P) {
+__global__ __launch_bounds__(kKeptThreads) void kept_commit(AppendParams P) {
   using V = typename VecT<VEC>::T;
   if (blockIdx.x == 0 && threadIdx.x == 0) commit_diagnostics(P, kCtlKTime, kCtlKBad);
   const int nv = static_cast<int>(P.row_bytes / VEC);
   const int tpe = 1 << P.tpe_log2;
-  const int epb = kThreads >> P.tpe_log2;
+  const int epb = kKeptThreads >> P.tpe_log2;
   const int64_t i = static_cast<int64_t>(blockIdx.x) * epb + (threadIdx.x >> P.tpe_log2);
   const int l = threadIdx.x & (tpe - 1);
   if (i >= P.n) return;
@@ -656,9 +657,9 @@ int setup_append(const char* who, const tgx_ring* ring, const int64_t* src, cons
 template <int VEC>
 void launch_commit_vec(const AppendParams& P, hipStream_t stream) {
   if (plan_fused_ok(P)) {
-    const int64_t epb = kThreads >> P.tpe_log2;
+    const int64_t epb = kKeptThreads >> P.tpe_log2;
     hipLaunchKernelGGL(kept_commit<VEC>, dim3(static_cast<unsigned>((P.n + epb - 1) / epb)),
-                       dim3(kThreads), 0, stream, P);
+                       dim3(kKeptThreads), 0, stream, P);
   } else {
     const int64_t gc = std::min<int64_t>(P.n / (kWave + 1) + 1, kLargeGroupBlocks);
     hipLaunchKernelGGL(append_commit<VEC>, dim3(static_cast<unsigned>(P.ga + P.gb + gc)),
