@@ -132,6 +132,7 @@ struct Params {
   float te_dt_small;
   double c_tmax;  // largest non-NaN CSR time (+inf: unknown)
   int wg_parts;   // csr_split: workgroups per query (1: a workgroup holds whole queries)
+  int te_nt;      // csr_split: nontemporal encoding stores (rows of at least kNtRowBytes)
 };
 
 template <int VEC>
@@ -209,6 +210,9 @@ constexpr int kCopyDepth = 4;
 // workgroups of this many (Reddit's 600 queries x 8 waves: 12.3 -> 11.7 us, LastFM's
 // 31.5 -> 30.0 us; 2 or 1 wave per workgroup measured no better)
 constexpr int kSplitGroupWaves = 4;
+// csr_split: rows of at least this many bytes stream, and the encodings beside
+// them go out as nontemporal stores
+constexpr int64_t kNtRowBytes = 64;
 // node ids per thread and step of the ring plan's batch scan when the plan runs
 // in a gather launch (its registers stay within the gather's)
 constexpr int kFusedPlanScan = 4;
@@ -1139,10 +1143,20 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void csr_split(Params P) {
       }
       const bool te_big = __ballot(big) != 0;
       wave_sync();
-      if (te_big)
-        encode_rows<true, true>(P, q * K + p0, np, pcode, pdt, s_w, s_b, off + lane, cstride);
-      else
-        encode_rows<false, true>(P, q * K + p0, np, pcode, pdt, s_w, s_b, off + lane, cstride);
+      // nontemporal encodings beside rows that stream; ordinary stores beside small
+      // rows, where the encodings are the launch's bytes (LastFM's 8-byte rows at
+      // K = 512: 29.9 -> 25.1 us; with 688-byte rows nontemporal stays faster)
+      if (P.te_nt) {
+        if (te_big)
+          encode_rows<true, true>(P, q * K + p0, np, pcode, pdt, s_w, s_b, off + lane, cstride);
+        else
+          encode_rows<false, true>(P, q * K + p0, np, pcode, pdt, s_w, s_b, off + lane, cstride);
+      } else {
+        if (te_big)
+          encode_rows<true, false>(P, q * K + p0, np, pcode, pdt, s_w, s_b, off + lane, cstride);
+        else
+          encode_rows<false, false>(P, q * K + p0, np, pcode, pdt, s_w, s_b, off + lane, cstride);
+      }
     }
     // ---- ids / times / mask / edge ids (without ranges: the query's first wave) ----
     if (lane < np && (RANGES || part == 0)) {
@@ -1596,6 +1610,7 @@ int setup_recent(const tgx_ring* ring, const tgx_csr* csr, const tgx_recent_args
       nblocks = a->num_queries * P.wg_parts;
     }
     lds = static_cast<size_t>(P.te_bytes) + static_cast<size_t>(waves) * P.wave_bytes;
+    P.te_nt = P.row_bytes >= kNtRowBytes ? 1 : 0;
   }
 
   // fused plan: one plan workgroup per blockDim entries, dispatched first
