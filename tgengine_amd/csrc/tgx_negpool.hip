@@ -9,14 +9,18 @@
 // accepted edges on one (u, slot) by whichever index_put_ write lands last;
 // here the later edge of the batch wins.  count[u] += (edges of u).
 //
-// Batches of more than 8,192 edges (several launches):
+// With the caller's cell table (scratch), batches of up to 32,768 edges: two
+// launches over the device (np_rank, np_commit below): ordered ranks from an LDS
+// hash of each workgroup's sources and one scan of the batch, the decisions, and
+// the latest edge per cell u*P + slot by atomicMax in the table.
+// Otherwise, batches of more than 8,192 edges (several launches):
 //   1. stable radix sort of the edges by source (tgx_radix.h): r = position
 //      - start of the source's run;
 //   2. decide: fill / replace / skip, and the key u*P + slot of accepted edges;
 //   3. stable radix sort of accepted edges by that key: the last of each equal
 //      run is the latest edge, which writes the slot;
 //   4. counts: the last edge of each source run adds the run length.
-// Batches of up to 8,192 edges: the same steps in one workgroup
+// and batches of up to 8,192 edges: the same steps in one workgroup
 // (np_update_small below), grouping sources through LDS hash tables.
 //
 // sample(src): with v = min(count[u], P) valid slots (slots fill in order, so
