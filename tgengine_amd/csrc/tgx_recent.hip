@@ -259,6 +259,39 @@ __device__ __forceinline__ int64_t wave_lower_bound(const double* __restrict__ t
   return lo + __popcll(__ballot(pr));
 }
 
+// wave_lower_bound<true> run by every sub-group of Bp = 2^lg lanes at once on
+// its own query (lo, hi and q uniform within the sub-group h; active: whether
+// the sub-group searches at all): Bp-ary rounds with probes clamped to hi - 1,
+// until at most Bp entries are left.  Returns the first index in [lo, hi] whose
+// time is not below q.
+__device__ __forceinline__ int64_t subgroup_lower_bound(const double* __restrict__ t, int64_t lo, int64_t hi,
+                                                        double q, bool active, int sl, int h, int lg) {
+  const int Bp = 1 << lg;
+  const uint64_t submask = Bp == kWave ? ~uint64_t(0) : ((uint64_t(1) << Bp) - 1);
+  while (true) {
+    const bool more = active && hi - lo > Bp;
+    if (__ballot(more) == 0) break;  // wave-uniform
+    int64_t step = 0;
+    bool pr = false;
+    if (more) {
+      step = (hi - lo + Bp - 1) >> lg;
+      const int64_t pos0 = lo + static_cast<int64_t>(sl + 1) * step - 1;
+      pr = t[pos0 < hi ? pos0 : hi - 1] < q;
+    }
+    const uint64_t below = (__ballot(more && pr) >> (h << lg)) & submask;
+    if (more) {
+      const int64_t c = __popcll(below);
+      const int64_t pc = lo + (c + 1) * step - 1;
+      const int64_t nl = lo + c * step;
+      lo = nl < hi ? nl : hi;
+      hi = pc < hi ? pc : hi;
+    }
+  }
+  const int64_t pos = lo + sl;
+  const bool pr = active && pos < hi && t[pos] < q;
+  return lo + __popcll((__ballot(pr) >> (h << lg)) & submask);
+}
+
 // Query j of plan group g (-1: none).  Event-major groups: group g is event g,
 // and its j-th query is, for each query group in order, one of that group's
 // times_per queries of event g; every query group holds b x times_per queries,
@@ -939,16 +972,9 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void csr_window(Params P) {
       lo = nl < s1 ? nl : s1;
       hi = pc < s1 ? pc : s1;
     }
-    int64_t cnt = 0;
-    for (int hh = 0; hh < m; ++hh) {
-      if (((slow >> (hh << lg)) & 1u) == 0) continue;  // wave-uniform
-      const int src = hh << lg;
-      const int64_t a0 = __shfl(lo, src);
-      const int64_t a1 = __shfl(hi, src);
-      const double th = __shfl(qt, src);
-      const int64_t b = wave_lower_bound<true>(P.c_times, a0, a1, th, lane);
-      if (h == hh) cnt = b - s0;
-    }
+    // every sub-group searches its own query at once (Bp-ary rounds; one query
+    // after another with 64-ary rounds took 2 x 3 rounds for C3's hop-2 windows)
+    const int64_t cnt = subgroup_lower_bound(P.c_times, lo, hi, qt, !after, sl, h, lg) - s0;
     if (!after) {
       const int take = static_cast<int>(cnt < K ? cnt : K);
       have = sl < K && sl >= K - take;
