@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define TGX_ABI_VERSION 15
+#define TGX_ABI_VERSION 16
 
 /* status codes */
 #define TGX_OK 0
@@ -314,6 +314,25 @@ typedef struct tgx_csr_build_args {
 
 size_t tgx_csr_build_workspace_size(int64_t num_entries);
 int tgx_csr_build(const tgx_csr_build_args* args, void* stream);
+
+/* Pre-freeze scan.  No counterpart in the reference, whose freeze_csr
+ * (temporal_graph.py:133-181) sorts host lists; here freeze_csr learns from it,
+ * in one round trip, the node range it checks, which build to run (event pairs
+ * or general) and the largest time.  Over the num_events > 0 events src/dst/time of the pre-freeze
+ * advance() calls, whose first events are call_starts [num_calls] (sorted,
+ * may be NULL when num_calls is 0), writes out int64 [4]:
+ *   out[0], out[1]  min and max node id over src and dst,
+ *   out[2]          1 when the stream is time-ordered in the sense of
+ *                   TGX_CSR_EVENT_PAIRS, else 0: for every k >= 1 the float64
+ *                   difference time[k] - time[k-1] is > 0, or == 0 with k in
+ *                   call_starts (NaN and inf - inf differences break it),
+ *   out[3]          the bits of the largest non-NaN time (-inf when all are NaN).
+ * workspace: tgx_csr_scan_workspace_size() bytes, no initialisation needed.
+ * Two launches; the caller reads out after the stream. */
+size_t tgx_csr_scan_workspace_size(void);
+int tgx_csr_scan(const int64_t* src, const int64_t* dst, const double* time, int64_t num_events,
+                 const int64_t* call_starts, int64_t num_calls, int64_t* out, void* workspace,
+                 size_t workspace_bytes, void* stream);
 
 /* Historical negative pool (HistoricalNegPool, pipeline/negatives.py:14-126).
  * pool int32 [num_nodes, pool_size] (-1 = empty), count int64 [num_nodes]

@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(L, n), n
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
-    assert L.tgx_abi_version() == _lib.TGX_ABI_VERSION == 15
+    assert L.tgx_abi_version() == _lib.TGX_ABI_VERSION == 16
     nm = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
                         text=True).stdout
     exported = set(re.findall(r"\bT (tgx_\w+)", nm))
@@ -345,6 +345,19 @@ def test_csr_build_argument_checks():
     # workspace: keys, values and node keys double-buffered, plus the digit counts
     assert L.tgx_csr_build_workspace_size(1 << 20) >= (1 << 20) * 32 + 256 * 512 * 4
     assert L.tgx_csr_build_workspace_size(0) > 0
+
+
+def test_csr_scan_argument_checks():
+    L = _lib.lib()
+    ws = L.tgx_csr_scan_workspace_size()
+    assert ws >= 1024 * 32
+    assert L.tgx_csr_scan(8, 8, 8, 0, None, 0, 8, 8, ws, None) == 1 and "positive" in _err()
+    assert L.tgx_csr_scan(8, 8, 8, 5, None, -1, 8, 8, ws, None) == 1 and "num_calls" in _err()
+    assert L.tgx_csr_scan(8, None, 8, 5, None, 0, 8, 8, ws, None) == 1 and "NULL" in _err()
+    assert L.tgx_csr_scan(8, 8, 8, 5, None, 2, 8, 8, ws, None) == 1 and "call_starts" in _err()
+    assert L.tgx_csr_scan(8, 8, 8, 5, None, 0, None, 8, ws, None) == 1 and "NULL" in _err()
+    assert L.tgx_csr_scan(8, 8, 8, 5, 8, 1, 8, 8, ws - 1, None) == 1 and "workspace" in _err()
+    assert L.tgx_csr_scan(8, 8, 8, 5, 8, 1, 8, None, ws, None) == 1 and "workspace" in _err()
 
 
 def test_negpool_argument_checks():

@@ -7,12 +7,15 @@ entries, hot nodes, one to several thousand radix tiles (and one build large
 enough for a three-level scan of the digit counts), f32 / bf16 / odd / zero
 row widths, batches without features, empty builds and out-of-range ids.
 """
+import struct
+
 import numpy as np
 import pytest
 import torch
 
 from oracle import spec as O
 from tgengine_amd import TemporalGraph
+from tgengine_amd.core import _lib
 from tgengine_amd.synthetic import f32_to_bf16_bits
 
 pytestmark = pytest.mark.gpu
@@ -178,6 +181,64 @@ def test_csr_build_almost_ordered_stream_sorts_by_time(where):
     g, ref = _build(40, 4, False, batches, True)
     assert not g._csr_time_sorted
     _compare(g, ref)
+
+
+def _scan(src, dst, t, starts):
+    """tgx_csr_scan on device copies: (lo, hi, ordered, largest non-NaN time)."""
+    L = _lib.lib()
+    s, d, tt = (torch.from_numpy(np.ascontiguousarray(x)).cuda() for x in (src, dst, t))
+    st = torch.tensor(starts, dtype=torch.int64, device="cuda")
+    ws = torch.empty(int(L.tgx_csr_scan_workspace_size()), dtype=torch.uint8, device="cuda")
+    out = torch.full((4,), 7, dtype=torch.int64, device="cuda")
+    assert L.tgx_csr_scan(s.data_ptr(), d.data_ptr(), tt.data_ptr(), len(src), st.data_ptr() if len(starts) else None,
+                          len(starts), out.data_ptr(), ws.data_ptr(), ws.numel(), None) == 0
+    lo, hi, ordered, bits = out.cpu().tolist()
+    return lo, hi, ordered, struct.unpack("<d", struct.pack("<q", bits))[0]
+
+
+@pytest.mark.parametrize("E", [1, 2, 255, 1024, 1025, 262_145, 1_500_001])
+def test_csr_scan_known_cases(E):
+    """The pre-freeze scan on streams whose answers are fixed by construction:
+    strictly increasing times with ties only at call starts are ordered; one tie
+    inside a call, a step back, a NaN or inf followed by inf is not, wherever it
+    sits (first step, a workgroup boundary, the last event); the node range comes
+    from planted extremes and the largest time skips NaN."""
+    rng = np.random.default_rng(E)
+    t = np.cumsum(rng.uniform(0.5, 1.5, E))
+    starts = sorted({0, *rng.integers(1, E, min(E - 1, 50)).tolist()}) if E > 1 else [0]
+    for k in starts[1:]:  # tie each call's first event with the previous one
+        t[k:] -= t[k] - t[k - 1]
+        t[k] = t[k - 1]
+    src = rng.integers(10, 1000, E)
+    dst = rng.integers(10, 1000, E)
+    src[-1], dst[E // 2] = 3, 5000
+    lo, hi, ordered, tmax = _scan(src, dst, t, starts)
+    assert (lo, hi, ordered, tmax) == (min(3, int(dst.min())), 5000, 1, float(t.max()))
+    if E < 2:
+        return
+    inner = [k for k in (1, E // 2, 1024, 4 * 256 * 1024, E - 1) if 0 < k < E and k not in starts]
+    for k in inner:
+        for kind in ("tie", "back", "nan", "inf"):
+            u = t.copy()
+            if kind == "tie":
+                u[k] = u[k - 1]
+            elif kind == "back":
+                u[k] = u[k - 1] - 1e-9
+            elif kind == "nan":
+                u[k] = np.nan
+            else:
+                u[k - 1] = u[k] = np.inf
+            got = _scan(src, dst, u, starts)
+            assert got[2] == 0, (k, kind)
+            want = np.inf if kind == "inf" else float(np.nanmax(u))
+            assert got[3] == want, (k, kind)
+    # -0.0 after +0.0 is a zero step: ordered only at a call start
+    z = np.zeros(2)
+    z[1] = -0.0
+    assert _scan(src[:2], dst[:2], z, [0, 1])[2] == 1
+    assert _scan(src[:2], dst[:2], z, [0])[2] == 0
+    # every time NaN: no largest time
+    assert _scan(src[:2], dst[:2], np.full(2, np.nan), [0, 1])[3] == -np.inf
 
 
 def test_csr_build_rejects_out_of_range_nodes():

@@ -24,7 +24,7 @@ TGX_CO_DYGFORMER = 2
 TGX_PLAN_TILES = 0
 TGX_PLAN_EVENTS = 1
 TGX_PLAN_LIST = 2
-TGX_ABI_VERSION = 15
+TGX_ABI_VERSION = 16
 TGX_STATUS_WORDS = 8
 TGX_ST_BAD_EVENT_NODE = 0
 TGX_ST_KEY_COLLISION = 1
@@ -108,6 +108,8 @@ SIGNATURES = {
     "tgx_co_occurrence": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i32, c_vp, c_vp, c_vp, c_vp]),
     "tgx_csr_build": (c_i32, [ctypes.POINTER(TgxCsrBuildArgs), c_vp]),
     "tgx_csr_build_workspace_size": (ctypes.c_size_t, [c_i64]),
+    "tgx_csr_scan": (c_i32, [c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, ctypes.c_size_t, c_vp]),
+    "tgx_csr_scan_workspace_size": (ctypes.c_size_t, []),
     "tgx_negpool_update_workspace_size": (ctypes.c_size_t, [c_i64]),
     "tgx_negpool_scratch_size": (ctypes.c_size_t, []),
     "tgx_negpool_update": (c_i32, [c_vp, c_vp, c_i64, c_i32, c_vp, c_vp, c_i64, ctypes.c_uint64,

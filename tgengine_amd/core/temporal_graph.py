@@ -21,6 +21,7 @@ Extensions (keyword-only, defaults match the reference):
 from __future__ import annotations
 
 import ctypes
+import struct
 import threading
 from dataclasses import dataclass
 from typing import Optional
@@ -427,21 +428,18 @@ class TemporalGraph:
             bufs = self._build
             src, dst, tt = bufs["src"][:E], bufs["dst"][:E], bufs["time"][:E]
             feats = bufs["feat"][:E] if "feat" in bufs else None
-            # one device round trip: node range, whether the stream is time-ordered,
-            # and the largest non-NaN time
-            lo = torch.minimum(src.min(), dst.min())
-            hi = torch.maximum(src.max(), dst.max())
-            tmax = torch.where(torch.isnan(tt), float("-inf"), tt).max()
-            if E > 1:
-                step = tt[1:] - tt[:-1]
-                first = torch.zeros(E, dtype=torch.bool, device=dev)
-                first[torch.tensor(self._build_starts, dtype=torch.int64).to(dev)] = True
-                ordered = ((step > 0) | ((step == 0) & first[1:])).all()
-            else:
-                ordered = torch.ones((), dtype=torch.bool, device=dev)
-            host = torch.stack([lo.double(), hi.double(), ordered.double(), tmax]).cpu().tolist()
-            lo, hi, ordered = (int(x) for x in host[:3])  # node ids below 2^53: exact
-            self._csr_max_time = host[3]
+            # one device round trip (tgx_csr_scan): node range, whether the stream
+            # is time-ordered, and the largest non-NaN time
+            L = _lib.lib()
+            ws = torch.empty(max(int(L.tgx_csr_build_workspace_size(n)), int(L.tgx_csr_scan_workspace_size())),
+                             dtype=torch.uint8, device=dev)
+            call_starts = torch.tensor(self._build_starts, dtype=torch.int64).to(dev)
+            scan = torch.empty(4, dtype=torch.int64, device=dev)
+            _lib.check(L.tgx_csr_scan(src.data_ptr(), dst.data_ptr(), tt.data_ptr(), E, call_starts.data_ptr(),
+                                      call_starts.numel(), scan.data_ptr(), ws.data_ptr(), ws.numel(),
+                                      _stream_handle(dev)), "tgx_csr_scan")
+            lo, hi, ordered, tbits = scan.cpu().tolist()
+            self._csr_max_time = struct.unpack("<d", struct.pack("<q", tbits))[0]
             if lo < 0 or hi >= N:
                 raise IndexError("advance() got node ids outside [0, num_nodes)")
             flags = 0
@@ -462,7 +460,6 @@ class TemporalGraph:
                 frm = torch.where(rev, dst[ev], src[ev])
                 to = torch.where(rev, src[ev], dst[ev])
                 tm = tt[ev]
-            ws = torch.empty(int(_lib.lib().tgx_csr_build_workspace_size(n)), dtype=torch.uint8, device=dev)
             a = _lib.TgxCsrBuildArgs(
                 num_nodes=N, num_entries=n, from_=frm.data_ptr(), to=to.data_ptr(),
                 time=tm.data_ptr(), event=_lib.ptr(ev),
@@ -474,7 +471,7 @@ class TemporalGraph:
                 out_feats=self._nbr_feats.data_ptr() if d > 0 else None,
                 out_eids=_lib.ptr(self._nbr_eids), workspace=ws.data_ptr(),
                 workspace_bytes=ws.numel(), status=self._status.data_ptr(), flags=flags)
-            _lib.check(_lib.lib().tgx_csr_build(ctypes.byref(a), _stream_handle(dev)), "tgx_csr_build")
+            _lib.check(L.tgx_csr_build(ctypes.byref(a), _stream_handle(dev)), "tgx_csr_build")
         self._frozen = True
         self._build = {}
         self._build_n = 0

@@ -134,6 +134,98 @@ __global__ __launch_bounds__(kThreads) void csr_gather(
     atomicAdd(&status[TGX_ST_BAD_EVENT_NODE], __popcll(bm));
 }
 
+// Pre-freeze scan (tgx_csr_scan): node range, time order and largest time of the
+// events in one pass.  Each workgroup reduces a grid-stride share into one
+// ScanPart; csr_scan_final folds the parts.
+constexpr int kScanParts = 1024;
+
+struct ScanPart {
+  int64_t lo, hi, bad;
+  double tmax;
+};
+
+// is k one of the sorted call starts?
+__device__ __forceinline__ bool is_call_start(const int64_t* __restrict__ starts, int64_t m, int64_t k) {
+  int64_t lo = 0, hi = m;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (starts[mid] < k)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  return lo < m && starts[lo] == k;
+}
+
+// block-wide fold of (lo, hi, bad, tmax); the result is valid in thread 0
+__device__ __forceinline__ ScanPart fold_block(ScanPart v, ScanPart* sm) {
+  for (int o = kWave / 2; o > 0; o >>= 1) {
+    v.lo = min(v.lo, static_cast<int64_t>(__shfl_xor(static_cast<long long>(v.lo), o)));
+    v.hi = max(v.hi, static_cast<int64_t>(__shfl_xor(static_cast<long long>(v.hi), o)));
+    v.bad += static_cast<int64_t>(__shfl_xor(static_cast<long long>(v.bad), o));
+    v.tmax = fmax(v.tmax, __shfl_xor(v.tmax, o));
+  }
+  const int w = threadIdx.x / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) sm[w] = v;
+  __syncthreads();
+  if (threadIdx.x == 0)
+    for (int i = 1; i < kThreads / kWave; ++i) {
+      v.lo = min(v.lo, sm[i].lo);
+      v.hi = max(v.hi, sm[i].hi);
+      v.bad += sm[i].bad;
+      v.tmax = fmax(v.tmax, sm[i].tmax);
+    }
+  return v;
+}
+
+// Event k >= 1 keeps the time order when t[k] - t[k-1] > 0, or == 0 with k the
+// first event of an advance() call (the same float64 difference and
+// comparisons as the check it replaces, so NaN and inf steps break the order).
+__global__ __launch_bounds__(kThreads) void csr_scan_part(const int64_t* __restrict__ src,
+                                                          const int64_t* __restrict__ dst,
+                                                          const double* __restrict__ t, int64_t E,
+                                                          const int64_t* __restrict__ starts, int64_t m,
+                                                          ScanPart* __restrict__ parts) {
+  __shared__ ScanPart sm[kThreads / kWave];
+  ScanPart v{INT64_MAX, INT64_MIN, 0, -__builtin_huge_val()};
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+#pragma unroll 4
+  for (int64_t k = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; k < E; k += stride) {
+    const int64_t s = src[k], d = dst[k];
+    const double x = t[k];
+    v.lo = min(v.lo, min(s, d));
+    v.hi = max(v.hi, max(s, d));
+    if (x == x) v.tmax = fmax(v.tmax, x);
+    if (k > 0) {
+      const double step = x - t[k - 1];
+      if (!(step > 0.0) && !(step == 0.0 && is_call_start(starts, m, k))) ++v.bad;
+    }
+  }
+  v = fold_block(v, sm);
+  if (threadIdx.x == 0) parts[blockIdx.x] = v;
+}
+
+// out = {min node, max node, 1 if time-ordered else 0, bits of the largest non-NaN time}
+__global__ __launch_bounds__(kThreads) void csr_scan_final(const ScanPart* __restrict__ parts, int np,
+                                                           int64_t* __restrict__ out) {
+  __shared__ ScanPart sm[kThreads / kWave];
+  ScanPart v{INT64_MAX, INT64_MIN, 0, -__builtin_huge_val()};
+  for (int i = threadIdx.x; i < np; i += kThreads) {
+    const ScanPart p = parts[i];
+    v.lo = min(v.lo, p.lo);
+    v.hi = max(v.hi, p.hi);
+    v.bad += p.bad;
+    v.tmax = fmax(v.tmax, p.tmax);
+  }
+  v = fold_block(v, sm);
+  if (threadIdx.x == 0) {
+    out[0] = v.lo;
+    out[1] = v.hi;
+    out[2] = v.bad == 0;
+    out[3] = __double_as_longlong(v.tmax);
+  }
+}
+
 struct Layout {
   RadixScratch r;
   size_t tkey = 0, idx = 0, nkey = 0, count = 0, sums = 0, total = 0;
@@ -264,4 +356,30 @@ extern "C" int tgx_csr_build(const tgx_csr_build_args* a, void* stream_) {
   else
     gather(csr_gather<2>);
   return check_launch("csr_gather");
+}
+
+extern "C" size_t tgx_csr_scan_workspace_size(void) { return kScanParts * sizeof(ScanPart); }
+
+extern "C" int tgx_csr_scan(const int64_t* src, const int64_t* dst, const double* time, int64_t num_events,
+                            const int64_t* call_starts, int64_t num_calls, int64_t* out, void* workspace,
+                            size_t workspace_bytes, void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (num_events <= 0) return fail(TGX_ERR_ARG, "tgx_csr_scan: num_events %lld must be positive", (long long)num_events);
+  if (num_calls < 0) return fail(TGX_ERR_ARG, "tgx_csr_scan: negative num_calls");
+  if (src == nullptr || dst == nullptr || time == nullptr || out == nullptr ||
+      (num_calls > 0 && call_starts == nullptr))
+    return fail(TGX_ERR_ARG, "tgx_csr_scan: src/dst/time/out (and call_starts when num_calls > 0) must not be NULL");
+  if (workspace == nullptr || workspace_bytes < tgx_csr_scan_workspace_size())
+    return fail(TGX_ERR_ARG, "tgx_csr_scan: workspace of %zu bytes needed, got %zu", tgx_csr_scan_workspace_size(),
+                workspace_bytes);
+  // about four events per thread before the grid reaches kScanParts workgroups
+  const int np = static_cast<int>(std::min<int64_t>(cdiv(num_events, 4 * kThreads), kScanParts));
+  ScanPart* parts = static_cast<ScanPart*>(workspace);
+  hipLaunchKernelGGL(csr_scan_part, dim3(np), dim3(kThreads), 0, stream, src, dst, time, num_events, call_starts,
+                     num_calls, parts);
+  int rc;
+  if ((rc = check_launch("csr_scan_part"))) return rc;
+  hipLaunchKernelGGL(csr_scan_final, dim3(1), dim3(kThreads), 0, stream, static_cast<const ScanPart*>(parts), np,
+                     out);
+  return check_launch("csr_scan_final");
 }
