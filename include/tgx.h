@@ -319,8 +319,9 @@ int tgx_csr_build(const tgx_csr_build_args* args, void* stream);
  * (temporal_graph.py:133-181) sorts host lists; here freeze_csr learns from it,
  * in one round trip, the node range it checks, which build to run (event pairs
  * or general) and the largest time.  Over the num_events > 0 events src/dst/time of the pre-freeze
- * advance() calls, whose first events are call_starts [num_calls] (sorted,
- * may be NULL when num_calls is 0), writes out int64 [4]:
+ * advance() calls, whose first events are call_starts [num_calls] (ascending,
+ * a repeated value counts once; may be NULL when num_calls is 0), writes out
+ * int64 [4]:
  *   out[0], out[1]  min and max node id over src and dst,
  *   out[2]          1 when the stream is time-ordered in the sense of
  *                   TGX_CSR_EVENT_PAIRS, else 0: for every k >= 1 the float64

@@ -237,6 +237,12 @@ def test_csr_scan_known_cases(E):
     z[1] = -0.0
     assert _scan(src[:2], dst[:2], z, [0, 1])[2] == 1
     assert _scan(src[:2], dst[:2], z, [0])[2] == 0
+    assert _scan(src[:2], dst[:2], z, [0, 1, 1])[2] == 1  # a repeated start counts once
+    # times 0, 0, 1, 1, 2, 2, ...: zero steps at every odd event break the order
+    # unless every odd event starts a call
+    u = np.repeat(np.arange(E // 2 + 1, dtype=np.float64), 2)[:E]
+    assert _scan(src, dst, u, list(range(0, E, 2)))[2] == 0
+    assert _scan(src, dst, u, list(range(1, E, 2)))[2] == 1
     # every time NaN: no largest time
     assert _scan(src[:2], dst[:2], np.full(2, np.nan), [0, 1])[3] == -np.inf
 

@@ -144,19 +144,6 @@ struct ScanPart {
   double tmax;
 };
 
-// is k one of the sorted call starts?
-__device__ __forceinline__ bool is_call_start(const int64_t* __restrict__ starts, int64_t m, int64_t k) {
-  int64_t lo = 0, hi = m;
-  while (lo < hi) {
-    const int64_t mid = (lo + hi) >> 1;
-    if (starts[mid] < k)
-      lo = mid + 1;
-    else
-      hi = mid;
-  }
-  return lo < m && starts[lo] == k;
-}
-
 // block-wide fold of (lo, hi, bad, tmax); the result is valid in thread 0
 __device__ __forceinline__ ScanPart fold_block(ScanPart v, ScanPart* sm) {
   for (int o = kWave / 2; o > 0; o >>= 1) {
@@ -181,6 +168,9 @@ __device__ __forceinline__ ScanPart fold_block(ScanPart v, ScanPart* sm) {
 // Event k >= 1 keeps the time order when t[k] - t[k-1] > 0, or == 0 with k the
 // first event of an advance() call (the same float64 difference and
 // comparisons as the check it replaces, so NaN and inf steps break the order).
+// Every step not > 0 counts against the order, and each call start whose step
+// is exactly 0 takes its count back (a second pass over the few call starts, in
+// place of a search of them at every tie).
 __global__ __launch_bounds__(kThreads) void csr_scan_part(const int64_t* __restrict__ src,
                                                           const int64_t* __restrict__ dst,
                                                           const double* __restrict__ t, int64_t E,
@@ -196,10 +186,11 @@ __global__ __launch_bounds__(kThreads) void csr_scan_part(const int64_t* __restr
     v.lo = min(v.lo, min(s, d));
     v.hi = max(v.hi, max(s, d));
     if (x == x) v.tmax = fmax(v.tmax, x);
-    if (k > 0) {
-      const double step = x - t[k - 1];
-      if (!(step > 0.0) && !(step == 0.0 && is_call_start(starts, m, k))) ++v.bad;
-    }
+    if (k > 0 && !(x - t[k - 1] > 0.0)) ++v.bad;
+  }
+  for (int64_t c = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; c < m; c += stride) {
+    const int64_t k = starts[c];
+    if (k >= 1 && k < E && (c == 0 || starts[c - 1] != k) && t[k] - t[k - 1] == 0.0) --v.bad;
   }
   v = fold_block(v, sm);
   if (threadIdx.x == 0) parts[blockIdx.x] = v;

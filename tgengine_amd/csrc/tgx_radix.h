@@ -9,7 +9,12 @@
 //   scatter : the tile's keys in order, kThreads at a time; each wavefront
 //             ranks equal digits among its lanes with eight ballots, the
 //             workgroup adds the earlier wavefronts' and rounds' counts, and
-//             every key lands at its stable position.
+//             every key lands at its stable position in an LDS copy of the
+//             tile sorted by digit (the tile's digit counts are differences of
+//             the scanned counts); then the copy goes out in order, so the
+//             keys of one digit leave as a run of consecutive positions
+//             instead of one scattered store each (C3's first node pass:
+//             216 -> 132 us for 20M keys).
 // Everything lives in an anonymous namespace: each including file gets its own
 // copy of the kernels.
 #pragma once
@@ -107,14 +112,38 @@ __global__ __launch_bounds__(kThreads) void radix_scatter(const K* __restrict__ 
                                                           uint32_t* __restrict__ vout, int64_t n,
                                                           int shift, int64_t ntiles,
                                                           const uint32_t* __restrict__ count) {
-  __shared__ uint32_t dbase[kBins];          // next output position per digit
+  __shared__ uint32_t gbase[kBins];          // first output position of the tile's digit d
+  __shared__ uint32_t lstart[kBins];         // first local position of digit d
+  __shared__ uint32_t lnext[kBins];          // next local position per digit
   __shared__ uint32_t wcnt[kWaves][kBins];   // this round's count per wave and digit
   __shared__ uint32_t wpos[kWaves][kBins];   // this round's first position per wave and digit
+  __shared__ uint32_t wtot[kWaves];
+  __shared__ K skey[kTile];                  // the tile in digit order
+  __shared__ uint32_t sval[kTile];
   const int lane = threadIdx.x & (kWave - 1);
   const int wv = threadIdx.x / kWave;
   const uint64_t lt = (uint64_t(1) << lane) - 1;
-  dbase[threadIdx.x] = count[static_cast<int64_t>(threadIdx.x) * ntiles + blockIdx.x];
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile;
+  {  // digit threadIdx.x: its output start and, from the next scanned count, its
+     // number of keys in this tile; their exclusive prefix is the local start
+    const int64_t L = static_cast<int64_t>(kBins) * ntiles;
+    const int64_t i = static_cast<int64_t>(threadIdx.x) * ntiles + blockIdx.x;
+    const uint32_t g0 = count[i];
+    const uint32_t c = (i + 1 < L ? count[i + 1] : static_cast<uint32_t>(n)) - g0;
+    uint32_t incl = c;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const uint32_t y = __shfl_up(incl, off, kWave);
+      if (lane >= off) incl += y;
+    }
+    if (lane == kWave - 1) wtot[wv] = incl;
+    __syncthreads();
+    uint32_t before = 0;
+    for (int w = 0; w < wv; ++w) before += wtot[w];
+    gbase[threadIdx.x] = g0;
+    lstart[threadIdx.x] = before + incl - c;
+    lnext[threadIdx.x] = before + incl - c;
+  }
   for (int r = 0; r < kItems; ++r) {
     const int64_t j = base + r * kThreads + threadIdx.x;
     const bool valid = j < n;
@@ -135,22 +164,32 @@ __global__ __launch_bounds__(kThreads) void radix_scatter(const K* __restrict__ 
     const uint32_t rank = static_cast<uint32_t>(__popcll(peers & lt));
     if (valid && rank == 0) wcnt[wv][d] = static_cast<uint32_t>(__popcll(peers));
     __syncthreads();
-    {  // digit threadIdx.x: positions of the waves in order, then advance the base
+    {  // digit threadIdx.x: local positions of the waves in order, then advance
       const int dd = threadIdx.x;
-      uint32_t p = dbase[dd];
+      uint32_t p = lnext[dd];
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) {
         wpos[w][dd] = p;
         p += wcnt[w][dd];
       }
-      dbase[dd] = p;
+      lnext[dd] = p;
     }
     __syncthreads();
     if (valid) {
       const uint32_t at = wpos[wv][d] + rank;
-      kout[at] = k;
-      vout[at] = v;
+      skey[at] = k;
+      sval[at] = v;
     }
+  }
+  __syncthreads();
+  // the tile in digit order: runs of one digit go out to consecutive positions
+  const int tn = static_cast<int>(n - base < kTile ? n - base : kTile);
+  for (int i = threadIdx.x; i < tn; i += kThreads) {
+    const K k = skey[i];
+    const int d = digit_of(k, shift);
+    const uint32_t at = gbase[d] + (static_cast<uint32_t>(i) - lstart[d]);
+    kout[at] = k;
+    vout[at] = sval[i];
   }
 }
 
