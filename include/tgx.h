@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define TGX_ABI_VERSION 16
+#define TGX_ABI_VERSION 17
 
 /* status codes */
 #define TGX_OK 0
@@ -287,7 +287,18 @@ int tgx_ring_discard(const tgx_ring* ring, const int64_t* src, const int64_t* ds
  * (both at time[k]; event index k, or event[k] when event is set): times
  * strictly increasing within every advance() call and non-decreasing across
  * calls, which makes this order the stable time order of the build order.  The
- * time passes are skipped; the caller checks the condition. */
+ * time passes are skipped; the caller checks the condition.
+ *
+ * flags & TGX_CSR_EVENTS_BY_CALL: from/to/time (and event) hold the n/2
+ * events in stream order, and call_starts [num_calls] the first event of each
+ * advance() call (ascending, starting at 0); the build forms the build order
+ * itself (per call: from->to of each event, then to->from of each) and sorts
+ * it by time.  With TGX_CSR_NONDECREASING as well, the caller asserts that
+ * time never decreases along the events (no NaN): the stable time order is
+ * then, run by run of equal times within a call, the run's from->to entries
+ * followed by its to->from entries, and the time passes are skipped.  Call
+ * starts outside [1, n/2) are ignored; a wrong order assertion gives a wrong
+ * order, never an access outside the arrays. */
 typedef struct tgx_csr_build_args {
   int64_t num_nodes;
   int64_t num_entries;
@@ -308,9 +319,13 @@ typedef struct tgx_csr_build_args {
   size_t workspace_bytes;
   int32_t* status;         /* [TGX_STATUS_WORDS] or NULL */
   uint32_t flags;          /* TGX_CSR_* */
+  const int64_t* call_starts;  /* [num_calls], TGX_CSR_EVENTS_BY_CALL only */
+  int64_t num_calls;
 } tgx_csr_build_args;
 
 #define TGX_CSR_EVENT_PAIRS 1u
+#define TGX_CSR_EVENTS_BY_CALL 2u
+#define TGX_CSR_NONDECREASING 4u
 
 size_t tgx_csr_build_workspace_size(int64_t num_entries);
 int tgx_csr_build(const tgx_csr_build_args* args, void* stream);
@@ -323,10 +338,12 @@ int tgx_csr_build(const tgx_csr_build_args* args, void* stream);
  * a repeated value counts once; may be NULL when num_calls is 0), writes out
  * int64 [4]:
  *   out[0], out[1]  min and max node id over src and dst,
- *   out[2]          1 when the stream is time-ordered in the sense of
- *                   TGX_CSR_EVENT_PAIRS, else 0: for every k >= 1 the float64
+ *   out[2]          2 when the stream is time-ordered in the sense of
+ *                   TGX_CSR_EVENT_PAIRS: for every k >= 1 the float64
  *                   difference time[k] - time[k-1] is > 0, or == 0 with k in
- *                   call_starts (NaN and inf - inf differences break it),
+ *                   call_starts (NaN and inf - inf differences break it);
+ *                   else 1 when time[k] >= time[k-1] for every k >= 1 (the
+ *                   TGX_CSR_NONDECREASING condition), else 0,
  *   out[3]          the bits of the largest non-NaN time (-inf when all are NaN).
  * workspace: tgx_csr_scan_workspace_size() bytes, no initialisation needed.
  * Two launches; the caller reads out after the stream. */

@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(L, n), n
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
-    assert L.tgx_abi_version() == _lib.TGX_ABI_VERSION == 16
+    assert L.tgx_abi_version() == _lib.TGX_ABI_VERSION == 17
     nm = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
                         text=True).stdout
     exported = set(re.findall(r"\bT (tgx_\w+)", nm))
@@ -59,7 +59,7 @@ int main(void) {
   S(tgx_csr_build_args) F(tgx_csr_build_args, num_entries) F(tgx_csr_build_args, event)
   F(tgx_csr_build_args, num_events) F(tgx_csr_build_args, feat_dtype) F(tgx_csr_build_args, out_offsets)
   F(tgx_csr_build_args, out_eids) F(tgx_csr_build_args, workspace_bytes) F(tgx_csr_build_args, status)
-  F(tgx_csr_build_args, flags)
+  F(tgx_csr_build_args, flags) F(tgx_csr_build_args, call_starts) F(tgx_csr_build_args, num_calls)
   return 0;
 }
 """
@@ -342,6 +342,22 @@ def test_csr_build_argument_checks():
     a.feat_dtype = 9
     assert L.tgx_csr_build(ctypes.byref(a), None) == 2
     assert L.tgx_csr_build(None, None) == 1
+    # build modes: pairs and by-call exclude each other, runs need by-call, by-call
+    # needs its call starts, and every mode takes events (an even entry count)
+    a = _lib.TgxCsrBuildArgs(num_nodes=10, num_entries=6, out_offsets=8, from_=8, to=8, time=8,
+                             out_ids=8, out_times=8, flags=_lib.TGX_CSR_EVENT_PAIRS | _lib.TGX_CSR_EVENTS_BY_CALL)
+    assert L.tgx_csr_build(ctypes.byref(a), None) == 1 and "exclude" in _err()
+    a.flags = _lib.TGX_CSR_NONDECREASING
+    assert L.tgx_csr_build(ctypes.byref(a), None) == 1 and "needs TGX_CSR_EVENTS_BY_CALL" in _err()
+    a.flags = _lib.TGX_CSR_EVENTS_BY_CALL | _lib.TGX_CSR_NONDECREASING
+    a.num_calls = 2
+    assert L.tgx_csr_build(ctypes.byref(a), None) == 1 and "call_starts" in _err()
+    a.num_calls = -1
+    assert L.tgx_csr_build(ctypes.byref(a), None) == 1 and "call_starts" in _err()
+    a.num_calls, a.num_entries = 0, 5
+    assert L.tgx_csr_build(ctypes.byref(a), None) == 1 and "even" in _err()
+    a.flags = 8
+    assert L.tgx_csr_build(ctypes.byref(a), None) == 1 and "unknown flags" in _err()
     # workspace: keys, values and node keys double-buffered, plus the digit counts
     assert L.tgx_csr_build_workspace_size(1 << 20) >= (1 << 20) * 32 + 256 * 512 * 4
     assert L.tgx_csr_build_workspace_size(0) > 0

@@ -168,7 +168,9 @@ def test_csr_build_time_ordered_stream(d, bf16, eids, N):
 @pytest.mark.parametrize("where", ["tie", "step_back", "nan"])
 def test_csr_build_almost_ordered_stream_sorts_by_time(where):
     """One tie inside a batch, one step back in time, or a NaN: the stream is not
-    time-ordered, so the build sorts the build order by time first."""
+    time-ordered.  With the tie it still never decreases, and the build takes the
+    time order from runs of equal times; otherwise it sorts the build order (formed
+    on the device from the events and the calls' first events) by time first."""
     rng = np.random.default_rng(30)
     batches = _ordered_batches(rng, 40, [300, 300, 300], 4, False)
     t = batches[1][2]
@@ -180,11 +182,64 @@ def test_csr_build_almost_ordered_stream_sorts_by_time(where):
         t[7] = np.nan
     g, ref = _build(40, 4, False, batches, True)
     assert not g._csr_time_sorted
+    assert g._csr_build_mode == ("runs" if where == "tie" else "sort")
+    _compare(g, ref)
+
+
+def _tied_batches(rng, N, sizes, d, bf16, grid, node_hi=None):
+    """A non-decreasing stream with many equal times: a running clock rounded down
+    to multiples of grid, so runs of equal times span events inside a batch and
+    reach across batch boundaries (each batch starts at its predecessor's last
+    time or later)."""
+    out, t = [], 10.0
+    hi = node_hi or N
+    for k, b in enumerate(sizes):
+        tt = np.floor((t + np.cumsum(rng.exponential(grid / 3, b))) / grid) * grid
+        if b > 0:
+            if k % 2 == 1:
+                tt[0] = t  # the previous batch's last time
+            tt = np.maximum.accumulate(np.maximum(tt, t))
+            t = float(tt[-1])
+        src = rng.integers(0, hi, b)
+        src[: b // 5] = 3 % N  # a hot node
+        feat = _feat(rng, b, d, bf16) if k % 2 == 0 else None
+        out.append((src.astype(np.int64), rng.integers(0, hi, b).astype(np.int64), tt.astype(np.float64), feat))
+    return out
+
+
+@pytest.mark.parametrize("d,bf16,eids,N,sizes,grid", [
+    (16, True, True, 5000, [500, 1, 0, 2000, 777, 3, 1, 1], 1.0),
+    (172, False, False, 300, [300, 300, 300], 10.0),
+    (0, False, True, 70_000, [1, 1, 1, 5, 4000], 1e6),
+    (4, True, False, 1_000_000, [2_500_000, 2_500_000], 0.5),
+])
+def test_csr_build_nondecreasing_stream_uses_runs(d, bf16, eids, N, sizes, grid):
+    """Ties everywhere but time never going down: the build order's stable time
+    order comes from runs of equal times within each call (no time passes); the
+    same CSR as the oracle's two stable sorts.  The last case has 5M events, so
+    the scan of the run marks has two levels."""
+    rng = np.random.default_rng(40 + d)
+    batches = _tied_batches(rng, N, sizes, d, bf16, grid, node_hi=N - 50)
+    g, ref = _build(N, d, bf16, batches, eids)
+    assert g._csr_build_mode == "runs"
+    _compare(g, ref)
+
+
+def test_csr_build_runs_with_signed_zero_and_infinity():
+    """-0.0 ties +0.0 and +inf ties +inf in a non-decreasing stream."""
+    rng = np.random.default_rng(44)
+    t1 = np.array([-5.0, -0.0, 0.0, -0.0, 0.0, 1.0, 1.0])
+    t2 = np.array([1.0, 1.0, 2.0, np.inf, np.inf])
+    batches = [(rng.integers(0, 9, len(t)).astype(np.int64), rng.integers(0, 9, len(t)).astype(np.int64), t,
+                _feat(rng, len(t), 4, False)) for t in (t1, t2)]
+    g, ref = _build(9, 4, False, batches, True)
+    assert g._csr_build_mode == "runs"
     _compare(g, ref)
 
 
 def _scan(src, dst, t, starts):
-    """tgx_csr_scan on device copies: (lo, hi, ordered, largest non-NaN time)."""
+    """tgx_csr_scan on device copies: (lo, hi, order level, largest non-NaN time);
+    the level is 2 for a time-ordered stream, 1 for a non-decreasing one, else 0."""
     L = _lib.lib()
     s, d, tt = (torch.from_numpy(np.ascontiguousarray(x)).cuda() for x in (src, dst, t))
     st = torch.tensor(starts, dtype=torch.int64, device="cuda")
@@ -213,7 +268,7 @@ def test_csr_scan_known_cases(E):
     dst = rng.integers(10, 1000, E)
     src[-1], dst[E // 2] = 3, 5000
     lo, hi, ordered, tmax = _scan(src, dst, t, starts)
-    assert (lo, hi, ordered, tmax) == (min(3, int(dst.min())), 5000, 1, float(t.max()))
+    assert (lo, hi, ordered, tmax) == (min(3, int(dst.min())), 5000, 2, float(t.max()))
     if E < 2:
         return
     inner = [k for k in (1, E // 2, 1024, 4 * 256 * 1024, E - 1) if 0 < k < E and k not in starts]
@@ -229,20 +284,23 @@ def test_csr_scan_known_cases(E):
             else:
                 u[k - 1] = u[k] = np.inf
             got = _scan(src, dst, u, starts)
-            assert got[2] == 0, (k, kind)
+            # a tie inside a call, or inf, inf at the very end, still never decreases
+            nondecreasing = kind == "tie" or (kind == "inf" and k == E - 1)
+            assert got[2] == (1 if nondecreasing else 0), (k, kind)
             want = np.inf if kind == "inf" else float(np.nanmax(u))
             assert got[3] == want, (k, kind)
-    # -0.0 after +0.0 is a zero step: ordered only at a call start
+    # -0.0 after +0.0 is a zero step: time-ordered only at a call start, and
+    # non-decreasing either way
     z = np.zeros(2)
     z[1] = -0.0
-    assert _scan(src[:2], dst[:2], z, [0, 1])[2] == 1
-    assert _scan(src[:2], dst[:2], z, [0])[2] == 0
-    assert _scan(src[:2], dst[:2], z, [0, 1, 1])[2] == 1  # a repeated start counts once
-    # times 0, 0, 1, 1, 2, 2, ...: zero steps at every odd event break the order
-    # unless every odd event starts a call
+    assert _scan(src[:2], dst[:2], z, [0, 1])[2] == 2
+    assert _scan(src[:2], dst[:2], z, [0])[2] == 1
+    assert _scan(src[:2], dst[:2], z, [0, 1, 1])[2] == 2  # a repeated start counts once
+    # times 0, 0, 1, 1, 2, 2, ...: zero steps at every odd event break the strict
+    # order unless every odd event starts a call; the stream never decreases
     u = np.repeat(np.arange(E // 2 + 1, dtype=np.float64), 2)[:E]
-    assert _scan(src, dst, u, list(range(0, E, 2)))[2] == 0
-    assert _scan(src, dst, u, list(range(1, E, 2)))[2] == 1
+    assert _scan(src, dst, u, list(range(0, E, 2)))[2] == 1
+    assert _scan(src, dst, u, list(range(1, E, 2)))[2] == 2
     # every time NaN: no largest time
     assert _scan(src[:2], dst[:2], np.full(2, np.nan), [0, 1])[3] == -np.inf
 

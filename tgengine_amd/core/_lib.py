@@ -24,7 +24,7 @@ TGX_CO_DYGFORMER = 2
 TGX_PLAN_TILES = 0
 TGX_PLAN_EVENTS = 1
 TGX_PLAN_LIST = 2
-TGX_ABI_VERSION = 16
+TGX_ABI_VERSION = 17
 TGX_STATUS_WORDS = 8
 TGX_ST_BAD_EVENT_NODE = 0
 TGX_ST_KEY_COLLISION = 1
@@ -80,10 +80,12 @@ class TgxCsrBuildArgs(ctypes.Structure):
                 ("feat_dim", c_i32), ("feat_dtype", c_i32), ("out_offsets", c_vp),
                 ("out_ids", c_vp), ("out_times", c_vp), ("out_feats", c_vp), ("out_eids", c_vp),
                 ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t), ("status", c_vp),
-                ("flags", ctypes.c_uint32)]
+                ("flags", ctypes.c_uint32), ("call_starts", c_vp), ("num_calls", c_i64)]
 
 
 TGX_CSR_EVENT_PAIRS = 1
+TGX_CSR_EVENTS_BY_CALL = 2
+TGX_CSR_NONDECREASING = 4
 
 
 # every symbol include/tgx.h declares, with its ctypes signature

@@ -146,6 +146,8 @@ class TemporalGraph:
         self._nbr_feats: Optional[Tensor] = None
         self._nbr_eids: Optional[Tensor] = None
         self._csr_max_time = float("inf")  # largest non-NaN CSR time (a search hint)
+        self._csr_time_sorted = False  # freeze_csr took the event-pair build
+        self._csr_build_mode = ""  # freeze_csr's build: "pairs", "runs" or "sort"
 
         self._ov_ids: Optional[Tensor] = None
         self._ov_times: Optional[Tensor] = None
@@ -413,8 +415,12 @@ class TemporalGraph:
         strictly within every call and never decrease across calls (a
         time-ordered stream), that time order is already the events' own order
         with each event's two entries side by side, and the build sorts by node
-        only (TGX_CSR_EVENT_PAIRS); otherwise it sorts the build order by time
-        first.
+        only (TGX_CSR_EVENT_PAIRS).  When they only never decrease (ties), the
+        time order is, run by run of equal times within a call, the run's
+        src->dst entries then its dst->src entries, and again only the node
+        passes run (TGX_CSR_EVENTS_BY_CALL | TGX_CSR_NONDECREASING).  Otherwise
+        the device forms the build order from the events and the calls' first
+        events and sorts it by time first (TGX_CSR_EVENTS_BY_CALL).
         """
         N, d, dev = self.num_nodes, self.edge_feat_dim, self.device
         E = self._build_n
@@ -438,31 +444,23 @@ class TemporalGraph:
             _lib.check(L.tgx_csr_scan(src.data_ptr(), dst.data_ptr(), tt.data_ptr(), E, call_starts.data_ptr(),
                                       call_starts.numel(), scan.data_ptr(), ws.data_ptr(), ws.numel(),
                                       _stream_handle(dev)), "tgx_csr_scan")
-            lo, hi, ordered, tbits = scan.cpu().tolist()
+            lo, hi, order, tbits = scan.cpu().tolist()
             self._csr_max_time = struct.unpack("<d", struct.pack("<q", tbits))[0]
             if lo < 0 or hi >= N:
                 raise IndexError("advance() got node ids outside [0, num_nodes)")
-            flags = 0
-            self._csr_time_sorted = bool(ordered)  # which build ran (diagnostics)
-            if ordered:
-                frm, to, tm, ev = src, dst, tt, None
+            # which build runs (diagnostics): the events in pairs (strictly
+            # increasing times within each call), runs of equal times of a
+            # non-decreasing stream, or the build order sorted by time
+            self._csr_time_sorted = order == 2
+            self._csr_build_mode = ("sort", "runs", "pairs")[order]
+            if order == 2:
                 flags = _lib.TGX_CSR_EVENT_PAIRS
             else:
-                # directed entries in build order: per call, the events as
-                # src->dst, then again as dst->src
-                starts = torch.tensor(self._build_starts + [E], dtype=torch.int64)
-                lens = (starts[1:] - starts[:-1]).to(dev)
-                seg = torch.arange(len(self._build_starts), device=dev).repeat_interleave(2 * lens, output_size=n)
-                s0 = starts[:-1].to(dev)
-                pos = torch.arange(n, dtype=torch.int64, device=dev) - 2 * s0[seg]
-                rev = pos >= lens[seg]
-                ev = s0[seg] + torch.where(rev, pos - lens[seg], pos)
-                frm = torch.where(rev, dst[ev], src[ev])
-                to = torch.where(rev, src[ev], dst[ev])
-                tm = tt[ev]
+                flags = _lib.TGX_CSR_EVENTS_BY_CALL | (_lib.TGX_CSR_NONDECREASING if order == 1 else 0)
             a = _lib.TgxCsrBuildArgs(
-                num_nodes=N, num_entries=n, from_=frm.data_ptr(), to=to.data_ptr(),
-                time=tm.data_ptr(), event=_lib.ptr(ev),
+                num_nodes=N, num_entries=n, from_=src.data_ptr(), to=dst.data_ptr(),
+                time=tt.data_ptr(), event=None, call_starts=call_starts.data_ptr(),
+                num_calls=call_starts.numel(),
                 feats=feats.data_ptr() if feats is not None else None,
                 num_events=E if feats is not None else 0,
                 feat_dim=d, feat_dtype=_DTYPES[self.feat_dtype],

@@ -140,7 +140,7 @@ __global__ __launch_bounds__(kThreads) void csr_gather(
 constexpr int kScanParts = 1024;
 
 struct ScanPart {
-  int64_t lo, hi, bad;
+  int64_t lo, hi, bad, nd;
   double tmax;
 };
 
@@ -150,6 +150,7 @@ __device__ __forceinline__ ScanPart fold_block(ScanPart v, ScanPart* sm) {
     v.lo = min(v.lo, static_cast<int64_t>(__shfl_xor(static_cast<long long>(v.lo), o)));
     v.hi = max(v.hi, static_cast<int64_t>(__shfl_xor(static_cast<long long>(v.hi), o)));
     v.bad += static_cast<int64_t>(__shfl_xor(static_cast<long long>(v.bad), o));
+    v.nd += static_cast<int64_t>(__shfl_xor(static_cast<long long>(v.nd), o));
     v.tmax = fmax(v.tmax, __shfl_xor(v.tmax, o));
   }
   const int w = threadIdx.x / kWave;
@@ -160,6 +161,7 @@ __device__ __forceinline__ ScanPart fold_block(ScanPart v, ScanPart* sm) {
       v.lo = min(v.lo, sm[i].lo);
       v.hi = max(v.hi, sm[i].hi);
       v.bad += sm[i].bad;
+      v.nd += sm[i].nd;
       v.tmax = fmax(v.tmax, sm[i].tmax);
     }
   return v;
@@ -170,14 +172,15 @@ __device__ __forceinline__ ScanPart fold_block(ScanPart v, ScanPart* sm) {
 // comparisons as the check it replaces, so NaN and inf steps break the order).
 // Every step not > 0 counts against the order, and each call start whose step
 // is exactly 0 takes its count back (a second pass over the few call starts, in
-// place of a search of them at every tie).
+// place of a search of them at every tie).  Apart, every step whose time goes
+// down (or is NaN) counts against a non-decreasing stream.
 __global__ __launch_bounds__(kThreads) void csr_scan_part(const int64_t* __restrict__ src,
                                                           const int64_t* __restrict__ dst,
                                                           const double* __restrict__ t, int64_t E,
                                                           const int64_t* __restrict__ starts, int64_t m,
                                                           ScanPart* __restrict__ parts) {
   __shared__ ScanPart sm[kThreads / kWave];
-  ScanPart v{INT64_MAX, INT64_MIN, 0, -__builtin_huge_val()};
+  ScanPart v{INT64_MAX, INT64_MIN, 0, 0, -__builtin_huge_val()};
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
 #pragma unroll 4
   for (int64_t k = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; k < E; k += stride) {
@@ -186,7 +189,11 @@ __global__ __launch_bounds__(kThreads) void csr_scan_part(const int64_t* __restr
     v.lo = min(v.lo, min(s, d));
     v.hi = max(v.hi, max(s, d));
     if (x == x) v.tmax = fmax(v.tmax, x);
-    if (k > 0 && !(x - t[k - 1] > 0.0)) ++v.bad;
+    if (k > 0) {
+      const double p = t[k - 1];
+      if (!(x - p > 0.0)) ++v.bad;
+      if (!(x >= p)) ++v.nd;
+    }
   }
   for (int64_t c = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; c < m; c += stride) {
     const int64_t k = starts[c];
@@ -196,24 +203,82 @@ __global__ __launch_bounds__(kThreads) void csr_scan_part(const int64_t* __restr
   if (threadIdx.x == 0) parts[blockIdx.x] = v;
 }
 
-// out = {min node, max node, 1 if time-ordered else 0, bits of the largest non-NaN time}
+// out = {min node, max node, 2 time-ordered / 1 non-decreasing / 0, bits of the largest non-NaN time}
 __global__ __launch_bounds__(kThreads) void csr_scan_final(const ScanPart* __restrict__ parts, int np,
                                                            int64_t* __restrict__ out) {
   __shared__ ScanPart sm[kThreads / kWave];
-  ScanPart v{INT64_MAX, INT64_MIN, 0, -__builtin_huge_val()};
+  ScanPart v{INT64_MAX, INT64_MIN, 0, 0, -__builtin_huge_val()};
   for (int i = threadIdx.x; i < np; i += kThreads) {
     const ScanPart p = parts[i];
     v.lo = min(v.lo, p.lo);
     v.hi = max(v.hi, p.hi);
     v.bad += p.bad;
+    v.nd += p.nd;
     v.tmax = fmax(v.tmax, p.tmax);
   }
   v = fold_block(v, sm);
   if (threadIdx.x == 0) {
     out[0] = v.lo;
     out[1] = v.hi;
-    out[2] = v.bad == 0;
+    out[2] = v.bad == 0 ? 2 : (v.nd == 0 ? 1 : 0);
     out[3] = __double_as_longlong(v.tmax);
+  }
+}
+
+// Build order from the events (TGX_CSR_EVENTS_BY_CALL).  The events fall into
+// segments: the advance() calls, or with TGX_CSR_NONDECREASING the runs of equal
+// times within a call.  The entries of segment [s, e) take build-order positions
+// [2s, 2e) -- from->to of event k at s + k, then to->from at e + k -- which for
+// runs of a non-decreasing stream is already its stable time order.  The
+// segment of event k comes from an exclusive scan of the segment-start marks,
+// so any call starts give a permutation of [0, 2E).
+__global__ __launch_bounds__(kThreads) void csr_seg_marks(const double* __restrict__ time, int64_t E, int runs,
+                                                          uint32_t* __restrict__ mark, uint32_t* __restrict__ ex) {
+  const int64_t k = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (k >= E) return;
+  const uint32_t f = k == 0 || (runs && !(time[k] == time[k - 1]));
+  mark[k] = f;
+  ex[k] = f;
+}
+
+__global__ __launch_bounds__(kThreads) void csr_seg_calls(const int64_t* __restrict__ starts, int64_t m, int64_t E,
+                                                          uint32_t* __restrict__ mark, uint32_t* __restrict__ ex) {
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (c >= m) return;
+  const int64_t k = starts[c];
+  if (k >= 1 && k < E) {
+    mark[k] = 1;
+    ex[k] = 1;
+  }
+}
+
+// gs[segment] = its first event, gs[number of segments] = E
+__global__ __launch_bounds__(kThreads) void csr_seg_starts(const uint32_t* __restrict__ mark,
+                                                           const uint32_t* __restrict__ ex, int64_t E,
+                                                           uint32_t* __restrict__ gs) {
+  const int64_t k = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (k >= E) return;
+  if (mark[k]) gs[ex[k]] = static_cast<uint32_t>(k);
+  if (k == E - 1) gs[ex[k] + mark[k]] = static_cast<uint32_t>(E);
+}
+
+// idx[position] = entry (2k + direction); tkey (when the time passes follow) its time key
+__global__ __launch_bounds__(kThreads) void csr_seg_order(const uint32_t* __restrict__ mark,
+                                                          const uint32_t* __restrict__ ex,
+                                                          const uint32_t* __restrict__ gs,
+                                                          const double* __restrict__ time, int64_t E,
+                                                          uint32_t* __restrict__ idx, uint64_t* __restrict__ tkey) {
+  const int64_t k = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (k >= E) return;
+  const uint32_t g = ex[k] + mark[k] - 1;
+  const int64_t pf = static_cast<int64_t>(gs[g]) + k;
+  const int64_t pr = static_cast<int64_t>(gs[g + 1]) + k;
+  idx[pf] = static_cast<uint32_t>(2 * k);
+  idx[pr] = static_cast<uint32_t>(2 * k + 1);
+  if (tkey != nullptr) {
+    const uint64_t key = time_key(time[k]);
+    tkey[pf] = key;
+    tkey[pr] = key;
   }
 }
 
@@ -258,11 +323,20 @@ extern "C" int tgx_csr_build(const tgx_csr_build_args* a, void* stream_) {
   if (esz == 0) return fail(TGX_ERR_DTYPE, "tgx_csr_build: unsupported feat dtype %d", a->feat_dtype);
   if (a->out_offsets == nullptr) return fail(TGX_ERR_ARG, "tgx_csr_build: out_offsets is NULL");
   const int64_t row_bytes = static_cast<int64_t>(a->feat_dim) * esz;
-  if ((a->flags & ~TGX_CSR_EVENT_PAIRS) != 0)
+  if ((a->flags & ~(TGX_CSR_EVENT_PAIRS | TGX_CSR_EVENTS_BY_CALL | TGX_CSR_NONDECREASING)) != 0)
     return fail(TGX_ERR_ARG, "tgx_csr_build: unknown flags 0x%x", a->flags);
-  const int pairs = (a->flags & TGX_CSR_EVENT_PAIRS) != 0;
+  const int by_call = (a->flags & TGX_CSR_EVENTS_BY_CALL) != 0;
+  const int runs = (a->flags & TGX_CSR_NONDECREASING) != 0;
+  if ((a->flags & TGX_CSR_EVENT_PAIRS) && by_call)
+    return fail(TGX_ERR_ARG, "tgx_csr_build: TGX_CSR_EVENT_PAIRS and TGX_CSR_EVENTS_BY_CALL exclude each other");
+  if (runs && !by_call)
+    return fail(TGX_ERR_ARG, "tgx_csr_build: TGX_CSR_NONDECREASING needs TGX_CSR_EVENTS_BY_CALL");
+  if (by_call && (a->num_calls < 0 || (a->num_calls > 0 && a->call_starts == nullptr)))
+    return fail(TGX_ERR_ARG, "tgx_csr_build: events by call need call_starts [num_calls >= 0]");
+  // entries addressed through their events: 2k = from->to, 2k + 1 = to->from of event k
+  const int pairs = (a->flags & TGX_CSR_EVENT_PAIRS) != 0 || by_call;
   if (pairs && n % 2 != 0)
-    return fail(TGX_ERR_ARG, "tgx_csr_build: event pairs need an even entry count, got %lld", (long long)n);
+    return fail(TGX_ERR_ARG, "tgx_csr_build: events need an even entry count, got %lld", (long long)n);
   if (n > 0) {
     if (a->from == nullptr || a->to == nullptr || a->time == nullptr || a->out_ids == nullptr ||
         a->out_times == nullptr)
@@ -297,7 +371,32 @@ extern "C" int tgx_csr_build(const tgx_csr_build_args* a, void* stream_) {
   uint32_t* sums = reinterpret_cast<uint32_t*>(ws + w.sums);
   const Entries E{a->from, a->to, a->event, pairs};
   int cur = 0;
-  if (pairs) {
+  if (by_call) {
+    // the build order from the segments; marks and their scan in nk[0], the
+    // segment starts in nk[1], the scan's tile sums in the digit counts (free
+    // until the first pass)
+    const int64_t ne = n / 2;
+    const unsigned ge = static_cast<unsigned>(cdiv(ne, kThreads));
+    uint32_t* mark = nk[0];
+    uint32_t* ex = nk[0] + ne;
+    hipLaunchKernelGGL(csr_seg_marks, dim3(ge), dim3(kThreads), 0, stream, a->time, ne, runs, mark, ex);
+    if ((rc = check_launch("csr_seg_marks"))) return rc;
+    if (a->num_calls > 0) {
+      hipLaunchKernelGGL(csr_seg_calls, dim3(static_cast<unsigned>(cdiv(a->num_calls, kThreads))), dim3(kThreads), 0,
+                         stream, a->call_starts, a->num_calls, ne, mark, ex);
+      if ((rc = check_launch("csr_seg_calls"))) return rc;
+    }
+    if ((rc = scan_exclusive(ex, ne, count, scan_levels(ne), 0, stream))) return rc;
+    hipLaunchKernelGGL(csr_seg_starts, dim3(ge), dim3(kThreads), 0, stream, static_cast<const uint32_t*>(mark),
+                       static_cast<const uint32_t*>(ex), ne, nk[1]);
+    if ((rc = check_launch("csr_seg_starts"))) return rc;
+    hipLaunchKernelGGL(csr_seg_order, dim3(ge), dim3(kThreads), 0, stream, static_cast<const uint32_t*>(mark),
+                       static_cast<const uint32_t*>(ex), static_cast<const uint32_t*>(nk[1]), a->time, ne, ix[0],
+                       runs ? static_cast<uint64_t*>(nullptr) : tk[0]);
+    if ((rc = check_launch("csr_seg_order"))) return rc;
+    // stable by time unless the runs already are
+    if (!runs && (rc = radix_sort<uint64_t>(tk, ix, cur, n, 64, w.r, count, sums, stream))) return rc;
+  } else if (pairs) {
     // already in stable time order
     hipLaunchKernelGGL(csr_identity, dim3(g1), dim3(kThreads), 0, stream, n, ix[0]);
     if ((rc = check_launch("csr_identity"))) return rc;
