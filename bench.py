@@ -245,7 +245,8 @@ def cpu_baseline(cfg, g, pipe, first, seconds, torch, log, last):
 def run_rows(a, log) -> None:
     """--rows: the functions beside the streaming path, on the C3 graph (1M nodes,
     16-d bf16 rows): freeze_csr (tgx_csr_build) of a pre-freeze prefix of the
-    stream, recent() on the frozen CSR, recent_2hop() and HistoricalNegPool
+    stream (as generated, with its times floored, and with its times permuted
+    within each batch: the three builds), recent() on the frozen CSR, recent_2hop() and HistoricalNegPool
     update + sample.  Each is timed on the device (HIP events; the gathers and the
     pool as graph replays of successive batches) and priced against its
     algorithmic bytes, and the oracle's restatement of the same function is timed
@@ -349,6 +350,52 @@ def run_rows(a, log) -> None:
           "sample": f"oracle.spec.csr_freeze (numpy) of batches 0..{S - 1} ({ES} events)"},
          f"CSR arrays of batches 0..{S - 1} equal to the oracle's", {"reps_ms": fr})
     log(f"rows: csr_build {ms:.2f} ms for {E} events")
+
+    # ---- the same freeze with tied times (floored to whole numbers: runs of equal
+    # times, no time passes) and with times permuted within each batch (the build
+    # order sorted by time first) ----
+    gen = torch.Generator(device=device)
+    gen.manual_seed(7)
+    perm = torch.cat([torch.randperm(int(e_ - s_), device=device, generator=gen) + int(s_)
+                      for s_, e_ in zip(offs[:P], offs[1:P + 1])])
+    for row, how, tv in (("csr_build_tied", "times floored to whole numbers", torch.floor(dev["time"][:E])),
+                         ("csr_build_shuffled", "times permuted within each batch", dev["time"][perm])):
+        def filled_v(n, tv=tv):
+            gv = make_graph(cfg)
+            for i in range(n):
+                s_, e_ = int(offs[i]), int(offs[i + 1])
+                gv.advance(dev["src"][s_:e_], dev["dst"][s_:e_], tv[s_:e_], dev["feat"][s_:e_])
+            torch.cuda.synchronize()
+            return gv
+        frv = []
+        for rep in range(3):
+            gv = filled_v(P)
+            frv.append(timed_ms(gv.freeze_csr))
+            mode = gv._csr_build_mode
+            del gv
+            torch.cuda.synchronize()
+        msv = min(frv)
+        tv_host = tv[:ES].cpu().numpy()
+        evs = [(bt["src"], bt["dst"], tv_host[int(offs[i]):int(offs[i + 1])], bt["feat"], int(offs[i]))
+               for i, bt in enumerate(bts[:S])]
+        c0 = time.perf_counter()
+        csr_v = spec.csr_freeze(N, d, evs, feat_dtype=np.uint16)
+        cv = time.perf_counter() - c0
+        gs = filled_v(S)
+        gs.freeze_csr()
+        same = (np.array_equal(gs._offsets.cpu().numpy(), csr_v.offsets)
+                and np.array_equal(gs._nbr_ids.cpu().numpy(), csr_v.ids)
+                and np.array_equal(gs._nbr_times.cpu().numpy().view(np.int64), csr_v.times.view(np.int64))
+                and np.array_equal(gs._nbr_feats.view(torch.int16).cpu().numpy().view(np.uint16), csr_v.feats))
+        del gs
+        if not same:
+            raise RuntimeError(f"rows: the device CSR of the {row} sample differs from the oracle's")
+        line(row, f"freeze_csr of C3 batches 0..{P - 1} with {how} ({mode} build): {E} events, "
+             f"{2 * E} directed entries, {N} nodes, {d}-d bf16 rows", "events/s", E / (msv * 1e-3), msv, fbytes,
+             {"value": ES / cv, "unit": "events/s", "cores": 1, "kind": "port",
+              "sample": f"oracle.spec.csr_freeze (numpy) of batches 0..{S - 1} ({ES} events)"},
+             f"CSR arrays of batches 0..{S - 1} equal to the oracle's", {"reps_ms": frv, "build": mode})
+        log(f"rows: {row} {msv:.2f} ms ({mode} build)")
 
     # ---- recent() on the frozen CSR: the next R batches' src/dst/neg queries ----
     qs = []
