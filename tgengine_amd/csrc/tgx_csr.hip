@@ -61,11 +61,6 @@ struct Entries {
   }
 };
 
-__global__ __launch_bounds__(kThreads) void csr_identity(int64_t n, uint32_t* __restrict__ idx) {
-  const int64_t j = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  if (j < n) idx[j] = static_cast<uint32_t>(j);
-}
-
 __global__ __launch_bounds__(kThreads) void csr_node_keys(Entries E,
                                                           const uint32_t* __restrict__ idx,
                                                           int64_t n, int64_t N,
@@ -74,7 +69,7 @@ __global__ __launch_bounds__(kThreads) void csr_node_keys(Entries E,
   const int64_t p = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   bool bad = false;
   if (p < n) {
-    const int64_t u = E.node(idx[p]);
+    const int64_t u = E.node(idx != nullptr ? idx[p] : p);  // NULL: the identity
     bad = u < 0 || u >= N;
     nkey[p] = bad ? 0xffffffffu : static_cast<uint32_t>(u);
   }
@@ -397,9 +392,8 @@ extern "C" int tgx_csr_build(const tgx_csr_build_args* a, void* stream_) {
     // stable by time unless the runs already are
     if (!runs && (rc = radix_sort<uint64_t>(tk, ix, cur, n, 64, w.r, count, sums, stream))) return rc;
   } else if (pairs) {
-    // already in stable time order
-    hipLaunchKernelGGL(csr_identity, dim3(g1), dim3(kThreads), 0, stream, n, ix[0]);
-    if ((rc = check_launch("csr_identity"))) return rc;
+    // already in stable time order: the identity, which the node keys and the
+    // first node pass take without reading it
   } else {
     hipLaunchKernelGGL(csr_init, dim3(g1), dim3(kThreads), 0, stream, a->time, n, tk[0], ix[0]);
     if ((rc = check_launch("csr_init"))) return rc;
@@ -407,8 +401,10 @@ extern "C" int tgx_csr_build(const tgx_csr_build_args* a, void* stream_) {
     if ((rc = radix_sort<uint64_t>(tk, ix, cur, n, 64, w.r, count, sums, stream))) return rc;
   }
   // then stable by node over ceil(log2 N) bits (out-of-range ids sort last)
+  const bool ident = pairs && !by_call;
   hipLaunchKernelGGL(csr_node_keys, dim3(g1), dim3(kThreads), 0, stream, E,
-                     static_cast<const uint32_t*>(ix[cur]), n, N, nk[0], a->status);
+                     ident ? static_cast<const uint32_t*>(nullptr) : static_cast<const uint32_t*>(ix[cur]), n, N,
+                     nk[0], a->status);
   if ((rc = check_launch("csr_node_keys"))) return rc;
   int bits = 1;
   while ((int64_t(1) << bits) < N + 1) ++bits;  // + 1: the out-of-range key 0xffffffff
@@ -416,7 +412,7 @@ extern "C" int tgx_csr_build(const tgx_csr_build_args* a, void* stream_) {
   // passes left it)
   uint32_t* pv[2] = {ix[cur], ix[1 - cur]};
   int ncur = 0;
-  if ((rc = radix_sort<uint32_t>(nk, pv, ncur, n, bits, w.r, count, sums, stream))) return rc;
+  if ((rc = radix_sort<uint32_t>(nk, pv, ncur, n, bits, w.r, count, sums, stream, ident))) return rc;
   uint32_t* perm_in = pv[ncur];
   hipLaunchKernelGGL(csr_offsets, dim3(static_cast<unsigned>(cdiv(N + 1, kThreads))), dim3(kThreads), 0,
                      stream, static_cast<const uint32_t*>(nk[ncur]), n, N, a->out_offsets);

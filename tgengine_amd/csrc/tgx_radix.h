@@ -148,7 +148,7 @@ __global__ __launch_bounds__(kThreads) void radix_scatter(const K* __restrict__ 
     const int64_t j = base + r * kThreads + threadIdx.x;
     const bool valid = j < n;
     const K k = valid ? kin[j] : K(0);
-    const uint32_t v = valid ? vin[j] : 0u;
+    const uint32_t v = valid ? (vin != nullptr ? vin[j] : static_cast<uint32_t>(j)) : 0u;  // NULL: the identity
     const int d = digit_of(k, shift);
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) wcnt[w][threadIdx.x] = 0;
@@ -270,12 +270,14 @@ int radix_pass(const K* kin, const uint32_t* vin, K* kout, uint32_t* vout, int64
 }
 
 // passes over bits [0, bits) of the keys, ping-ponging between k[0]/v[0] and
-// k[1]/v[1]; `cur` is the buffer holding the input, and then the output
+// k[1]/v[1]; `cur` is the buffer holding the input, and then the output.  With
+// ident_values the first pass takes the values 0, 1, ..., n-1 without reading them
 template <typename K>
 int radix_sort(K* k[2], uint32_t* v[2], int& cur, int64_t n, int bits, const RadixScratch& r,
-               uint32_t* count, uint32_t* sums, hipStream_t stream) {
+               uint32_t* count, uint32_t* sums, hipStream_t stream, bool ident_values = false) {
   for (int shift = 0; shift < bits; shift += 8) {
-    const int rc = radix_pass<K>(k[cur], v[cur], k[1 - cur], v[1 - cur], n, shift, r, count, sums, stream);
+    const uint32_t* vin = shift == 0 && ident_values ? nullptr : v[cur];
+    const int rc = radix_pass<K>(k[cur], vin, k[1 - cur], v[1 - cur], n, shift, r, count, sums, stream);
     if (rc) return rc;
     cur = 1 - cur;
   }
